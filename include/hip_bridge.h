@@ -1,0 +1,267 @@
+/*
+ * hip_bridge.h — C ABI of libhip_bridge.so, the MI355X (gfx950) replacement for
+ * rustane's `ane-bridge` on the transformer forward path and the single-token
+ * decode loop.
+ *
+ * Reference boundary being replaced (paths relative to the rustane tree):
+ *   crates/ane-bridge/src/lib.rs:8-9          re-export of the `ane` crate (Graph,
+ *                                             Executable, TensorData) that every
+ *                                             forward kernel is built and run through
+ *   crates/engine/src/layer.rs:239-274        CompiledKernels::compile (graph build)
+ *   crates/engine/src/layer.rs:684-806        per-layer dispatch (run_cached_direct)
+ *   crates/engine/src/full_model.rs:187-247   forward_ws (model forward + mean loss)
+ *   crates/engine/src/full_model.rs:717-767   forward_losses (per-position losses)
+ *   crates/metal-decode/src/lib.rs:1-8        planned single-token decode (placeholder)
+ *
+ * Conventions
+ *   - Every entry point returns int: 0 (HB_OK) on success, a negative HB_E_* code
+ *     on failure. hb_last_error() returns a thread-local message for the last
+ *     failure on the calling thread. Nothing throws across the ABI.
+ *   - Host pointers ("h_" in the docs) are borrowed for the duration of the call.
+ *     Device pointers ("d_") must point to memory on the context's device.
+ *   - Entry points taking host buffers are synchronous. Entry points documented
+ *     as "async" enqueue on the context stream and return immediately.
+ *   - A context is single-owner, as the reference's CompiledKernels/IOSurfaces
+ *     are: use one context per host thread.
+ *   - Weights are passed in the reference's fp32 layouts (layer.rs:16-26,
+ *     full_model.rs:13-17) and are converted to fp16 and repacked on the device.
+ *   - Token ids are uint32 as in the reference (full_model.rs:191-192).
+ */
+#ifndef HIP_BRIDGE_H
+#define HIP_BRIDGE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------- */
+enum {
+  HB_OK = 0,
+  HB_E_INVALID = -1, /* bad argument: null pointer, out-of-range size or token */
+  HB_E_CONFIG = -2,  /* model config rejected (see hb_model_create)            */
+  HB_E_DEVICE = -3,  /* HIP runtime error (launch, copy, sync)                 */
+  HB_E_OOM = -4,     /* device allocation failed                               */
+  HB_E_STATE = -5,   /* call out of order (e.g. weights not uploaded, KV full) */
+  HB_E_INJECTED = -6 /* error injected by hb_debug_inject_error                */
+};
+
+/* ---- dtypes --------------------------------------------------------------- */
+enum { HB_DTYPE_F16 = 1 };
+
+typedef struct hb_ctx hb_ctx;
+typedef struct hb_model hb_model;
+typedef struct hb_kv hb_kv;
+
+/*
+ * Model shape. Field names and meaning follow rustane's ModelConfig
+ * (crates/engine/src/model.rs:5-17); the last four fields are the constants the
+ * reference hard-codes: RoPE base 10000 (kernels/sdpa_fwd.rs:22), RMSNorm eps
+ * 1e-5 (cpu/rmsnorm.rs:10), residual scale 1/sqrt(2*nlayers) (layer.rs:698,
+ * kernels/ffn_fused.rs:29) and logit softcap (full_model.rs:234-239, default 0).
+ * `seq` is the longest sequence hb_forward accepts. q_dim must equal heads*hd and
+ * kv_dim kv_heads*hd; gqa_ratio = heads/kv_heads.
+ */
+typedef struct hb_model_config {
+  int32_t dim;
+  int32_t hidden;
+  int32_t heads;
+  int32_t kv_heads;
+  int32_t hd;
+  int32_t seq;
+  int32_t nlayers;
+  int32_t vocab;
+  int32_t q_dim;
+  int32_t kv_dim;
+  int32_t gqa_ratio;
+  float rope_theta;     /* 0 -> 10000                 */
+  float norm_eps;       /* 0 -> 1e-5                  */
+  float residual_alpha; /* 0 -> 1/sqrt(2*nlayers)     */
+  float softcap;        /* 0 -> no softcap            */
+} hb_model_config;
+
+/* ---- library / context ---------------------------------------------------- */
+
+/* "hip-gfx950". Replaces nothing in the reference (the ANE backend is implicit). */
+const char* hb_backend_name(void);
+/* Message for the last failing call on this thread ("" if none). */
+const char* hb_last_error(void);
+/* Number of visible HIP devices (0 on a host without a GPU). */
+int hb_device_count(int* out_count);
+
+/* Create a context on `device`: owns a HIP stream (default priority). */
+int hb_ctx_create(int device, hb_ctx** out);
+int hb_ctx_destroy(hb_ctx* ctx);
+/* Use a caller-owned hipStream_t for all work of this context (NULL restores
+ * the context's own stream). The stream must belong to the context's device. */
+int hb_ctx_set_stream(hb_ctx* ctx, void* hip_stream);
+int hb_ctx_get_stream(hb_ctx* ctx, void** hip_stream);
+/* Wait for all work on the context stream; reports device-side input errors
+ * (an out-of-range token seen by an async entry point) as HB_E_INVALID. */
+int hb_ctx_synchronize(hb_ctx* ctx);
+
+/* ---- model ---------------------------------------------------------------- */
+
+/*
+ * Validate `cfg` and allocate the device model (weights only; activations are
+ * sized on first use). Replaces CompiledKernels::compile (layer.rs:239-274).
+ * Requirements (HB_E_CONFIG otherwise): all dims > 0; dim, hidden, q_dim,
+ * kv_dim and vocab multiples of 64; hd in {64, 128}; q_dim == heads*hd;
+ * kv_dim == kv_heads*hd; heads % kv_heads == 0; dtype == HB_DTYPE_F16.
+ */
+int hb_model_create(hb_ctx* ctx, const hb_model_config* cfg, int dtype, hb_model** out);
+int hb_model_destroy(hb_model* model);
+/* The effective config (defaults filled in). */
+int hb_model_get_config(const hb_model* model, hb_model_config* out);
+/* Bytes of device memory held by weights. */
+int hb_model_weight_bytes(const hb_model* model, uint64_t* out);
+/* Logit softcap for later forwards (0 = off). The reference passes it per call
+ * (forward_ws(..., softcap, ..), full_model.rs:187-195). */
+int hb_model_set_softcap(hb_model* model, float softcap);
+
+/*
+ * Upload one layer's weights from host fp32 arrays in the reference layouts
+ * (LayerWeights, layer.rs:16-26):
+ *   wq [dim*q_dim], wk [dim*kv_dim], wv [dim*kv_dim]   element [c*out + j]
+ *   wo [q_dim*dim]                                      element [j*dim + c]
+ *   w1, w3 [dim*hidden]                                 element [c*hidden + k]
+ *   w2 [dim*hidden] (used transposed, ffn_fused.rs:65-72) element [c*hidden + k]
+ *   gamma1, gamma2 [dim]
+ */
+int hb_model_upload_layer(hb_model* model, int layer, const float* wq, const float* wk,
+                          const float* wv, const float* wo, const float* w1, const float* w3,
+                          const float* w2, const float* gamma1, const float* gamma2);
+/* Tied embedding E [vocab*dim] (element [v*dim + c]) and final gamma [dim]
+ * (ModelWeights, full_model.rs:13-17). */
+int hb_model_upload_embed(hb_model* model, const float* embed, const float* gamma_final);
+/*
+ * Fill every weight on the device with the seeded synthetic values that
+ * hb_synth_normal produces on the host for the same (seed, tensor id), with
+ * gammas = 1 — bit-identical to uploading those host arrays. Tensor ids:
+ * layer l: wq 16l+0, wk 16l+1, wv 16l+2, wo 16l+3, w1 16l+4, w3 16l+5,
+ * w2 16l+6; embedding: HB_SYNTH_EMBED_ID.
+ */
+int hb_model_init_synthetic(hb_model* model, uint64_t seed, float std);
+
+/* ---- seeded synthetic inputs (host, deterministic) ------------------------- */
+#define HB_SYNTH_EMBED_ID 0xFFFFu
+/* out[i], i < n: approximately N(0, std^2) (standardised sum of eight uniform
+ * 16-bit draws of a counter-based hash of (seed, tensor_id, i)). */
+int hb_synth_normal(uint64_t seed, uint64_t tensor_id, float std, uint64_t n, float* out);
+/* out[i], i < n: uniform over [0, vocab) from the same hash. */
+int hb_synth_tokens(uint64_t seed, uint64_t stream, uint32_t vocab, uint64_t n, uint32_t* out);
+
+/* ---- forward (prefill) ----------------------------------------------------- */
+
+/*
+ * Full forward over B independent sequences of S tokens (token-major
+ * [B*S]): embedding -> nlayers x layer -> final RMSNorm -> tied logits ->
+ * optional softcap -> cross-entropy. Mirrors forward_ws / forward_losses
+ * (full_model.rs:187-247, 717-767); B > 1 is B independent B=1 calls.
+ * Synchronous. targets may be NULL (no loss); per_pos_loss [B*S], logits
+ * [B*S*vocab] and mean_loss (mean over all B*S positions) may each be NULL.
+ * Requires 1 <= S <= cfg.seq.
+ */
+int hb_forward(hb_model* model, const uint32_t* h_tokens, const uint32_t* h_targets, int B,
+               int S, float* h_per_pos_loss, float* h_logits, float* h_mean_loss);
+/* Same on device buffers; async on the context stream. Out-of-range tokens
+ * are not read (the row is zeroed) and make the next hb_ctx_synchronize fail. */
+int hb_forward_device(hb_model* model, const uint32_t* d_tokens, const uint32_t* d_targets,
+                      int B, int S, float* d_per_pos_loss, float* d_logits, float* d_mean_loss);
+/* Pre-size activation buffers for forwards of up to B sequences of S tokens
+ * so that later calls of that size allocate nothing. */
+int hb_model_reserve(hb_model* model, int B, int S);
+
+/* ---- per-kernel entry points (device buffers, async) -----------------------
+ * The reference runs each layer as CPU RMSNorm -> sdpaFwd -> woFwd -> CPU
+ * residual + RMSNorm -> ffnFused (layer.rs:684-806). These expose the same
+ * split so each stage can be checked on its own. T = B*S token rows. */
+
+/* RMSNorm over rows of x [T, dim] fp32 -> out fp16 [T, dim]; rms_inv [T] fp32
+ * (nullable). cpu/rmsnorm.rs:149-183. */
+int hb_op_rmsnorm(hb_ctx* ctx, const float* d_x, const float* d_gamma, int T, int dim, float eps,
+                  void* d_out_f16, float* d_rms_inv);
+/* x[t, :] = E[tokens[t], :] as fp32 (cpu/embedding.rs:8-16). */
+int hb_op_embedding(hb_model* model, const uint32_t* d_tokens, int T, float* d_x);
+/*
+ * sdpaFwd (kernels/sdpa_fwd.rs:49-161): Q/K/V projections of xnorm (fp16
+ * [B*S, dim]), interleaved RoPE on Q and K, causal softmax attention. Writes
+ * attn_out fp16 [B*S, q_dim] (channel h*hd+e). If d_qkv_tap is non-NULL it also
+ * receives fp32 [B*S, q_dim + 2*kv_dim] = Q_rope | K_rope | V.
+ */
+int hb_op_sdpa_fwd(hb_model* model, int layer, const void* d_xnorm_f16, int B, int S,
+                   void* d_attn_f16, float* d_qkv_tap);
+/* woFwd + residual (dyn_matmul.rs:15-46, layer.rs:784):
+ * x2 = x + alpha * attn @ Wo, x and x2 fp32 [T, dim]. */
+int hb_op_wo_fwd(hb_model* model, int layer, const void* d_attn_f16, const float* d_x, int T,
+                 float* d_x2);
+/*
+ * ffnFused (kernels/ffn_fused.rs:22-83): h1 = xn@W1, h3 = xn@W3,
+ * gate = silu(h1)*h3, x_next = x2 + alpha * gate @ W2^T. xn fp16 [T, dim], x2
+ * and x_next fp32 [T, dim]. Taps (nullable): h13 fp32 [T, 2*hidden] = h1 | h3,
+ * gate fp16 [T, hidden].
+ */
+int hb_op_ffn_fused(hb_model* model, int layer, const void* d_x2norm_f16, const float* d_x2,
+                    int T, float* d_x_next, float* d_h13_tap, void* d_gate_f16);
+/* The up half of ffnFused alone (one kernel: W1|W3 GEMM with the SwiGLU gate
+ * formed in its epilogue): gate fp16 [T, hidden] = silu(xn@W1) * (xn@W3). */
+int hb_op_ffn_up(hb_model* model, int layer, const void* d_x2norm_f16, int T, void* d_gate_f16,
+                 float* d_h13_tap);
+/* Final stage (full_model.rs:228-246): logits = xf @ E^T (+softcap), then
+ * per-row cross-entropy (cpu/cross_entropy.rs:58-96) when targets != NULL.
+ * xf fp16 [T, dim]; logits fp32 [T, vocab] (nullable only if losses wanted);
+ * losses fp32 [T] (nullable). */
+int hb_op_logits_ce(hb_model* model, const void* d_xf_f16, const uint32_t* d_targets, int T,
+                    float* d_logits, float* d_losses);
+/* Plain C[M,N] = A[M,K] @ B[N,K]^T, fp16 inputs, fp32 output, on the same
+ * MFMA kernel the model GEMMs use. K % 64 == 0, N % 4 == 0. */
+int hb_op_gemm_nt(hb_ctx* ctx, const void* d_a_f16, const void* d_b_f16, float* d_c, int M,
+                  int N, int K);
+
+/* ---- single-token decode (the loop metal-decode/src/lib.rs:1-8 plans) ----- */
+
+/* Preallocate a contiguous fp16 KV cache for `batch` sequences of up to
+ * ctx_max positions: [nlayers][batch][K,V][kv_heads][ctx_max][hd]. */
+int hb_kv_create(hb_model* model, int batch, int ctx_max, hb_kv** out);
+int hb_kv_destroy(hb_kv* kv);
+/* Forget all positions (length -> 0). */
+int hb_kv_reset(hb_kv* kv);
+int hb_kv_length(hb_kv* kv, int* out_len);
+/* Bytes of device memory held by the cache. */
+int hb_kv_bytes(hb_kv* kv, uint64_t* out);
+/*
+ * Run the prompt tokens [batch*S] (token-major per sequence) through the
+ * forward path, writing K/V for positions [0, S) into the cache. Returns the
+ * last position's logits [batch*vocab] and greedy next token [batch]
+ * (nullable). Requires an empty cache and S <= ctx_max.
+ */
+int hb_prefill(hb_model* model, hb_kv* kv, const uint32_t* h_tokens, int S, float* h_logits,
+               uint32_t* h_next);
+/*
+ * One decode step: tokens [batch] at position p = current length; appends
+ * K/V at p, returns logits [batch*vocab] and argmax [batch] (nullable), and
+ * advances the length. Logits at p equal row p of a full forward over the
+ * same token history.
+ */
+int hb_decode_step(hb_model* model, hb_kv* kv, const uint32_t* h_tokens, float* h_logits,
+                   uint32_t* h_next);
+/*
+ * nsteps greedy steps entirely on the device: each step consumes the previous
+ * step's argmax (the first consumes h_first [batch]); writes the generated
+ * tokens [nsteps*batch] to h_out (nullable). The step is replayed from one
+ * captured HIP graph.
+ */
+int hb_decode_greedy(hb_model* model, hb_kv* kv, const uint32_t* h_first, int nsteps,
+                     uint32_t* h_out);
+
+/* ---- failure injection (host-side test hook) ------------------------------ */
+/* While `code` != 0, every entry point above except hb_last_error,
+ * hb_backend_name and this one returns HB_E_INJECTED without touching the GPU. */
+int hb_debug_inject_error(int code);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HIP_BRIDGE_H */

@@ -1,0 +1,1161 @@
+// C ABI of libhip_bridge.so (declared in include/hip_bridge.h): contexts, the
+// device model, the prefill forward, the per-kernel entry points and the decode
+// loop. Host orchestration only; kernels live in gemm.hip, gemv.hip,
+// attention.hip and elementwise.hip.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/hip_bridge.h"
+#include "internal.hpp"
+#include "synth.hpp"
+
+using namespace hb;
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_err;
+static std::atomic<int> g_inject{0};
+
+static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HB_INJECT_CHECK()                                                  \
+  do {                                                                     \
+    if (int c_ = g_inject.load()) return fail(HB_E_INJECTED, "injected error %d", c_); \
+  } while (0)
+
+#define HIP_TRY(expr)                                                                    \
+  do {                                                                                   \
+    hipError_t e_ = (expr);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      return fail(e_ == hipErrorOutOfMemory ? HB_E_OOM : HB_E_DEVICE, "%s failed: %s (%s:%d)", \
+                  #expr, hipGetErrorString(e_), __FILE__, __LINE__);                     \
+  } while (0)
+
+#define TRY(expr)                \
+  do {                           \
+    int r_ = (expr);             \
+    if (r_ != HB_OK) return r_;  \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// objects
+// ---------------------------------------------------------------------------
+struct hb_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t user = nullptr;
+  hipStream_t capture = nullptr;
+  int* d_err = nullptr;
+  hipStream_t stream() const { return user ? user : own; }
+};
+
+namespace {
+
+struct LayerW {
+  f16* wqkv = nullptr;  // [q+2kv, dim]
+  f16* wo = nullptr;    // [dim, q]
+  f16* w13 = nullptr;   // [2*hidden, dim], row-interleaved (see EpiSwiGLU)
+  f16* w2 = nullptr;    // [dim, hidden]
+  float* g1 = nullptr;
+  float* g2 = nullptr;
+  bool uploaded = false;
+};
+
+// Prefill activations. Q/K/V^T rows are padded per sequence to S_pad (multiple
+// of 32) for the attention kernel.
+struct Workspace {
+  long cap_T = 0, cap_Tpad = 0;
+  void* base = nullptr;
+  float *x = nullptr, *x2 = nullptr, *logits = nullptr, *loss = nullptr, *mean = nullptr;
+  f16 *xn = nullptr, *q = nullptr, *k = nullptr, *vt = nullptr, *attn = nullptr, *gate = nullptr;
+  uint32_t *tok = nullptr, *tgt = nullptr;
+};
+
+}  // namespace
+
+struct hb_model {
+  hb_ctx* ctx = nullptr;
+  int device = 0;
+  hb_model_config cfg{};
+  void* wbase = nullptr;
+  size_t wbytes = 0;
+  std::vector<LayerW> layers;
+  f16* embed = nullptr;  // [vocab, dim]
+  float* gamma_f = nullptr;
+  bool embed_uploaded = false;
+  float2* rope = nullptr;
+  int rope_len = 0;
+  float* staging = nullptr;
+  size_t staging_floats = 0;
+  Workspace ws;
+  int graph_epoch = 0;  // bumped when a captured decode graph goes stale
+};
+
+struct hb_kv {
+  hb_model* model = nullptr;
+  int device = 0;
+  int B = 0, ctx_max = 0, ctx_cap = 0, nch = 0;
+  int len = 0;
+  f16* cache = nullptr;  // [L][B][2][KVH][ctx_cap][hd]
+  size_t cache_bytes = 0;
+  void* sbase = nullptr;  // small decode buffers
+  int *d_pos = nullptr, *d_pos0 = nullptr;
+  uint32_t *d_tok = nullptr, *d_next = nullptr, *d_hist = nullptr;
+  float *x = nullptr, *x2 = nullptr, *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
+  f16 *xn = nullptr, *qd = nullptr, *attn = nullptr, *gate = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int graph_epoch = -1;
+};
+
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+int check_err_word(hb_ctx* ctx) {
+  int h = 0;
+  HIP_TRY(hipMemcpyAsync(&h, ctx->d_err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream()));
+  HIP_TRY(hipStreamSynchronize(ctx->stream()));
+  if (h) {
+    int zero = 0;
+    HIP_TRY(hipMemcpyAsync(ctx->d_err, &zero, sizeof(int), hipMemcpyHostToDevice, ctx->stream()));
+    HIP_TRY(hipStreamSynchronize(ctx->stream()));
+    return fail(HB_E_INVALID, "device saw an out-of-range %s id (error word 0x%x)",
+                (h & 1) ? "token" : "target", h);
+  }
+  return HB_OK;
+}
+
+float alpha_of(const hb_model_config& c) { return c.residual_alpha; }
+
+int validate_config(const hb_model_config& c) {
+  if (c.dim <= 0 || c.hidden <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.hd <= 0 || c.seq <= 0 ||
+      c.nlayers <= 0 || c.vocab <= 0)
+    return fail(HB_E_CONFIG, "all dimensions must be positive");
+  if (c.hd != 64 && c.hd != 128) return fail(HB_E_CONFIG, "hd must be 64 or 128 (got %d)", c.hd);
+  if (c.q_dim != c.heads * c.hd) return fail(HB_E_CONFIG, "q_dim != heads*hd");
+  if (c.kv_dim != c.kv_heads * c.hd) return fail(HB_E_CONFIG, "kv_dim != kv_heads*hd");
+  if (c.heads % c.kv_heads) return fail(HB_E_CONFIG, "heads %% kv_heads != 0");
+  if (c.gqa_ratio != c.heads / c.kv_heads) return fail(HB_E_CONFIG, "gqa_ratio != heads/kv_heads");
+  if (c.dim % 64 || c.hidden % 64 || c.q_dim % 64 || c.kv_dim % 64 || c.vocab % 64)
+    return fail(HB_E_CONFIG, "dim, hidden, q_dim, kv_dim and vocab must be multiples of 64");
+  if (c.vocab >= (1 << 30) || c.dim > 65536 || c.hidden > 262144)
+    return fail(HB_E_CONFIG, "dimension too large");
+  return HB_OK;
+}
+
+// RoPE table exactly as kernels/sdpa_fwd.rs:18-33 computes it:
+// theta = p / base^(2i/hd) in f32; (cos, sin) per (p, i).
+int ensure_rope(hb_model* m, int len) {
+  if (len <= m->rope_len) return HB_OK;
+  const int half = m->cfg.hd / 2;
+  std::vector<float2> tab((size_t)len * half);
+  for (int p = 0; p < len; ++p)
+    for (int i = 0; i < half; ++i) {
+      const float theta =
+          (float)p / powf(m->cfg.rope_theta, 2.0f * (float)i / (float)m->cfg.hd);
+      tab[(size_t)p * half + i] = make_float2(cosf(theta), sinf(theta));
+    }
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
+  if (m->rope) HIP_TRY(hipFree(m->rope));
+  m->rope = nullptr;
+  HIP_TRY(hipMalloc(&m->rope, tab.size() * sizeof(float2)));
+  HIP_TRY(hipMemcpy(m->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+  m->rope_len = len;
+  m->graph_epoch++;  // captured decode graphs hold the old table address
+  return HB_OK;
+}
+
+int ensure_staging(hb_model* m, size_t floats) {
+  if (floats <= m->staging_floats) return HB_OK;
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
+  if (m->staging) HIP_TRY(hipFree(m->staging));
+  m->staging = nullptr;
+  HIP_TRY(hipMalloc(&m->staging, floats * sizeof(float)));
+  m->staging_floats = floats;
+  return HB_OK;
+}
+
+int ensure_workspace(hb_model* m, long T, long Tpad) {
+  Workspace& w = m->ws;
+  if (T <= w.cap_T && Tpad <= w.cap_Tpad) return HB_OK;
+  T = std::max(T, w.cap_T);
+  Tpad = std::max(Tpad, w.cap_Tpad);
+  const hb_model_config& c = m->cfg;
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
+  if (w.base) HIP_TRY(hipFree(w.base));
+  w = Workspace{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  const size_t o_x = take(T * c.dim * 4), o_x2 = take(T * c.dim * 4);
+  const size_t o_logits = take((size_t)T * c.vocab * 4), o_loss = take(T * 4), o_mean = take(4);
+  const size_t o_xn = take(T * c.dim * 2), o_attn = take(T * c.q_dim * 2);
+  const size_t o_gate = take((size_t)T * c.hidden * 2);
+  const size_t o_q = take(Tpad * c.q_dim * 2), o_k = take(Tpad * c.kv_dim * 2);
+  const size_t o_vt = take(Tpad * c.kv_dim * 2);
+  const size_t o_tok = take(T * 4), o_tgt = take(T * 4);
+  char* base = nullptr;
+  HIP_TRY(hipMalloc(&base, off));
+  w.base = base;
+  w.cap_T = T;
+  w.cap_Tpad = Tpad;
+  w.x = (float*)(base + o_x);
+  w.x2 = (float*)(base + o_x2);
+  w.logits = (float*)(base + o_logits);
+  w.loss = (float*)(base + o_loss);
+  w.mean = (float*)(base + o_mean);
+  w.xn = (f16*)(base + o_xn);
+  w.attn = (f16*)(base + o_attn);
+  w.gate = (f16*)(base + o_gate);
+  w.q = (f16*)(base + o_q);
+  w.k = (f16*)(base + o_k);
+  w.vt = (f16*)(base + o_vt);
+  w.tok = (uint32_t*)(base + o_tok);
+  w.tgt = (uint32_t*)(base + o_tgt);
+  // Padding rows/columns of Q, K and V^T are read (and masked) by attention:
+  // keep them finite.
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(fill_f16_zero(w.q, (size_t)Tpad * c.q_dim, st));
+  HIP_TRY(fill_f16_zero(w.k, (size_t)Tpad * c.kv_dim, st));
+  HIP_TRY(fill_f16_zero(w.vt, (size_t)Tpad * c.kv_dim, st));
+  return HB_OK;
+}
+
+int S_pad_of(int S) { return (S + 31) & ~31; }
+
+bool weights_ready(hb_model* m) {
+  if (!m->embed_uploaded) return false;
+  for (auto& l : m->layers)
+    if (!l.uploaded) return false;
+  return true;
+}
+
+// One transformer layer over T = B*S token rows (layer.rs:684-806 order).
+// x -> x (in place through x2). K/V targets are either the workspace scratch
+// (forward) or the KV cache (prefill for decode).
+struct KVTarget {
+  f16* k;
+  size_t k_bstride, k_hstride;
+  f16* v;  // nullable
+  size_t v_bstride, v_hstride;
+};
+
+int zero_vt_pad(hb_model* m, int B, int S, hipStream_t st);
+
+int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_tap) {
+  const hb_model_config& c = m->cfg;
+  Workspace& w = m->ws;
+  const LayerW& L = m->layers[l];
+  hipStream_t st = m->ctx->stream();
+  const int T = B * S, Sp = S_pad_of(S);
+  const float alpha = alpha_of(c);
+
+  HIP_TRY(rmsnorm(w.x, c.dim, L.g1, T, c.dim, c.norm_eps, w.xn, nullptr, st));
+  EpiQKV e{};
+  e.q_dim = c.q_dim;
+  e.kv_dim = c.kv_dim;
+  e.hd = c.hd;
+  e.S = S;
+  e.heads = c.heads;
+  e.kv_heads = c.kv_heads;
+  e.rope = m->rope;
+  e.d_pos = nullptr;
+  e.q = w.q;
+  e.q_rows = Sp;
+  e.k = kv.k;
+  e.k_bstride = kv.k_bstride;
+  e.k_hstride = kv.k_hstride;
+  e.v = kv.v;
+  e.v_bstride = kv.v_bstride;
+  e.v_hstride = kv.v_hstride;
+  e.vt = w.vt;
+  e.vt_ld = Sp;
+  e.tap = qkv_tap;
+  HIP_TRY(gemm_qkv(L.wqkv, w.xn, c.q_dim + 2 * c.kv_dim, T, c.dim, e, st));
+  TRY(zero_vt_pad(m, B, S, st));
+  AttnPrefill a{};
+  a.q = w.q;
+  a.q_rows = Sp;
+  a.k = kv.k;
+  a.k_bstride = kv.k_bstride;
+  a.k_hstride = kv.k_hstride;
+  a.vt = w.vt;
+  a.vt_ld = Sp;
+  a.out = w.attn;
+  a.B = B;
+  a.S = S;
+  a.H = c.heads;
+  a.KVH = c.kv_heads;
+  a.hd = c.hd;
+  a.scale = 1.0f / sqrtf((float)c.hd);
+  HIP_TRY(attention_prefill(a, st));
+  HIP_TRY(gemm_residual(L.wo, w.attn, c.dim, T, c.q_dim, EpiResidual{w.x, w.x2, c.dim, alpha}, st));
+  HIP_TRY(rmsnorm(w.x2, c.dim, L.g2, T, c.dim, c.norm_eps, w.xn, nullptr, st));
+  HIP_TRY(gemm_swiglu(L.w13, w.xn, 2 * c.hidden, T, c.dim, EpiSwiGLU{w.gate, nullptr, c.hidden}, st));
+  HIP_TRY(gemm_residual(L.w2, w.gate, c.dim, T, c.hidden, EpiResidual{w.x2, w.x, c.dim, alpha}, st));
+  return HB_OK;
+}
+
+KVTarget scratch_kv(hb_model* m, int B, int S) {
+  const hb_model_config& c = m->cfg;
+  const int Sp = S_pad_of(S);
+  KVTarget t{};
+  t.k = m->ws.k;
+  t.k_hstride = (size_t)Sp * c.hd;
+  t.k_bstride = (size_t)c.kv_heads * t.k_hstride;
+  t.v = nullptr;
+  (void)B;
+  return t;
+}
+
+}  // namespace
+
+// Zero the V^T columns [S, S_pad) so masked (p = 0) keys never meet a NaN.
+__global__ void zero_vt_pad_kernel(f16* vt, int rows, int ld, int S) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 5);
+  const int c = S + (threadIdx.x & 31);
+  if (r < rows && c < ld) vt[(size_t)r * ld + c] = (f16)0.f;
+}
+
+namespace {
+int zero_vt_pad(hb_model* m, int B, int S, hipStream_t st) {
+  const int Sp = S_pad_of(S);
+  if (Sp == S) return HB_OK;
+  const int rows = B * m->cfg.kv_heads * m->cfg.hd;
+  hipLaunchKernelGGL(zero_vt_pad_kernel, dim3((rows + 3) / 4), dim3(128), 0, st, m->ws.vt, rows, Sp,
+                     S);
+  HIP_TRY(hipGetLastError());
+  return HB_OK;
+}
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// library / context
+// ---------------------------------------------------------------------------
+extern "C" const char* hb_backend_name(void) { return "hip-gfx950"; }
+extern "C" const char* hb_last_error(void) { return g_err.c_str(); }
+
+extern "C" int hb_debug_inject_error(int code) {
+  g_inject.store(code);
+  return HB_OK;
+}
+
+extern "C" int hb_device_count(int* out) {
+  HB_INJECT_CHECK();
+  if (!out) return fail(HB_E_INVALID, "null out");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *out = n;
+  return HB_OK;
+}
+
+extern "C" int hb_ctx_create(int device, hb_ctx** out) {
+  HB_INJECT_CHECK();
+  if (!out) return fail(HB_E_INVALID, "null out");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(HB_E_DEVICE, "no HIP device");
+  if (device < 0 || device >= n) return fail(HB_E_INVALID, "device %d out of range [0,%d)", device, n);
+  DeviceGuard g(device);
+  hb_ctx* c = new hb_ctx();
+  c->device = device;
+  // The context's own stream is a blocking stream: it orders with work that
+  // callers put on the null stream (torch's default). Graph capture uses a
+  // separate non-blocking stream.
+  hipError_t e = hipStreamCreateWithFlags(&c->own, hipStreamDefault);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->capture, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(&c->d_err, 256);
+  if (e == hipSuccess) e = hipMemset(c->d_err, 0, 256);
+  if (e != hipSuccess) {
+    if (c->own) (void)hipStreamDestroy(c->own);
+    if (c->capture) (void)hipStreamDestroy(c->capture);
+    delete c;
+    return fail(HB_E_DEVICE, "context setup failed: %s", hipGetErrorString(e));
+  }
+  *out = c;
+  return HB_OK;
+}
+
+extern "C" int hb_ctx_destroy(hb_ctx* c) {
+  if (!c) return HB_OK;
+  DeviceGuard g(c->device);
+  (void)hipDeviceSynchronize();  // the caller's stream may already be gone
+  (void)hipFree(c->d_err);
+  (void)hipStreamDestroy(c->own);
+  (void)hipStreamDestroy(c->capture);
+  delete c;
+  return HB_OK;
+}
+
+extern "C" int hb_ctx_set_stream(hb_ctx* c, void* s) {
+  HB_INJECT_CHECK();
+  if (!c) return fail(HB_E_INVALID, "null ctx");
+  c->user = (hipStream_t)s;
+  return HB_OK;
+}
+
+extern "C" int hb_ctx_get_stream(hb_ctx* c, void** s) {
+  HB_INJECT_CHECK();
+  if (!c || !s) return fail(HB_E_INVALID, "null argument");
+  *s = (void*)c->stream();
+  return HB_OK;
+}
+
+extern "C" int hb_ctx_synchronize(hb_ctx* c) {
+  HB_INJECT_CHECK();
+  if (!c) return fail(HB_E_INVALID, "null ctx");
+  DeviceGuard g(c->device);
+  HIP_TRY(hipStreamSynchronize(c->stream()));
+  return check_err_word(c);
+}
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+extern "C" int hb_model_create(hb_ctx* ctx, const hb_model_config* cfg_in, int dtype,
+                               hb_model** out) {
+  HB_INJECT_CHECK();
+  if (!ctx || !cfg_in || !out) return fail(HB_E_INVALID, "null argument");
+  *out = nullptr;
+  if (dtype != HB_DTYPE_F16) return fail(HB_E_CONFIG, "unsupported dtype %d", dtype);
+  hb_model_config c = *cfg_in;
+  if (c.rope_theta == 0.f) c.rope_theta = 10000.0f;
+  if (c.norm_eps == 0.f) c.norm_eps = 1e-5f;
+  if (c.residual_alpha == 0.f && c.nlayers > 0)
+    c.residual_alpha = 1.0f / sqrtf(2.0f * (float)c.nlayers);
+  TRY(validate_config(c));
+  DeviceGuard g(ctx->device);
+
+  const size_t d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden, V = c.vocab;
+  const size_t per_layer = align256((q + 2 * kv) * d * 2) + align256(d * q * 2) +
+                           align256(2 * h * d * 2) + align256(d * h * 2) + 2 * align256(d * 4);
+  const size_t total = per_layer * c.nlayers + align256(V * d * 2) + align256(d * 4);
+  char* base = nullptr;
+  hipError_t e = hipMalloc(&base, total);
+  if (e != hipSuccess)
+    return fail(e == hipErrorOutOfMemory ? HB_E_OOM : HB_E_DEVICE,
+                "weight allocation of %zu bytes failed: %s", total, hipGetErrorString(e));
+  hb_model* m = new hb_model();
+  m->ctx = ctx;
+  m->device = ctx->device;
+  m->cfg = c;
+  m->wbase = base;
+  m->wbytes = total;
+  m->layers.resize(c.nlayers);
+  size_t off = 0;
+  for (int l = 0; l < c.nlayers; ++l) {
+    LayerW& L = m->layers[l];
+    L.wqkv = (f16*)(base + off); off += align256((q + 2 * kv) * d * 2);
+    L.wo = (f16*)(base + off); off += align256(d * q * 2);
+    L.w13 = (f16*)(base + off); off += align256(2 * h * d * 2);
+    L.w2 = (f16*)(base + off); off += align256(d * h * 2);
+    L.g1 = (float*)(base + off); off += align256(d * 4);
+    L.g2 = (float*)(base + off); off += align256(d * 4);
+  }
+  m->embed = (f16*)(base + off); off += align256(V * d * 2);
+  m->gamma_f = (float*)(base + off);
+  int r = ensure_rope(m, c.seq);
+  if (r != HB_OK) {
+    (void)hipFree(base);
+    delete m;
+    return r;
+  }
+  *out = m;
+  return HB_OK;
+}
+
+// Destroy functions touch only their own object: callers (for instance a
+// garbage collector finalising a reference cycle) may destroy a context or
+// model before the objects created from it.
+extern "C" int hb_model_destroy(hb_model* m) {
+  if (!m) return HB_OK;
+  DeviceGuard g(m->device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(m->wbase);
+  if (m->rope) (void)hipFree(m->rope);
+  if (m->staging) (void)hipFree(m->staging);
+  if (m->ws.base) (void)hipFree(m->ws.base);
+  delete m;
+  return HB_OK;
+}
+
+extern "C" int hb_model_get_config(const hb_model* m, hb_model_config* out) {
+  HB_INJECT_CHECK();
+  if (!m || !out) return fail(HB_E_INVALID, "null argument");
+  *out = m->cfg;
+  return HB_OK;
+}
+
+extern "C" int hb_model_weight_bytes(const hb_model* m, uint64_t* out) {
+  HB_INJECT_CHECK();
+  if (!m || !out) return fail(HB_E_INVALID, "null argument");
+  *out = m->wbytes;
+  return HB_OK;
+}
+
+extern "C" int hb_model_set_softcap(hb_model* m, float softcap) {
+  HB_INJECT_CHECK();
+  if (!m) return fail(HB_E_INVALID, "null model");
+  if (!(softcap >= 0.f)) return fail(HB_E_INVALID, "softcap must be >= 0");
+  if (softcap != m->cfg.softcap) {
+    m->cfg.softcap = softcap;
+    // The decode graphs bake the softcap into their logits launch.
+    m->graph_epoch++;
+  }
+  return HB_OK;
+}
+
+namespace {
+// Host fp32 [R][C] -> staging -> packed fp16.
+int upload_packed(hb_model* m, const float* src, int R, int C, f16* dst, int ld, int row0, int mode) {
+  TRY(ensure_staging(m, (size_t)R * C));
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(m->staging, src, (size_t)R * C * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(repack(m->staging, R, C, dst, ld, row0, mode, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+int upload_f32(hb_model* m, const float* src, size_t n, float* dst) {
+  HIP_TRY(hipMemcpyAsync(dst, src, n * 4, hipMemcpyHostToDevice, m->ctx->stream()));
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
+  return HB_OK;
+}
+}  // namespace
+
+extern "C" int hb_model_upload_layer(hb_model* m, int layer, const float* wq, const float* wk,
+                                     const float* wv, const float* wo, const float* w1,
+                                     const float* w3, const float* w2, const float* g1,
+                                     const float* g2) {
+  HB_INJECT_CHECK();
+  if (!m) return fail(HB_E_INVALID, "null model");
+  if (layer < 0 || layer >= m->cfg.nlayers) return fail(HB_E_INVALID, "layer %d out of range", layer);
+  if (!wq || !wk || !wv || !wo || !w1 || !w3 || !w2 || !g1 || !g2)
+    return fail(HB_E_INVALID, "null weight pointer");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  LayerW& L = m->layers[layer];
+  const int d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden;
+  TRY(upload_packed(m, wq, d, q, L.wqkv, d, 0, 0));
+  TRY(upload_packed(m, wk, d, kv, L.wqkv, d, q, 0));
+  TRY(upload_packed(m, wv, d, kv, L.wqkv, d, q + kv, 0));
+  TRY(upload_packed(m, wo, q, d, L.wo, q, 0, 0));
+  TRY(upload_packed(m, w1, d, h, L.w13, d, 0, 1));
+  TRY(upload_packed(m, w3, d, h, L.w13, d, 2, 1));
+  TRY(upload_packed(m, w2, d, h, L.w2, h, 0, 2));
+  TRY(upload_f32(m, g1, d, L.g1));
+  TRY(upload_f32(m, g2, d, L.g2));
+  L.uploaded = true;
+  return HB_OK;
+}
+
+extern "C" int hb_model_upload_embed(hb_model* m, const float* embed, const float* gamma_final) {
+  HB_INJECT_CHECK();
+  if (!m || !embed || !gamma_final) return fail(HB_E_INVALID, "null argument");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  // Upload in row chunks to bound the staging buffer.
+  const int rows_per = std::max(1, (int)std::min<size_t>(c.vocab, (64u << 20) / c.dim));
+  for (int r0 = 0; r0 < c.vocab; r0 += rows_per) {
+    const int rows = std::min(rows_per, c.vocab - r0);
+    TRY(upload_packed(m, embed + (size_t)r0 * c.dim, rows, c.dim, m->embed, c.dim, r0, 2));
+  }
+  TRY(upload_f32(m, gamma_final, c.dim, m->gamma_f));
+  m->embed_uploaded = true;
+  return HB_OK;
+}
+
+extern "C" int hb_model_init_synthetic(hb_model* m, uint64_t seed, float std) {
+  HB_INJECT_CHECK();
+  if (!m) return fail(HB_E_INVALID, "null model");
+  if (!(std > 0.f)) return fail(HB_E_INVALID, "std must be positive");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  hipStream_t st = m->ctx->stream();
+  const float sc = hb_normal_scale(std);
+  const int d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden;
+  // Same staging -> repack path as a host upload, with the fp32 source array
+  // generated on the device instead of copied from the host.
+  auto put = [&](uint64_t id, int R, int C, f16* dst, int ld, int row0, int mode) -> int {
+    TRY(ensure_staging(m, (size_t)R * C));
+    HIP_TRY(synth_f32(seed, id, sc, 0, (size_t)R * C, m->staging, st));
+    HIP_TRY(repack(m->staging, R, C, dst, ld, row0, mode, st));
+    return HB_OK;
+  };
+  for (int l = 0; l < c.nlayers; ++l) {
+    LayerW& L = m->layers[l];
+    const uint64_t id = 16ull * l;
+    TRY(put(id + 0, d, q, L.wqkv, d, 0, 0));
+    TRY(put(id + 1, d, kv, L.wqkv, d, q, 0));
+    TRY(put(id + 2, d, kv, L.wqkv, d, q + kv, 0));
+    TRY(put(id + 3, q, d, L.wo, q, 0, 0));
+    TRY(put(id + 4, d, h, L.w13, d, 0, 1));
+    TRY(put(id + 5, d, h, L.w13, d, 2, 1));
+    TRY(put(id + 6, d, h, L.w2, h, 0, 2));
+    HIP_TRY(fill_f32(L.g1, 1.0f, d, st));
+    HIP_TRY(fill_f32(L.g2, 1.0f, d, st));
+    L.uploaded = true;
+  }
+  const int rows_per = std::max(1, (int)std::min<size_t>(c.vocab, (64u << 20) / c.dim));
+  for (int r0 = 0; r0 < c.vocab; r0 += rows_per) {
+    const int rows = std::min(rows_per, c.vocab - r0);
+    TRY(ensure_staging(m, (size_t)rows * d));
+    HIP_TRY(synth_f32(seed, HB_SYNTH_EMBED_ID, sc, (uint64_t)r0 * d, (size_t)rows * d, m->staging, st));
+    HIP_TRY(repack(m->staging, rows, d, m->embed, d, r0, 2, st));
+  }
+  HIP_TRY(fill_f32(m->gamma_f, 1.0f, d, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  m->embed_uploaded = true;
+  return HB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// synthetic host inputs
+// ---------------------------------------------------------------------------
+template <class F>
+static void parallel_for(uint64_t n, F f) {
+  unsigned nt = std::min(16u, std::max(1u, std::thread::hardware_concurrency()));
+  if (n < (1u << 16)) nt = 1;
+  std::vector<std::thread> th;
+  for (unsigned i = 0; i < nt; ++i)
+    th.emplace_back([=] {
+      const uint64_t a = n * i / nt, b = n * (i + 1) / nt;
+      for (uint64_t j = a; j < b; ++j) f(j);
+    });
+  for (auto& t : th) t.join();
+}
+
+extern "C" int hb_synth_normal(uint64_t seed, uint64_t tensor_id, float std, uint64_t n, float* out) {
+  HB_INJECT_CHECK();
+  if (!out && n) return fail(HB_E_INVALID, "null out");
+  const uint64_t key = hb_stream_key(seed, tensor_id);
+  const float sc = hb_normal_scale(std);
+  parallel_for(n, [=](uint64_t i) { out[i] = hb_normal_value(key, i, sc); });
+  return HB_OK;
+}
+
+extern "C" int hb_synth_tokens(uint64_t seed, uint64_t stream, uint32_t vocab, uint64_t n,
+                               uint32_t* out) {
+  HB_INJECT_CHECK();
+  if (!out && n) return fail(HB_E_INVALID, "null out");
+  if (vocab == 0) return fail(HB_E_INVALID, "vocab must be positive");
+  const uint64_t key = hb_stream_key(seed, stream);
+  parallel_for(n, [=](uint64_t i) { out[i] = hb_token_value(key, i, vocab); });
+  return HB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+extern "C" int hb_model_reserve(hb_model* m, int B, int S) {
+  HB_INJECT_CHECK();
+  if (!m || B <= 0 || S <= 0) return fail(HB_E_INVALID, "bad argument");
+  DeviceGuard g(m->ctx->device);
+  return ensure_workspace(m, (long)B * S, (long)B * S_pad_of(S));
+}
+
+static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets,
+                               int B, int S, float* d_loss, float* d_logits, float* d_mean) {
+  const hb_model_config& c = m->cfg;
+  if (B <= 0 || S <= 0 || S > c.seq) return fail(HB_E_INVALID, "need B >= 1 and 1 <= S <= seq (%d)", c.seq);
+  if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
+  if (!d_tokens) return fail(HB_E_INVALID, "null tokens");
+  const long T = (long)B * S, Tp = (long)B * S_pad_of(S);
+  TRY(ensure_workspace(m, T, Tp));
+  Workspace& w = m->ws;
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(embedding(m->embed, d_tokens, (int)T, c.dim, c.vocab, w.x, m->ctx->d_err, st));
+  const KVTarget kv = scratch_kv(m, B, S);
+  for (int l = 0; l < c.nlayers; ++l) TRY(run_layer(m, l, B, S, kv, nullptr));
+  HIP_TRY(rmsnorm(w.x, c.dim, m->gamma_f, (int)T, c.dim, c.norm_eps, w.xn, nullptr, st));
+  float* logits = d_logits ? d_logits : w.logits;
+  HIP_TRY(gemm_logits(m->embed, w.xn, c.vocab, (int)T, c.dim, EpiLogits{logits, c.vocab, c.softcap}, st));
+  if (d_targets) {
+    float* loss = d_loss ? d_loss : w.loss;
+    HIP_TRY(cross_entropy(logits, d_targets, (int)T, c.vocab, loss, nullptr, m->ctx->d_err, st));
+    if (d_mean) HIP_TRY(mean_reduce(loss, (int)T, d_mean, st));
+  }
+  return HB_OK;
+}
+
+extern "C" int hb_forward_device(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets,
+                                 int B, int S, float* d_loss, float* d_logits, float* d_mean) {
+  HB_INJECT_CHECK();
+  if (!m) return fail(HB_E_INVALID, "null model");
+  DeviceGuard g(m->ctx->device);
+  return forward_device_impl(m, d_tokens, d_targets, B, S, d_loss, d_logits, d_mean);
+}
+
+static int check_ids(const uint32_t* ids, size_t n, int vocab, const char* what) {
+  for (size_t i = 0; i < n; ++i)
+    if (ids[i] >= (uint32_t)vocab)
+      return fail(HB_E_INVALID, "%s[%zu] = %u out of range [0,%d)", what, i, ids[i], vocab);
+  return HB_OK;
+}
+
+extern "C" int hb_forward(hb_model* m, const uint32_t* tokens, const uint32_t* targets, int B,
+                          int S, float* per_pos_loss, float* logits, float* mean_loss) {
+  HB_INJECT_CHECK();
+  if (!m || !tokens) return fail(HB_E_INVALID, "null argument");
+  if (B <= 0 || S <= 0 || S > m->cfg.seq) return fail(HB_E_INVALID, "need B >= 1 and 1 <= S <= seq (%d)", m->cfg.seq);
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  const size_t T = (size_t)B * S;
+  TRY(check_ids(tokens, T, c.vocab, "tokens"));
+  if (targets) TRY(check_ids(targets, T, c.vocab, "targets"));
+  TRY(ensure_workspace(m, (long)T, (long)B * S_pad_of(S)));
+  Workspace& w = m->ws;
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(w.tok, tokens, T * 4, hipMemcpyHostToDevice, st));
+  if (targets) HIP_TRY(hipMemcpyAsync(w.tgt, targets, T * 4, hipMemcpyHostToDevice, st));
+  TRY(forward_device_impl(m, w.tok, targets ? w.tgt : nullptr, B, S, w.loss, w.logits, w.mean));
+  if (targets && per_pos_loss)
+    HIP_TRY(hipMemcpyAsync(per_pos_loss, w.loss, T * 4, hipMemcpyDeviceToHost, st));
+  if (targets && mean_loss) HIP_TRY(hipMemcpyAsync(mean_loss, w.mean, 4, hipMemcpyDeviceToHost, st));
+  if (logits) HIP_TRY(hipMemcpyAsync(logits, w.logits, T * c.vocab * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return check_err_word(m->ctx);
+}
+
+// ---------------------------------------------------------------------------
+// per-kernel entry points
+// ---------------------------------------------------------------------------
+extern "C" int hb_op_rmsnorm(hb_ctx* ctx, const float* x, const float* gamma, int T, int dim,
+                             float eps, void* out, float* rms_inv) {
+  HB_INJECT_CHECK();
+  if (!ctx || !x || !gamma || !out) return fail(HB_E_INVALID, "null argument");
+  if (T < 0 || dim <= 0 || dim % 4) return fail(HB_E_INVALID, "need T >= 0 and dim %% 4 == 0");
+  DeviceGuard g(ctx->device);
+  HIP_TRY(rmsnorm(x, dim, gamma, T, dim, eps, (f16*)out, rms_inv, ctx->stream()));
+  return HB_OK;
+}
+
+extern "C" int hb_op_embedding(hb_model* m, const uint32_t* tok, int T, float* x) {
+  HB_INJECT_CHECK();
+  if (!m || !tok || !x) return fail(HB_E_INVALID, "null argument");
+  if (!m->embed_uploaded) return fail(HB_E_STATE, "embedding not uploaded");
+  DeviceGuard g(m->ctx->device);
+  HIP_TRY(embedding(m->embed, tok, T, m->cfg.dim, m->cfg.vocab, x, m->ctx->d_err, m->ctx->stream()));
+  return HB_OK;
+}
+
+extern "C" int hb_op_sdpa_fwd(hb_model* m, int layer, const void* xnorm, int B, int S, void* attn,
+                              float* qkv_tap) {
+  HB_INJECT_CHECK();
+  if (!m || !xnorm || !attn) return fail(HB_E_INVALID, "null argument");
+  if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
+    return fail(HB_E_STATE, "layer %d not available", layer);
+  if (B <= 0 || S <= 0 || S > m->cfg.seq) return fail(HB_E_INVALID, "bad B/S");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  const int T = B * S, Sp = S_pad_of(S);
+  TRY(ensure_workspace(m, T, (long)B * Sp));
+  Workspace& w = m->ws;
+  hipStream_t st = m->ctx->stream();
+  const KVTarget kv = scratch_kv(m, B, S);
+  EpiQKV e{};
+  e.q_dim = c.q_dim; e.kv_dim = c.kv_dim; e.hd = c.hd; e.S = S; e.heads = c.heads;
+  e.kv_heads = c.kv_heads; e.rope = m->rope; e.d_pos = nullptr; e.q = w.q; e.q_rows = Sp;
+  e.k = kv.k; e.k_bstride = kv.k_bstride; e.k_hstride = kv.k_hstride; e.v = nullptr;
+  e.vt = w.vt; e.vt_ld = Sp; e.tap = qkv_tap;
+  HIP_TRY(gemm_qkv(m->layers[layer].wqkv, (const f16*)xnorm, c.q_dim + 2 * c.kv_dim, T, c.dim, e, st));
+  TRY(zero_vt_pad(m, B, S, st));
+  AttnPrefill a{};
+  a.q = w.q; a.q_rows = Sp; a.k = kv.k; a.k_bstride = kv.k_bstride; a.k_hstride = kv.k_hstride;
+  a.vt = w.vt; a.vt_ld = Sp; a.out = (f16*)attn; a.B = B; a.S = S; a.H = c.heads;
+  a.KVH = c.kv_heads; a.hd = c.hd; a.scale = 1.0f / sqrtf((float)c.hd);
+  HIP_TRY(attention_prefill(a, st));
+  return HB_OK;
+}
+
+extern "C" int hb_op_wo_fwd(hb_model* m, int layer, const void* attn, const float* x, int T, float* x2) {
+  HB_INJECT_CHECK();
+  if (!m || !attn || !x || !x2) return fail(HB_E_INVALID, "null argument");
+  if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
+    return fail(HB_E_STATE, "layer %d not available", layer);
+  if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  HIP_TRY(gemm_residual(m->layers[layer].wo, (const f16*)attn, c.dim, T, c.q_dim,
+                        EpiResidual{x, x2, c.dim, alpha_of(c)}, m->ctx->stream()));
+  return HB_OK;
+}
+
+extern "C" int hb_op_ffn_fused(hb_model* m, int layer, const void* x2norm, const float* x2, int T,
+                               float* x_next, float* h13_tap, void* gate_out) {
+  HB_INJECT_CHECK();
+  if (!m || !x2norm || !x2 || !x_next) return fail(HB_E_INVALID, "null argument");
+  if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
+    return fail(HB_E_STATE, "layer %d not available", layer);
+  if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  f16* gate = (f16*)gate_out;
+  if (!gate) {
+    TRY(ensure_workspace(m, T, std::max<long>(m->ws.cap_Tpad, 32)));
+    gate = m->ws.gate;
+  }
+  hipStream_t st = m->ctx->stream();
+  const LayerW& L = m->layers[layer];
+  HIP_TRY(gemm_swiglu(L.w13, (const f16*)x2norm, 2 * c.hidden, T, c.dim, EpiSwiGLU{gate, h13_tap, c.hidden}, st));
+  HIP_TRY(gemm_residual(L.w2, gate, c.dim, T, c.hidden, EpiResidual{x2, x_next, c.dim, alpha_of(c)}, st));
+  return HB_OK;
+}
+
+extern "C" int hb_op_ffn_up(hb_model* m, int layer, const void* x2norm, int T, void* gate,
+                            float* h13_tap) {
+  HB_INJECT_CHECK();
+  if (!m || !x2norm || !gate) return fail(HB_E_INVALID, "null argument");
+  if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
+    return fail(HB_E_STATE, "layer %d not available", layer);
+  if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  HIP_TRY(gemm_swiglu(m->layers[layer].w13, (const f16*)x2norm, 2 * c.hidden, T, c.dim,
+                      EpiSwiGLU{(f16*)gate, h13_tap, c.hidden}, m->ctx->stream()));
+  return HB_OK;
+}
+
+extern "C" int hb_op_logits_ce(hb_model* m, const void* xf, const uint32_t* targets, int T,
+                               float* logits, float* losses) {
+  HB_INJECT_CHECK();
+  if (!m || !xf) return fail(HB_E_INVALID, "null argument");
+  if (!logits) return fail(HB_E_INVALID, "logits buffer required");
+  if (!m->embed_uploaded) return fail(HB_E_STATE, "embedding not uploaded");
+  if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(gemm_logits(m->embed, (const f16*)xf, c.vocab, T, c.dim, EpiLogits{logits, c.vocab, c.softcap}, st));
+  if (targets && losses)
+    HIP_TRY(cross_entropy(logits, targets, T, c.vocab, losses, nullptr, m->ctx->d_err, st));
+  return HB_OK;
+}
+
+extern "C" int hb_op_gemm_nt(hb_ctx* ctx, const void* a, const void* b, float* cmat, int M, int N, int K) {
+  HB_INJECT_CHECK();
+  if (!ctx || !a || !b || !cmat) return fail(HB_E_INVALID, "null argument");
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 || N % 4) return fail(HB_E_INVALID, "need K %% 64 == 0 and N %% 4 == 0");
+  DeviceGuard g(ctx->device);
+  HIP_TRY(gemm_store((const f16*)b, (const f16*)a, N, M, K, cmat, ctx->stream()));
+  return HB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// decode
+// ---------------------------------------------------------------------------
+namespace {
+
+f16* cache_k(hb_kv* kv, int l) {
+  const hb_model_config& c = kv->model->cfg;
+  return kv->cache + (size_t)l * kv->B * 2 * c.kv_heads * kv->ctx_cap * c.hd;
+}
+
+KVTarget cache_target(hb_kv* kv, int l) {
+  const hb_model_config& c = kv->model->cfg;
+  KVTarget t{};
+  t.k = cache_k(kv, l);
+  t.k_hstride = (size_t)kv->ctx_cap * c.hd;
+  t.k_bstride = 2 * (size_t)c.kv_heads * t.k_hstride;
+  t.v = t.k + (size_t)c.kv_heads * t.k_hstride;
+  t.v_bstride = t.k_bstride;
+  t.v_hstride = t.k_hstride;
+  return t;
+}
+
+// One decode step over the kv->B sequences at position *d_pos. Launch shapes
+// do not depend on the position, so the sequence can be captured once.
+int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
+  hb_model* m = kv->model;
+  const hb_model_config& c = m->cfg;
+  const int B = kv->B;
+  const float alpha = alpha_of(c);
+  HIP_TRY(embedding(m->embed, kv->d_tok, B, c.dim, c.vocab, kv->x, m->ctx->d_err, st));
+  for (int l = 0; l < c.nlayers; ++l) {
+    const LayerW& L = m->layers[l];
+    const KVTarget t = cache_target(kv, l);
+    HIP_TRY(rmsnorm(kv->x, c.dim, L.g1, B, c.dim, c.norm_eps, kv->xn, nullptr, st));
+    EpiQKV e{};
+    e.q_dim = c.q_dim; e.kv_dim = c.kv_dim; e.hd = c.hd; e.S = 1; e.heads = c.heads;
+    e.kv_heads = c.kv_heads; e.rope = m->rope; e.d_pos = kv->d_pos; e.q = kv->qd; e.q_rows = 1;
+    e.k = t.k; e.k_bstride = t.k_bstride; e.k_hstride = t.k_hstride;
+    e.v = t.v; e.v_bstride = t.v_bstride; e.v_hstride = t.v_hstride; e.vt = nullptr; e.vt_ld = 0;
+    e.tap = nullptr;
+    HIP_TRY(gemv_qkv(L.wqkv, kv->xn, c.q_dim + 2 * c.kv_dim, B, c.dim, e, st));
+    AttnDecode a{};
+    a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
+    a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
+    a.ctx_max = kv->ctx_cap; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
+    a.part_ml = kv->part_ml; a.out = kv->attn;
+    HIP_TRY(attention_decode(a, st));
+    HIP_TRY(gemv_residual(L.wo, kv->attn, c.dim, B, c.q_dim, EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
+    HIP_TRY(rmsnorm(kv->x2, c.dim, L.g2, B, c.dim, c.norm_eps, kv->xn, nullptr, st));
+    HIP_TRY(gemv_swiglu(L.w13, kv->xn, 2 * c.hidden, B, c.dim, EpiSwiGLU{kv->gate, nullptr, c.hidden}, st));
+    HIP_TRY(gemv_residual(L.w2, kv->gate, c.dim, B, c.hidden, EpiResidual{kv->x2, kv->x, c.dim, alpha}, st));
+  }
+  HIP_TRY(rmsnorm(kv->x, c.dim, m->gamma_f, B, c.dim, c.norm_eps, kv->xn, nullptr, st));
+  HIP_TRY(gemv_logits(m->embed, kv->xn, c.vocab, B, c.dim, EpiLogits{kv->logits, c.vocab, c.softcap}, st));
+  HIP_TRY(cross_entropy(kv->logits, nullptr, B, c.vocab, nullptr, kv->d_next, nullptr, st));
+  HIP_TRY(decode_advance(kv->d_next, kv->d_tok, kv->d_hist, kv->d_pos, kv->d_pos0, B, st));
+  return HB_OK;
+}
+
+bool graphs_enabled() {
+  const char* s = getenv("HB_NO_GRAPH");
+  return !(s && s[0] == '1');
+}
+
+int launch_decode_step(hb_kv* kv) {
+  hb_ctx* ctx = kv->model->ctx;
+  if (!graphs_enabled()) return enqueue_decode_step(kv, ctx->stream());
+  if (kv->exec && kv->graph_epoch != kv->model->graph_epoch) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream()));
+    (void)hipGraphExecDestroy(kv->exec);
+    (void)hipGraphDestroy(kv->graph);
+    kv->exec = nullptr;
+    kv->graph = nullptr;
+  }
+  if (!kv->exec) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream()));
+    HIP_TRY(hipStreamBeginCapture(ctx->capture, hipStreamCaptureModeThreadLocal));
+    int r = enqueue_decode_step(kv, ctx->capture);
+    hipGraph_t gr = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->capture, &gr);
+    if (r != HB_OK) {
+      if (gr) (void)hipGraphDestroy(gr);
+      return r;
+    }
+    if (e != hipSuccess) return fail(HB_E_DEVICE, "graph capture failed: %s", hipGetErrorString(e));
+    kv->graph = gr;
+    HIP_TRY(hipGraphInstantiate(&kv->exec, gr, nullptr, nullptr, 0));
+    kv->graph_epoch = kv->model->graph_epoch;
+  }
+  HIP_TRY(hipGraphLaunch(kv->exec, ctx->stream()));
+  return HB_OK;
+}
+
+}  // namespace
+
+extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
+  HB_INJECT_CHECK();
+  if (!m || !out) return fail(HB_E_INVALID, "null argument");
+  *out = nullptr;
+  if (batch < 1 || batch > 16) return fail(HB_E_INVALID, "batch must be in [1, 16] (got %d)", batch);
+  if (ctx_max < 1) return fail(HB_E_INVALID, "ctx_max must be positive");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  hb_kv* kv = new hb_kv();
+  kv->model = m;
+  kv->device = m->device;
+  kv->B = batch;
+  kv->ctx_max = ctx_max;
+  kv->ctx_cap = (ctx_max + 63) & ~63;
+  kv->nch = attn_decode_chunks(kv->ctx_cap);
+  int r = ensure_rope(m, kv->ctx_cap);
+  if (r != HB_OK) {
+    delete kv;
+    return r;
+  }
+  kv->cache_bytes = (size_t)c.nlayers * batch * 2 * c.kv_heads * kv->ctx_cap * c.hd * 2;
+  hipError_t e = hipMalloc(&kv->cache, kv->cache_bytes);
+  if (e != hipSuccess) {
+    delete kv;
+    return fail(e == hipErrorOutOfMemory ? HB_E_OOM : HB_E_DEVICE, "KV cache of %zu bytes: %s",
+                kv->cache_bytes, hipGetErrorString(e));
+  }
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  const size_t B = batch;
+  const size_t o_pos = take(4), o_pos0 = take(4), o_tok = take(B * 4), o_next = take(B * 4);
+  const size_t o_hist = take((size_t)kv->ctx_cap * B * 4);
+  const size_t o_x = take(B * c.dim * 4), o_x2 = take(B * c.dim * 4);
+  const size_t o_logits = take(B * c.vocab * 4);
+  const size_t o_po = take(B * c.heads * kv->nch * c.hd * 4), o_pml = take(B * c.heads * kv->nch * 8);
+  const size_t o_xn = take(B * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(B * c.q_dim * 2);
+  const size_t o_gate = take(B * c.hidden * 2);
+  char* sb = nullptr;
+  e = hipMalloc(&sb, off);
+  if (e != hipSuccess) {
+    (void)hipFree(kv->cache);
+    delete kv;
+    return fail(HB_E_OOM, "decode buffers: %s", hipGetErrorString(e));
+  }
+  kv->sbase = sb;
+  kv->d_pos = (int*)(sb + o_pos);
+  kv->d_pos0 = (int*)(sb + o_pos0);
+  kv->d_tok = (uint32_t*)(sb + o_tok);
+  kv->d_next = (uint32_t*)(sb + o_next);
+  kv->d_hist = (uint32_t*)(sb + o_hist);
+  kv->x = (float*)(sb + o_x);
+  kv->x2 = (float*)(sb + o_x2);
+  kv->logits = (float*)(sb + o_logits);
+  kv->part_o = (float*)(sb + o_po);
+  kv->part_ml = (float*)(sb + o_pml);
+  kv->xn = (f16*)(sb + o_xn);
+  kv->qd = (f16*)(sb + o_qd);
+  kv->attn = (f16*)(sb + o_attn);
+  kv->gate = (f16*)(sb + o_gate);
+  hipStream_t st = m->ctx->stream();
+  e = hipMemsetAsync(sb, 0, off, st);
+  if (e == hipSuccess) e = fill_f16_zero(kv->cache, kv->cache_bytes / 2, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    (void)hipFree(kv->cache);
+    (void)hipFree(sb);
+    delete kv;
+    return fail(HB_E_DEVICE, "KV init: %s", hipGetErrorString(e));
+  }
+  *out = kv;
+  return HB_OK;
+}
+
+extern "C" int hb_kv_destroy(hb_kv* kv) {
+  if (!kv) return HB_OK;
+  DeviceGuard g(kv->device);
+  (void)hipDeviceSynchronize();
+  if (kv->exec) (void)hipGraphExecDestroy(kv->exec);
+  if (kv->graph) (void)hipGraphDestroy(kv->graph);
+  (void)hipFree(kv->cache);
+  (void)hipFree(kv->sbase);
+  delete kv;
+  return HB_OK;
+}
+
+extern "C" int hb_kv_reset(hb_kv* kv) {
+  HB_INJECT_CHECK();
+  if (!kv) return fail(HB_E_INVALID, "null kv");
+  DeviceGuard g(kv->model->ctx->device);
+  HIP_TRY(set_int(kv->d_pos, 0, kv->model->ctx->stream()));
+  HIP_TRY(hipStreamSynchronize(kv->model->ctx->stream()));
+  kv->len = 0;
+  return HB_OK;
+}
+
+extern "C" int hb_kv_length(hb_kv* kv, int* out) {
+  HB_INJECT_CHECK();
+  if (!kv || !out) return fail(HB_E_INVALID, "null argument");
+  *out = kv->len;
+  return HB_OK;
+}
+
+extern "C" int hb_kv_bytes(hb_kv* kv, uint64_t* out) {
+  HB_INJECT_CHECK();
+  if (!kv || !out) return fail(HB_E_INVALID, "null argument");
+  *out = kv->cache_bytes;
+  return HB_OK;
+}
+
+extern "C" int hb_prefill(hb_model* m, hb_kv* kv, const uint32_t* tokens, int S, float* h_logits,
+                          uint32_t* h_next) {
+  HB_INJECT_CHECK();
+  if (!m || !kv || !tokens) return fail(HB_E_INVALID, "null argument");
+  if (kv->model != m) return fail(HB_E_INVALID, "kv cache belongs to another model");
+  if (kv->len != 0) return fail(HB_E_STATE, "prefill needs an empty cache (length %d)", kv->len);
+  if (S < 1 || S > kv->ctx_max) return fail(HB_E_INVALID, "S must be in [1, ctx_max]");
+  if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  const int B = kv->B;
+  const long T = (long)B * S;
+  TRY(check_ids(tokens, T, c.vocab, "tokens"));
+  TRY(ensure_rope(m, kv->ctx_cap));
+  TRY(ensure_workspace(m, T, (long)B * S_pad_of(S)));
+  Workspace& w = m->ws;
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(w.tok, tokens, T * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(embedding(m->embed, w.tok, (int)T, c.dim, c.vocab, w.x, m->ctx->d_err, st));
+  for (int l = 0; l < c.nlayers; ++l) TRY(run_layer(m, l, B, S, cache_target(kv, l), nullptr));
+  // Last position of each sequence -> logits and greedy token.
+  HIP_TRY(rmsnorm(w.x + (size_t)(S - 1) * c.dim, (long)S * c.dim, m->gamma_f, B, c.dim, c.norm_eps,
+                  kv->xn, nullptr, st));
+  HIP_TRY(gemv_logits(m->embed, kv->xn, c.vocab, B, c.dim, EpiLogits{kv->logits, c.vocab, c.softcap}, st));
+  HIP_TRY(cross_entropy(kv->logits, nullptr, B, c.vocab, nullptr, kv->d_next, nullptr, st));
+  HIP_TRY(set_int(kv->d_pos, S, st));
+  if (h_logits) HIP_TRY(hipMemcpyAsync(h_logits, kv->logits, (size_t)B * c.vocab * 4, hipMemcpyDeviceToHost, st));
+  if (h_next) HIP_TRY(hipMemcpyAsync(h_next, kv->d_next, (size_t)B * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  TRY(check_err_word(m->ctx));
+  kv->len = S;
+  return HB_OK;
+}
+
+extern "C" int hb_decode_step(hb_model* m, hb_kv* kv, const uint32_t* tokens, float* h_logits,
+                              uint32_t* h_next) {
+  HB_INJECT_CHECK();
+  if (!m || !kv || !tokens) return fail(HB_E_INVALID, "null argument");
+  if (kv->model != m) return fail(HB_E_INVALID, "kv cache belongs to another model");
+  if (kv->len >= kv->ctx_max) return fail(HB_E_STATE, "KV cache full (%d positions)", kv->ctx_max);
+  if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  TRY(check_ids(tokens, kv->B, c.vocab, "tokens"));
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(kv->d_tok, tokens, (size_t)kv->B * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(set_int(kv->d_pos0, kv->len, st));
+  TRY(launch_decode_step(kv));
+  if (h_logits) HIP_TRY(hipMemcpyAsync(h_logits, kv->logits, (size_t)kv->B * c.vocab * 4, hipMemcpyDeviceToHost, st));
+  if (h_next) HIP_TRY(hipMemcpyAsync(h_next, kv->d_next, (size_t)kv->B * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  TRY(check_err_word(m->ctx));
+  kv->len += 1;
+  return HB_OK;
+}
+
+extern "C" int hb_decode_greedy(hb_model* m, hb_kv* kv, const uint32_t* first, int nsteps,
+                                uint32_t* h_out) {
+  HB_INJECT_CHECK();
+  if (!m || !kv || !first) return fail(HB_E_INVALID, "null argument");
+  if (kv->model != m) return fail(HB_E_INVALID, "kv cache belongs to another model");
+  if (nsteps < 0 || kv->len + nsteps > kv->ctx_max)
+    return fail(HB_E_STATE, "%d steps from length %d exceed ctx_max %d", nsteps, kv->len, kv->ctx_max);
+  if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
+  DeviceGuard g(m->ctx->device);
+  const hb_model_config& c = m->cfg;
+  TRY(check_ids(first, kv->B, c.vocab, "first tokens"));
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(kv->d_tok, first, (size_t)kv->B * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(set_int(kv->d_pos0, kv->len, st));
+  for (int i = 0; i < nsteps; ++i) TRY(launch_decode_step(kv));
+  if (h_out && nsteps)
+    HIP_TRY(hipMemcpyAsync(h_out, kv->d_hist, (size_t)nsteps * kv->B * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  TRY(check_err_word(m->ctx));
+  kv->len += nsteps;
+  return HB_OK;
+}

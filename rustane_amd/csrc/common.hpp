@@ -1,0 +1,66 @@
+// Shared types and device helpers for the gfx950 kernels of libhip_bridge.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define HB_DEV __device__ __forceinline__
+
+// 1/ln(2): softmax is evaluated as exp2((s - m) * log2(e)).
+#define HB_LOG2E 1.4426950408889634f
+
+// Wave-wide reductions (64 lanes). __shfl_xor lowers to DPP / ds_swizzle.
+HB_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+HB_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Block-wide reduction through LDS; `red` holds one float per wave.
+template <int NWAVES>
+HB_DEV float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < NWAVES; ++w) s += red[w];
+  return s;
+}
+template <int NWAVES>
+HB_DEV float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < NWAVES; ++w) m = fmaxf(m, red[w]);
+  return m;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (wg % 8). Remap so
+// that each XCD receives a contiguous range of tile ids: tiles that share a
+// weight panel then run on one XCD and share its L2. Bijective for any n.
+HB_DEV int xcd_remap(int wg, int n) {
+  const int q = n >> 3, r = n & 7;
+  const int xcd = wg & 7, slot = wg >> 3;
+  return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+}
+
+HB_DEV float silu_f(float x) { return x * (1.0f / (1.0f + __expf(-x))); }

@@ -1,0 +1,279 @@
+// Bandwidth-bound kernels: embedding gather, RMSNorm, cross-entropy/argmax,
+// reductions, weight repacking and the seeded synthetic fill.
+#include "internal.hpp"
+#include "synth.hpp"
+
+namespace hb {
+
+// ---- embedding (cpu/embedding.rs:8-16): x[t,:] = E[tok[t],:] -------------------
+__global__ __launch_bounds__(256) void embedding_kernel(const f16* __restrict__ E,
+                                                        const uint32_t* __restrict__ tok, int dim,
+                                                        int vocab, float* __restrict__ x,
+                                                        int* err) {
+  const int t = blockIdx.x;
+  const uint32_t id = tok[t];
+  float* xr = x + (size_t)t * dim;
+  if (id >= (uint32_t)vocab) {
+    // Never read outside E; report through the error word.
+    for (int c = threadIdx.x * 4; c < dim; c += 256 * 4) *(f32x4*)(xr + c) = f32x4{};
+    if (threadIdx.x == 0 && err) atomicOr(err, 1);
+    return;
+  }
+  const f16* er = E + (size_t)id * dim;
+  for (int c = threadIdx.x * 8; c < dim; c += 256 * 8) {
+    const f16x8 v = *(const f16x8*)(er + c);
+    f32x4 a, b;
+    a.x = (float)v[0]; a.y = (float)v[1]; a.z = (float)v[2]; a.w = (float)v[3];
+    b.x = (float)v[4]; b.y = (float)v[5]; b.z = (float)v[6]; b.w = (float)v[7];
+    *(f32x4*)(xr + c) = a;
+    *(f32x4*)(xr + c + 4) = b;
+  }
+}
+
+hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
+                     int* err, hipStream_t st) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(embedding_kernel, dim3(T), dim3(256), 0, st, E, tok, dim, vocab, x, err);
+  return hipGetLastError();
+}
+
+// ---- RMSNorm (cpu/rmsnorm.rs:149-183) -------------------------------------------
+// r = 1/sqrt(sum(x^2) * (1/dim) + eps); y = x * r * gamma. One workgroup per row.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, long row_stride,
+                                                      const float* __restrict__ gamma, int dim,
+                                                      float eps, f16* __restrict__ out,
+                                                      float* __restrict__ rms_inv) {
+  __shared__ float red[4];
+  const int t = blockIdx.x;
+  const float* xr = x + (size_t)t * row_stride;
+  float ss = 0.f;
+  for (int c = threadIdx.x * 4; c < dim; c += 1024) {
+    const f32x4 v = *(const f32x4*)(xr + c);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = block_sum<4>(ss, red);
+  const float r = 1.0f / sqrtf(ss * (1.0f / (float)dim) + eps);
+  if (rms_inv && threadIdx.x == 0) rms_inv[t] = r;
+  f16* orow = out + (size_t)t * dim;
+  for (int c = threadIdx.x * 4; c < dim; c += 1024) {
+    const f32x4 v = *(const f32x4*)(xr + c);
+    const f32x4 g = *(const f32x4*)(gamma + c);
+    f16x4 o;
+    o.x = (f16)(v.x * r * g.x);
+    o.y = (f16)(v.y * r * g.y);
+    o.z = (f16)(v.z * r * g.z);
+    o.w = (f16)(v.w * r * g.w);
+    *(f16x4*)(orow + c) = o;
+  }
+}
+
+hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
+                   f16* out, float* rms_inv, hipStream_t st) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, st, x, row_stride, gamma, dim, eps,
+                     out, rms_inv);
+  return hipGetLastError();
+}
+
+// ---- cross-entropy + argmax (cpu/cross_entropy.rs:13-38, 58-96) ------------------
+// One workgroup per row, one pass over the logits: each thread keeps a running
+// (max, sum of exp(x - max)) pair and the first index of its maximum; pairs are
+// merged across the block. loss = ln(sum) - (x[y] - max).
+struct SoftState {
+  float m, s, best;
+  int idx;
+};
+HB_DEV void soft_push(SoftState& st, float x, int i) {
+  if (x > st.m) {
+    st.s = st.s * exp2f((st.m - x) * HB_LOG2E) + 1.0f;
+    st.m = x;
+  } else {
+    st.s += exp2f((x - st.m) * HB_LOG2E);
+  }
+  if (x > st.best || (x == st.best && i < st.idx)) {
+    st.best = x;
+    st.idx = i;
+  }
+}
+HB_DEV void soft_merge(SoftState& a, const SoftState& b) {
+  const float m = fmaxf(a.m, b.m);
+  float s = 0.f;
+  if (a.m != -INFINITY) s += a.s * exp2f((a.m - m) * HB_LOG2E);
+  if (b.m != -INFINITY) s += b.s * exp2f((b.m - m) * HB_LOG2E);
+  a.m = m;
+  a.s = s;
+  if (b.best > a.best || (b.best == a.best && b.idx < a.idx)) {
+    a.best = b.best;
+    a.idx = b.idx;
+  }
+}
+
+__global__ __launch_bounds__(256) void cross_entropy_kernel(const float* __restrict__ logits,
+                                                            const uint32_t* __restrict__ targets,
+                                                            int vocab, float* __restrict__ loss,
+                                                            uint32_t* __restrict__ argmax,
+                                                            int* err) {
+  __shared__ SoftState red[256];
+  const int t = blockIdx.x;
+  const float* row = logits + (size_t)t * vocab;
+  SoftState st{-INFINITY, 0.f, -INFINITY, 0x7fffffff};
+  for (int c = threadIdx.x * 4; c < vocab; c += 1024) {
+    const f32x4 v = *(const f32x4*)(row + c);
+    soft_push(st, v.x, c);
+    soft_push(st, v.y, c + 1);
+    soft_push(st, v.z, c + 2);
+    soft_push(st, v.w, c + 3);
+  }
+  red[threadIdx.x] = st;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      SoftState a = red[threadIdx.x];
+      soft_merge(a, red[threadIdx.x + o]);
+      red[threadIdx.x] = a;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const SoftState r = red[0];
+    if (argmax) argmax[t] = (uint32_t)r.idx;
+    if (loss && targets) {
+      const uint32_t y = targets[t];
+      if (y < (uint32_t)vocab) {
+        loss[t] = logf(r.s) - (row[y] - r.m);
+      } else {
+        loss[t] = NAN;
+        if (err) atomicOr(err, 2);
+      }
+    }
+  }
+}
+
+hipError_t cross_entropy(const float* logits, const uint32_t* targets, int T, int vocab,
+                         float* loss, uint32_t* argmax, int* err, hipStream_t st) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(cross_entropy_kernel, dim3(T), dim3(256), 0, st, logits, targets, vocab, loss,
+                     argmax, err);
+  return hipGetLastError();
+}
+
+// Deterministic mean: fixed-order per-thread sums, fixed tree.
+__global__ __launch_bounds__(256) void mean_kernel(const float* __restrict__ v, int n,
+                                                   float* __restrict__ out) {
+  __shared__ float red[4];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < n; i += 256) s += v[i];
+  s = block_sum<4>(s, red);
+  if (threadIdx.x == 0) out[0] = s / (float)n;
+}
+
+hipError_t mean_reduce(const float* v, int n, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(mean_kernel, dim3(1), dim3(256), 0, st, v, n, out);
+  return hipGetLastError();
+}
+
+__global__ void decode_advance_kernel(const uint32_t* next, uint32_t* tok, uint32_t* hist,
+                                      int* d_pos, const int* d_pos0, int B) {
+  const int b = threadIdx.x;
+  const int pos = *d_pos;
+  if (b < B) {
+    tok[b] = next[b];
+    if (hist) hist[(size_t)(pos - *d_pos0) * B + b] = next[b];
+  }
+  __syncthreads();
+  if (b == 0) *d_pos = pos + 1;
+}
+
+hipError_t decode_advance(const uint32_t* next, uint32_t* tok, uint32_t* hist, int* d_pos,
+                          const int* d_pos0, int B, hipStream_t st) {
+  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(64), 0, st, next, tok, hist, d_pos,
+                     d_pos0, B);
+  return hipGetLastError();
+}
+
+__global__ void set_int_kernel(int* d, int v) { *d = v; }
+hipError_t set_int(int* d, int value, hipStream_t st) {
+  hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, st, d, value);
+  return hipGetLastError();
+}
+
+// ---- weight repacking -------------------------------------------------------------
+HB_DEV int repack_row(int mode, int i, int j, int row0) {
+  if (mode == 0) return row0 + j;
+  if (mode == 1) return ((j >> 1) << 2) + (j & 1) + row0;
+  return row0 + i;
+}
+
+// 64x64 tiles through LDS so both the fp32 reads and fp16 writes are coalesced.
+__global__ __launch_bounds__(256) void repack_kernel(const float* __restrict__ src, int R, int C,
+                                                     f16* __restrict__ dst, int ld, int row0,
+                                                     int mode) {
+  __shared__ float tile[64][65];
+  const int i0 = blockIdx.y * 64, j0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int i = i0 + r, j = j0 + tx;
+    tile[r][tx] = (i < R && j < C) ? src[(size_t)i * C + j] : 0.f;
+  }
+  __syncthreads();
+  if (mode == 2) {
+    for (int r = ty; r < 64; r += 4) {
+      const int i = i0 + r, j = j0 + tx;
+      if (i < R && j < C) dst[(size_t)repack_row(mode, i, j, row0) * ld + j] = (f16)tile[r][tx];
+    }
+  } else {
+    // dst row indexed by source column j, dst column = source row i.
+    for (int r = ty; r < 64; r += 4) {
+      const int j = j0 + r, i = i0 + tx;
+      if (i < R && j < C) dst[(size_t)repack_row(mode, i, j, row0) * ld + i] = (f16)tile[tx][r];
+    }
+  }
+}
+
+hipError_t repack(const float* src, int R, int C, f16* dst, int ld, int row0, int mode,
+                  hipStream_t st) {
+  dim3 grid((C + 63) / 64, (R + 63) / 64);
+  hipLaunchKernelGGL(repack_kernel, grid, dim3(256), 0, st, src, R, C, dst, ld, row0, mode);
+  return hipGetLastError();
+}
+
+// Synthetic values of hb_synth_normal's sequence, elements [first, first+n),
+// written as fp32 (the fp16 conversion then happens in repack_kernel, exactly
+// as for a host upload of the same array).
+__global__ __launch_bounds__(256) void synth_f32_kernel(uint64_t key, float scale, uint64_t first,
+                                                        size_t n, float* __restrict__ dst) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    dst[i] = hb_normal_value(key, first + i, scale);
+}
+
+hipError_t synth_f32(uint64_t seed, uint64_t tensor_id, float scale, uint64_t first, size_t n,
+                     float* dst, hipStream_t st) {
+  const uint64_t key = hb_stream_key(seed, tensor_id);
+  const int blocks = (int)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(synth_f32_kernel, dim3(blocks), dim3(256), 0, st, key, scale, first, n, dst);
+  return hipGetLastError();
+}
+
+__global__ void fill_f32_kernel(float* d, float v, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    d[i] = v;
+}
+hipError_t fill_f32(float* d, float v, size_t n, hipStream_t st) {
+  const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks), dim3(256), 0, st, d, v, n);
+  return hipGetLastError();
+}
+__global__ void fill_f16_zero_kernel(f16* d, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    d[i] = (f16)0.f;
+}
+hipError_t fill_f16_zero(f16* d, size_t n, hipStream_t st) {
+  const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_f16_zero_kernel, dim3(blocks), dim3(256), 0, st, d, n);
+  return hipGetLastError();
+}
+
+}  // namespace hb

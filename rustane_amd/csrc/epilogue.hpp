@@ -1,0 +1,159 @@
+// GEMM epilogues. Both the prefill MFMA GEMM and the decode GEMV hand each
+// lane's results to an epilogue as (token row t, first feature f0, 4 values
+// for features f0..f0+3). f0 is always a multiple of 4, and feature blocks of
+// 4 never straddle a Q/K/V or head boundary because hd % 64 == 0.
+#pragma once
+#include "common.hpp"
+
+namespace hb {
+
+// C[t, f0..f0+3] = v (fp32). Plain GEMM output.
+struct EpiStore {
+  float* c;
+  int ldc;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    *(f32x4*)(c + (size_t)t * ldc + f0) = v;
+  }
+};
+
+// out = res + alpha * v (fp32 residual stream). woFwd + vsma (layer.rs:784) and
+// the ffnFused residual (kernels/ffn_fused.rs:74-77).
+struct EpiResidual {
+  const float* res;
+  float* out;
+  int ld;
+  float alpha;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    const size_t o = (size_t)t * ld + f0;
+    const f32x4 r = *(const f32x4*)(res + o);
+    f32x4 y;
+    y.x = v.x * alpha + r.x;
+    y.y = v.y * alpha + r.y;
+    y.z = v.z * alpha + r.z;
+    y.w = v.w * alpha + r.w;
+    *(f32x4*)(out + o) = y;
+  }
+};
+
+// W1 and W3 are packed row-interleaved in groups of four: packed rows 4j..4j+3
+// are W1 column 2j, W1 column 2j+1, W3 column 2j, W3 column 2j+1. A lane's
+// 4 consecutive features are therefore (h1[u], h1[u+1], h3[u], h3[u+1]) with
+// u = f0/2, and the SwiGLU gate (kernels/ffn_fused.rs:60-62) is formed in
+// registers: gate = silu(h1) * h3.
+struct EpiSwiGLU {
+  f16* gate;   // [T, hidden]
+  float* tap;  // nullable [T, 2*hidden] = h1 | h3
+  int hidden;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    const int u = f0 >> 1;
+    f16x2 g;
+    g.x = (f16)(silu_f(v.x) * v.z);
+    g.y = (f16)(silu_f(v.y) * v.w);
+    *(f16x2*)(gate + (size_t)t * hidden + u) = g;
+    if (tap) {
+      float* r = tap + (size_t)t * 2 * hidden;
+      r[u] = v.x;
+      r[u + 1] = v.y;
+      r[hidden + u] = v.z;
+      r[hidden + u + 1] = v.w;
+    }
+  }
+};
+
+// Tied-embedding logits with optional softcap (full_model.rs:228-239).
+struct EpiLogits {
+  float* logits;
+  int vocab;
+  float softcap;  // 0 = off
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    if (softcap > 0.f) {
+      const float ic = 1.0f / softcap;
+      v.x = softcap * tanhf(v.x * ic);
+      v.y = softcap * tanhf(v.y * ic);
+      v.z = softcap * tanhf(v.z * ic);
+      v.w = softcap * tanhf(v.w * ic);
+    }
+    *(f32x4*)(logits + (size_t)t * vocab + f0) = v;
+  }
+};
+
+// Fused-QKV epilogue (kernels/sdpa_fwd.rs:70-128): the packed weight has Wq,
+// Wk, Wv output rows stacked, so features [0,q) are Q, [q,q+kv) K, the rest V.
+// Q and K get the interleaved RoPE of sdpa_fwd.rs:18-33 / 105-128 on pairs
+// (2i, 2i+1) — both elements of a pair are in the same lane:
+//   out[2i] = x[2i] c - x[2i+1] s,   out[2i+1] = x[2i+1] c + x[2i] s.
+// Token t is position s = pos0 + t % S of sequence b = t / S (prefill), or
+// position *d_pos of sequence b = t (decode, S = 1, pos0 read from d_pos).
+struct EpiQKV {
+  int q_dim, kv_dim, hd, S, heads, kv_heads;
+  const float2* rope;  // [pos][hd/2] (cos, sin)
+  const int* d_pos;    // decode: position of the current token; prefill: NULL
+  // Q: q[((b*heads + h)*q_rows + s)*hd + e]
+  f16* q;
+  int q_rows;
+  // K rows [s][hd] at k + b*k_bstride + kvh*k_hstride
+  f16* k;
+  size_t k_bstride, k_hstride;
+  // V rows [s][hd] (KV cache layout), nullable
+  f16* v;
+  size_t v_bstride, v_hstride;
+  // V transposed [hd][s] for prefill attention: vt + (b*kv_heads+kvh)*hd*vt_ld, nullable
+  f16* vt;
+  int vt_ld;
+  float* tap;  // nullable [T, q+2kv] fp32 = Q_rope | K_rope | V
+
+  HB_DEV void operator()(int t, int f0, f32x4 v4) const {
+    int b, s;
+    if (d_pos) {
+      b = t;
+      s = *d_pos;
+    } else {
+      b = t / S;
+      s = t - b * S;
+    }
+    const int qkv = q_dim + 2 * kv_dim;
+    if (f0 < q_dim + kv_dim) {
+      const bool isq = f0 < q_dim;
+      const int f = isq ? f0 : f0 - q_dim;
+      const int h = f / hd, e = f - h * hd;
+      const float2* rp = rope + (size_t)s * (hd >> 1) + (e >> 1);
+      const float2 c0 = rp[0], c1 = rp[1];
+      f32x4 o;
+      o.x = v4.x * c0.x - v4.y * c0.y;
+      o.y = v4.y * c0.x + v4.x * c0.y;
+      o.z = v4.z * c1.x - v4.w * c1.y;
+      o.w = v4.w * c1.x + v4.z * c1.y;
+      f16x4 oh;
+      oh.x = (f16)o.x;
+      oh.y = (f16)o.y;
+      oh.z = (f16)o.z;
+      oh.w = (f16)o.w;
+      if (isq) {
+        const int qs = d_pos ? 0 : s;  // decode keeps one Q row per sequence
+        *(f16x4*)(q + (((size_t)b * heads + h) * q_rows + qs) * hd + e) = oh;
+      } else {
+        *(f16x4*)(k + b * k_bstride + h * k_hstride + (size_t)s * hd + e) = oh;
+      }
+      if (tap) *(f32x4*)(tap + (size_t)t * qkv + f0) = o;
+    } else {
+      const int f = f0 - q_dim - kv_dim;
+      const int h = f / hd, e = f - h * hd;
+      f16x4 vh;
+      vh.x = (f16)v4.x;
+      vh.y = (f16)v4.y;
+      vh.z = (f16)v4.z;
+      vh.w = (f16)v4.w;
+      if (v) *(f16x4*)(v + b * v_bstride + h * v_hstride + (size_t)s * hd + e) = vh;
+      if (vt) {
+        f16* p = vt + ((size_t)b * kv_heads + h) * hd * vt_ld + (size_t)e * vt_ld + s;
+        p[0] = vh.x;
+        p[vt_ld] = vh.y;
+        p[2 * vt_ld] = vh.z;
+        p[3 * vt_ld] = vh.w;
+      }
+      if (tap) *(f32x4*)(tap + (size_t)t * qkv + f0) = v4;
+    }
+  }
+};
+
+}  // namespace hb

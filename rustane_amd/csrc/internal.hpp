@@ -1,0 +1,86 @@
+// Internal launcher API shared by the kernel translation units and the C ABI.
+#pragma once
+#include "common.hpp"
+#include "epilogue.hpp"
+
+namespace hb {
+
+// ---- prefill GEMM (gemm.hip) ----
+hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st);
+hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
+                         hipStream_t st);
+hipError_t gemm_swiglu(const f16* W, const f16* X, int N, int T, int K, const EpiSwiGLU& e,
+                       hipStream_t st);
+hipError_t gemm_logits(const f16* W, const f16* X, int N, int T, int K, const EpiLogits& e,
+                       hipStream_t st);
+hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQKV& e,
+                    hipStream_t st);
+
+// ---- decode GEMV (gemv.hip): rows of X are the B <= 16 sequences ----
+hipError_t gemv_residual(const f16* W, const f16* X, int N, int B, int K, const EpiResidual& e,
+                         hipStream_t st);
+hipError_t gemv_swiglu(const f16* W, const f16* X, int N, int B, int K, const EpiSwiGLU& e,
+                       hipStream_t st);
+hipError_t gemv_logits(const f16* W, const f16* X, int N, int B, int K, const EpiLogits& e,
+                       hipStream_t st);
+hipError_t gemv_qkv(const f16* W, const f16* X, int N, int B, int K, const EpiQKV& e,
+                    hipStream_t st);
+hipError_t gemv_store(const f16* W, const f16* X, int N, int B, int K, float* C, hipStream_t st);
+
+// ---- attention (attention.hip) ----
+struct AttnPrefill {
+  const f16* q;  // [B][H][q_rows][hd]
+  int q_rows;
+  const f16* k;  // rows [s][hd] at k + b*k_bstride + kvh*k_hstride
+  size_t k_bstride, k_hstride;
+  const f16* vt;  // [B][KVH][hd][vt_ld]
+  int vt_ld;
+  f16* out;  // [B*S][H*hd]
+  int B, S, H, KVH, hd;
+  float scale;  // 1/sqrt(hd)
+};
+hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st);
+
+struct AttnDecode {
+  const f16* q;  // [B][H][hd]
+  const f16* k;  // cache rows [s][hd] at k + b*bstride + kvh*hstride
+  const f16* v;
+  size_t bstride, hstride;
+  const int* d_pos;  // keys 0..*d_pos are attended
+  int B, H, KVH, hd, ctx_max;
+  float scale;
+  float* part_o;   // [B][H][nchunks][hd]
+  float* part_ml;  // [B][H][nchunks][2]
+  f16* out;        // [B][H*hd]
+};
+int attn_decode_chunks(int ctx_max);
+hipError_t attention_decode(const AttnDecode& p, hipStream_t st);
+
+// ---- elementwise / reductions (elementwise.hip) ----
+hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
+                     int* err, hipStream_t st);
+// Rows r < T of x at x + r*row_stride (floats), dim contiguous.
+hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
+                   f16* out, float* rms_inv, hipStream_t st);
+// Per-row cross-entropy (targets nullable) and argmax (nullable).
+hipError_t cross_entropy(const float* logits, const uint32_t* targets, int T, int vocab,
+                         float* loss, uint32_t* argmax, int* err, hipStream_t st);
+hipError_t mean_reduce(const float* v, int n, float* out, hipStream_t st);
+// Decode bookkeeping: tok[b] = next[b]; hist[(pos - pos0)*B + b] = next[b]; pos += 1.
+hipError_t decode_advance(const uint32_t* next, uint32_t* tok, uint32_t* hist, int* d_pos,
+                          const int* d_pos0, int B, hipStream_t st);
+hipError_t set_int(int* d, int value, hipStream_t st);
+
+// Weight repacking: src fp32 [R][C] row-major (device), dst fp16.
+//   mode 0: dst[(row0 + j) * ld + i] = src[i][j]              (transpose)
+//   mode 1: dst[((j>>1)*4 + (j&1) + row0) * ld + i] = src[i][j] (W1/W3 interleave)
+//   mode 2: dst[(row0 + i) * ld + j] = src[i][j]              (copy)
+hipError_t repack(const float* src, int R, int C, f16* dst, int ld, int row0, int mode,
+                  hipStream_t st);
+// Elements [first, first+n) of hb_synth_normal(seed, tensor_id) as fp32.
+hipError_t synth_f32(uint64_t seed, uint64_t tensor_id, float scale, uint64_t first, size_t n,
+                     float* dst, hipStream_t st);
+hipError_t fill_f32(float* d, float v, size_t n, hipStream_t st);
+hipError_t fill_f16_zero(f16* d, size_t n, hipStream_t st);
+
+}  // namespace hb

@@ -1,0 +1,323 @@
+"""Model-level API of rustane's engine crate, served by libhip_bridge.
+
+Mirrors the names and argument meaning of the reference so callers switch
+without changes:
+
+  ModelConfig        crates/engine/src/model.rs:5-152 (fields, presets, param_count)
+  LayerWeights       crates/engine/src/layer.rs:16-26 (fp32, reference layouts)
+  ModelWeights       crates/engine/src/full_model.rs:13-17, random 84-90
+  CompiledKernels    crates/engine/src/layer.rs:220-275 (compile(cfg))
+  forward            crates/engine/src/full_model.rs:345-410 -> ForwardResult.loss
+  forward_ws         crates/engine/src/full_model.rs:187-247 -> mean loss
+  forward_losses     crates/engine/src/full_model.rs:717-767 -> per-position losses
+  Decoder            the single-token loop crates/metal-decode/src/lib.rs:1-8 plans
+
+All arithmetic runs on the GPU through the C ABI; this module only moves host
+arrays across it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass, field, replace
+from typing import List, Optional
+
+import numpy as np
+
+from . import hip_bridge as hb
+
+
+@dataclass
+class ModelConfig:
+    dim: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    hd: int
+    seq: int
+    nlayers: int
+    vocab: int
+    q_dim: int
+    kv_dim: int
+    gqa_ratio: int
+    # Constants the reference hard-codes (sdpa_fwd.rs:22, rmsnorm.rs:10,
+    # layer.rs:698, full_model.rs:67); 0 selects the reference value.
+    rope_theta: float = 10000.0
+    norm_eps: float = 1e-5
+    residual_alpha: float = 0.0
+    softcap: float = 0.0
+
+    @staticmethod
+    def make(dim, hidden, heads, nlayers, seq, vocab, hd=128, kv_heads=None, **kw) -> "ModelConfig":
+        kv_heads = heads if kv_heads is None else kv_heads
+        return ModelConfig(dim=dim, hidden=hidden, heads=heads, kv_heads=kv_heads, hd=hd, seq=seq,
+                           nlayers=nlayers, vocab=vocab, q_dim=heads * hd, kv_dim=kv_heads * hd,
+                           gqa_ratio=heads // kv_heads, **kw)
+
+    # -- reference presets (model.rs:21-151) --
+    @staticmethod
+    def gpt_karpathy():
+        return ModelConfig.make(768, 2048, 6, 6, 512, 8192)
+
+    @staticmethod
+    def gpt_1024():
+        return ModelConfig.make(1024, 2816, 8, 8, 512, 8192)
+
+    @staticmethod
+    def target_600m():
+        return ModelConfig.make(1536, 4096, 12, 20, 512, 8192)
+
+    @staticmethod
+    def target_800m():
+        return ModelConfig.make(1792, 4864, 14, 24, 512, 8192)
+
+    @staticmethod
+    def target_1b():
+        return ModelConfig.make(2048, 5632, 16, 28, 512, 8192)
+
+    @staticmethod
+    def target_1_5b():
+        return ModelConfig.make(2304, 6144, 18, 32, 512, 8192)
+
+    @staticmethod
+    def mha_28l():
+        return ModelConfig.make(1024, 3072, 8, 28, 256, 8192)
+
+    # bench_fwd_only_scale.rs:16-27 (hd 128, vocab 8192)
+    @staticmethod
+    def custom(dim, hidden, heads, nlayers, seq):
+        return ModelConfig.make(dim, hidden, heads, nlayers, seq, 8192)
+
+    # -- the measured workloads (vocab 32000) --
+    @staticmethod
+    def llama_48m():
+        return ModelConfig.make(512, 1536, 8, 8, 512, 32000, hd=64)
+
+    @staticmethod
+    def llama_600m(seq=512):
+        return ModelConfig.make(1536, 4096, 12, 20, seq, 32000)
+
+    @staticmethod
+    def llama_5b(seq=512):
+        return ModelConfig.make(2560, 6912, 20, 60, seq, 32000)
+
+    @staticmethod
+    def llama_7b(seq=512):
+        return ModelConfig.make(4096, 11008, 32, 32, seq, 32000)
+
+    def param_count(self) -> int:
+        """model.rs:109-114 (counts 4*dim*dim for attention, as the reference does)."""
+        per_layer = 4 * self.dim * self.dim + 3 * self.dim * self.hidden
+        return self.nlayers * per_layer + self.vocab * self.dim + self.dim * (2 * self.nlayers + 1)
+
+    def alpha(self) -> float:
+        return self.residual_alpha or float(np.float32(1.0) / np.sqrt(np.float32(2.0 * self.nlayers)))
+
+
+@dataclass
+class LayerWeights:
+    wq: np.ndarray  # [dim*q_dim]
+    wk: np.ndarray  # [dim*kv_dim]
+    wv: np.ndarray  # [dim*kv_dim]
+    wo: np.ndarray  # [q_dim*dim]
+    w1: np.ndarray  # [dim*hidden]
+    w3: np.ndarray  # [dim*hidden]
+    w2: np.ndarray  # [dim*hidden]
+    gamma1: np.ndarray
+    gamma2: np.ndarray
+
+    @staticmethod
+    def random(cfg: ModelConfig) -> "LayerWeights":
+        """layer.rs:358-372: Wq/Wk/Wv 1/sqrt(dim), Wo = W2 = 0 (DeepNet), W1/W3 1/sqrt(hidden)."""
+        sq = 1.0 / math.sqrt(cfg.dim)
+        sf = 1.0 / math.sqrt(cfg.hidden)
+        return LayerWeights(
+            wq=random_vec(cfg.dim * cfg.q_dim, sq), wk=random_vec(cfg.dim * cfg.kv_dim, sq),
+            wv=random_vec(cfg.dim * cfg.kv_dim, sq), wo=np.zeros(cfg.q_dim * cfg.dim, np.float32),
+            w1=random_vec(cfg.dim * cfg.hidden, sf), w3=random_vec(cfg.dim * cfg.hidden, sf),
+            w2=np.zeros(cfg.dim * cfg.hidden, np.float32),
+            gamma1=np.ones(cfg.dim, np.float32), gamma2=np.ones(cfg.dim, np.float32))
+
+    @staticmethod
+    def synthetic(cfg: ModelConfig, layer: int, seed: int, std: float = 0.02) -> "LayerWeights":
+        """Seeded N(0, std) weights, gammas 1; the same values hb_model_init_synthetic
+        writes on the device (tensor ids 16*layer + 0..6)."""
+        b = 16 * layer
+        n = hb.synth_normal
+        d, q, kv, h = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden
+        return LayerWeights(
+            wq=n(seed, b + 0, d * q, std), wk=n(seed, b + 1, d * kv, std), wv=n(seed, b + 2, d * kv, std),
+            wo=n(seed, b + 3, q * d, std), w1=n(seed, b + 4, d * h, std), w3=n(seed, b + 5, d * h, std),
+            w2=n(seed, b + 6, d * h, std), gamma1=np.ones(d, np.float32), gamma2=np.ones(d, np.float32))
+
+
+@dataclass
+class ModelWeights:
+    embed: np.ndarray  # [vocab*dim]
+    layers: List[LayerWeights]
+    gamma_final: np.ndarray
+    version: int = 0  # bump after mutating arrays in place to force re-upload
+
+    @staticmethod
+    def random(cfg: ModelConfig) -> "ModelWeights":
+        """full_model.rs:84-90 (embed scale 0.005, gamma 1)."""
+        return ModelWeights(embed=random_vec(cfg.vocab * cfg.dim, 0.005),
+                            layers=[LayerWeights.random(cfg) for _ in range(cfg.nlayers)],
+                            gamma_final=np.ones(cfg.dim, np.float32))
+
+    @staticmethod
+    def synthetic(cfg: ModelConfig, seed: int, std: float = 0.02) -> "ModelWeights":
+        return ModelWeights(embed=hb.synth_normal(seed, hb.HB_SYNTH_EMBED_ID, cfg.vocab * cfg.dim, std),
+                            layers=[LayerWeights.synthetic(cfg, l, seed, std) for l in range(cfg.nlayers)],
+                            gamma_final=np.ones(cfg.dim, np.float32))
+
+
+_LCG_A = np.uint64(6364136223846793005)
+_LCG_C = np.uint64(1442695040888963407)
+
+
+def random_vec(n: int, scale: float) -> np.ndarray:
+    """layer.rs:404-413: seed = 42 + n; seed = seed*A + C (wrapping); r = (seed>>32)/u32::MAX*2-1.
+
+    Vectorised with LCG jump-ahead: block k+1 = A^m * block k + C_m elementwise.
+    """
+    if n == 0:
+        return np.zeros(0, np.float32)
+    m = min(n, 4096)
+    seeds = np.empty(m, np.uint64)
+    s = np.uint64(42 + n)
+    with np.errstate(over="ignore"):
+        for i in range(m):
+            s = s * _LCG_A + _LCG_C
+            seeds[i] = s
+        # jump of m steps: A_m = A^m, C_m = C*(A^(m-1) + ... + 1)
+        am, cm = np.uint64(1), np.uint64(0)
+        for _ in range(m):
+            am, cm = am * _LCG_A, cm * _LCG_A + _LCG_C
+        out = np.empty(n, np.uint64)
+        blk = seeds
+        for start in range(0, n, m):
+            take = min(m, n - start)
+            out[start:start + take] = blk[:take]
+            blk = blk * am + cm
+    hi = (out >> np.uint64(32)).astype(np.float32)
+    r = (hi / np.float32(4294967295.0)) * np.float32(2.0) - np.float32(1.0)
+    return (r * np.float32(scale)).astype(np.float32)
+
+
+class CompiledKernels:
+    """layer.rs:239-274 analogue: a device context + model for one config.
+
+    compile() validates the config and allocates device weights; weights are
+    uploaded on the first forward that sees a ModelWeights object (and again
+    only when a different object or version is passed).
+    """
+
+    def __init__(self, cfg: ModelConfig, device: int = 0):
+        self.cfg = cfg
+        self.ctx = hb.Context(device)
+        self.model = hb.Model(self.ctx, cfg)
+        self._uploaded = None
+
+    @staticmethod
+    def compile(cfg: ModelConfig, device: int = 0) -> "CompiledKernels":
+        return CompiledKernels(cfg, device)
+
+    def ensure_weights(self, weights: Optional[ModelWeights]) -> None:
+        if weights is None:
+            if self._uploaded is None:
+                raise RuntimeError("no weights uploaded")
+            return
+        key = (id(weights), weights.version)
+        if self._uploaded == key:
+            return
+        for l, lw in enumerate(weights.layers):
+            self.model.upload_layer(l, lw)
+        self.model.upload_embed(weights.embed, weights.gamma_final)
+        self._uploaded = key
+
+    def init_synthetic(self, seed: int, std: float = 0.02) -> None:
+        """Device-side seeded weights (no host copy); equals ModelWeights.synthetic."""
+        self.model.init_synthetic(seed, std)
+        self._uploaded = ("synthetic", seed, std)
+
+    def set_softcap(self, softcap: float) -> None:
+        hb.call("hb_model_set_softcap", self.model.handle, float(softcap))
+
+
+@dataclass
+class ForwardResult:
+    """full_model.rs:73-81 (forward-only fields)."""
+    loss: float
+    losses: np.ndarray
+    logits: Optional[np.ndarray] = None
+
+
+def _run(cfg, kernels, weights, tokens, targets, softcap, want_logits, batch=1):
+    kernels.ensure_weights(weights)
+    kernels.set_softcap(softcap)
+    tok = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+    T = tok.size
+    if T % batch:
+        raise ValueError("token count not divisible by batch")
+    S = T // batch
+    tgt = None if targets is None else np.ascontiguousarray(targets, dtype=np.uint32).reshape(-1)
+    losses = np.empty(T, np.float32) if tgt is not None else None
+    logits = np.empty((T, cfg.vocab), np.float32) if want_logits else None
+    mean = np.zeros(1, np.float32)
+    hb.call("hb_forward", kernels.model.handle, hb.ptr(tok), hb.ptr(tgt), batch, S, hb.ptr(losses),
+            hb.ptr(logits), hb.ptr(mean) if tgt is not None else None)
+    return float(mean[0]), losses, logits
+
+
+def forward(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights], tokens,
+            targets, softcap: float = 0.0, want_logits: bool = True, batch: int = 1) -> ForwardResult:
+    loss, losses, logits = _run(cfg, kernels, weights, tokens, targets, softcap, want_logits, batch)
+    return ForwardResult(loss=loss, losses=losses, logits=logits)
+
+
+def forward_ws(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights], tokens,
+               targets, softcap: float = 0.0, batch: int = 1) -> float:
+    return _run(cfg, kernels, weights, tokens, targets, softcap, False, batch)[0]
+
+
+def forward_losses(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights],
+                   tokens, targets, softcap: float = 0.0, batch: int = 1) -> np.ndarray:
+    return _run(cfg, kernels, weights, tokens, targets, softcap, False, batch)[1]
+
+
+class Decoder:
+    """Greedy single-token decode over a preallocated fp16 KV cache."""
+
+    def __init__(self, kernels: CompiledKernels, batch: int, ctx_max: int):
+        self.kernels = kernels
+        self.cfg = kernels.cfg
+        self.kv = hb.KVCache(kernels.model, batch, ctx_max)
+        self.batch = batch
+
+    def prefill(self, tokens) -> tuple:
+        tok = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        S = tok.size // self.batch
+        logits = np.empty((self.batch, self.cfg.vocab), np.float32)
+        nxt = np.empty(self.batch, np.uint32)
+        hb.call("hb_prefill", self.kernels.model.handle, self.kv.handle, hb.ptr(tok), S,
+                hb.ptr(logits), hb.ptr(nxt))
+        return logits, nxt
+
+    def step(self, tokens) -> tuple:
+        tok = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        logits = np.empty((self.batch, self.cfg.vocab), np.float32)
+        nxt = np.empty(self.batch, np.uint32)
+        hb.call("hb_decode_step", self.kernels.model.handle, self.kv.handle, hb.ptr(tok),
+                hb.ptr(logits), hb.ptr(nxt))
+        return logits, nxt
+
+    def greedy(self, first, nsteps: int) -> np.ndarray:
+        f = np.ascontiguousarray(first, dtype=np.uint32).reshape(-1)
+        out = np.empty((nsteps, self.batch), np.uint32)
+        hb.call("hb_decode_greedy", self.kernels.model.handle, self.kv.handle, hb.ptr(f), nsteps,
+                hb.ptr(out))
+        return out
+
+    def length(self) -> int:
+        return self.kv.length()

@@ -1,0 +1,340 @@
+"""ctypes binding of libhip_bridge.so (include/hip_bridge.h).
+
+This is the Python counterpart of the `hip-bridge` crate that replaces rustane's
+`ane-bridge` (crates/ane-bridge/src/lib.rs:8-9): a thin, typed wrapper over the
+C ABI. Errors come back as :class:`HipBridgeError` carrying the library's code
+and message, where the reference panicked with ``.expect("ANE eval failed")``
+(crates/engine/src/layer.rs:727).
+
+The library is loaded from the package directory only; there is no fallback
+implementation. If ``libhip_bridge.so`` is missing, :func:`lib` raises.
+"""
+from __future__ import annotations
+
+import atexit
+import ctypes as C
+import os
+import threading
+from dataclasses import dataclass, fields
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhip_bridge.so")
+
+HB_OK = 0
+HB_E_INVALID = -1
+HB_E_CONFIG = -2
+HB_E_DEVICE = -3
+HB_E_OOM = -4
+HB_E_STATE = -5
+HB_E_INJECTED = -6
+HB_DTYPE_F16 = 1
+HB_SYNTH_EMBED_ID = 0xFFFF
+
+_CODE_NAMES = {
+    HB_E_INVALID: "HB_E_INVALID",
+    HB_E_CONFIG: "HB_E_CONFIG",
+    HB_E_DEVICE: "HB_E_DEVICE",
+    HB_E_OOM: "HB_E_OOM",
+    HB_E_STATE: "HB_E_STATE",
+    HB_E_INJECTED: "HB_E_INJECTED",
+}
+
+
+class HipBridgeError(RuntimeError):
+    def __init__(self, code: int, msg: str, func: str):
+        self.code = code
+        super().__init__(f"{func}: {_CODE_NAMES.get(code, code)}: {msg}")
+
+
+class hb_model_config(C.Structure):
+    _fields_ = [
+        ("dim", C.c_int32),
+        ("hidden", C.c_int32),
+        ("heads", C.c_int32),
+        ("kv_heads", C.c_int32),
+        ("hd", C.c_int32),
+        ("seq", C.c_int32),
+        ("nlayers", C.c_int32),
+        ("vocab", C.c_int32),
+        ("q_dim", C.c_int32),
+        ("kv_dim", C.c_int32),
+        ("gqa_ratio", C.c_int32),
+        ("rope_theta", C.c_float),
+        ("norm_eps", C.c_float),
+        ("residual_alpha", C.c_float),
+        ("softcap", C.c_float),
+    ]
+
+
+_P = C.c_void_p
+_I = C.c_int
+_F = C.c_float
+_U64 = C.c_uint64
+_U32 = C.c_uint32
+_FP = C.POINTER(C.c_float)
+_UP = C.POINTER(C.c_uint32)
+
+# name -> argtypes; every function returns int status unless listed in _RESTYPE.
+SIGNATURES = {
+    "hb_backend_name": [],
+    "hb_last_error": [],
+    "hb_device_count": [C.POINTER(C.c_int)],
+    "hb_ctx_create": [_I, C.POINTER(_P)],
+    "hb_ctx_destroy": [_P],
+    "hb_ctx_set_stream": [_P, _P],
+    "hb_ctx_get_stream": [_P, C.POINTER(_P)],
+    "hb_ctx_synchronize": [_P],
+    "hb_model_create": [_P, C.POINTER(hb_model_config), _I, C.POINTER(_P)],
+    "hb_model_destroy": [_P],
+    "hb_model_get_config": [_P, C.POINTER(hb_model_config)],
+    "hb_model_weight_bytes": [_P, C.POINTER(C.c_uint64)],
+    "hb_model_set_softcap": [_P, _F],
+    "hb_model_upload_layer": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "hb_model_upload_embed": [_P, _P, _P],
+    "hb_model_init_synthetic": [_P, _U64, _F],
+    "hb_synth_normal": [_U64, _U64, _F, _U64, _P],
+    "hb_synth_tokens": [_U64, _U64, _U32, _U64, _P],
+    "hb_forward": [_P, _P, _P, _I, _I, _P, _P, _P],
+    "hb_forward_device": [_P, _P, _P, _I, _I, _P, _P, _P],
+    "hb_model_reserve": [_P, _I, _I],
+    "hb_op_rmsnorm": [_P, _P, _P, _I, _I, _F, _P, _P],
+    "hb_op_embedding": [_P, _P, _I, _P],
+    "hb_op_sdpa_fwd": [_P, _I, _P, _I, _I, _P, _P],
+    "hb_op_wo_fwd": [_P, _I, _P, _P, _I, _P],
+    "hb_op_ffn_fused": [_P, _I, _P, _P, _I, _P, _P, _P],
+    "hb_op_ffn_up": [_P, _I, _P, _I, _P, _P],
+    "hb_op_logits_ce": [_P, _P, _P, _I, _P, _P],
+    "hb_op_gemm_nt": [_P, _P, _P, _P, _I, _I, _I],
+    "hb_kv_create": [_P, _I, _I, C.POINTER(_P)],
+    "hb_kv_destroy": [_P],
+    "hb_kv_reset": [_P],
+    "hb_kv_length": [_P, C.POINTER(C.c_int)],
+    "hb_kv_bytes": [_P, C.POINTER(C.c_uint64)],
+    "hb_prefill": [_P, _P, _P, _I, _P, _P],
+    "hb_decode_step": [_P, _P, _P, _P, _P],
+    "hb_decode_greedy": [_P, _P, _P, _I, _P],
+    "hb_debug_inject_error": [_I],
+}
+_RESTYPE = {"hb_backend_name": C.c_char_p, "hb_last_error": C.c_char_p}
+
+_lib = None
+_lock = threading.Lock()
+_exiting = False
+
+
+def _mark_exiting():
+    # After interpreter exit has begun, torch may already have released the
+    # streams a context was bound to; the process is about to free all device
+    # memory anyway, so finalizers stop calling into the library.
+    global _exiting
+    _exiting = True
+
+
+atexit.register(_mark_exiting)
+
+
+def lib() -> C.CDLL:
+    """Load libhip_bridge.so (once). Raises if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise FileNotFoundError(
+                    f"{LIB_PATH} not built: run `make -C rustane_amd/csrc` or "
+                    "`python -c 'import __graft_entry__ as g; g.build()'`")
+            L = C.CDLL(LIB_PATH, mode=C.RTLD_GLOBAL)
+            for name, argtypes in SIGNATURES.items():
+                f = getattr(L, name)
+                f.argtypes = argtypes
+                f.restype = _RESTYPE.get(name, C.c_int)
+            _lib = L
+        return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call an int-returning entry point and raise on a non-zero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != HB_OK:
+        msg = lib().hb_last_error().decode(errors="replace")
+        raise HipBridgeError(rc, msg, name)
+
+
+def last_error() -> str:
+    return lib().hb_last_error().decode(errors="replace")
+
+
+def backend_name() -> str:
+    return lib().hb_backend_name().decode()
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    call("hb_device_count", C.byref(n))
+    return n.value
+
+
+def ptr(a) -> int | None:
+    """Address of a numpy array or torch tensor (None passes through as NULL)."""
+    if a is None:
+        return None
+    if hasattr(a, "data_ptr"):
+        return a.data_ptr()
+    return a.ctypes.data
+
+
+def config_struct(cfg) -> hb_model_config:
+    s = hb_model_config()
+    for f in fields(hb_model_config_fields):
+        setattr(s, f.name, getattr(cfg, f.name))
+    return s
+
+
+@dataclass
+class hb_model_config_fields:
+    dim: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    hd: int
+    seq: int
+    nlayers: int
+    vocab: int
+    q_dim: int
+    kv_dim: int
+    gqa_ratio: int
+    rope_theta: float
+    norm_eps: float
+    residual_alpha: float
+    softcap: float
+
+
+# ---- object wrappers ---------------------------------------------------------
+
+class Context:
+    """hb_ctx: one device + one HIP stream. Single owner, like CompiledKernels."""
+
+    def __init__(self, device: int = 0):
+        h = _P()
+        call("hb_ctx_create", device, C.byref(h))
+        self.handle = h
+        self.device = device
+
+    def set_stream(self, stream_ptr: int | None) -> None:
+        call("hb_ctx_set_stream", self.handle, stream_ptr)
+
+    def stream(self) -> int:
+        s = _P()
+        call("hb_ctx_get_stream", self.handle, C.byref(s))
+        return s.value or 0
+
+    def synchronize(self) -> None:
+        call("hb_ctx_synchronize", self.handle)
+
+    def close(self) -> None:
+        if self.handle and not _exiting:
+            lib().hb_ctx_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Model:
+    """hb_model: device weights for one ModelConfig."""
+
+    def __init__(self, ctx: Context, cfg):
+        h = _P()
+        s = config_struct(cfg)
+        call("hb_model_create", ctx.handle, C.byref(s), HB_DTYPE_F16, C.byref(h))
+        self.handle = h
+        self.ctx = ctx
+        out = hb_model_config()
+        call("hb_model_get_config", h, C.byref(out))
+        self.config = out
+
+    def upload_layer(self, layer: int, lw) -> None:
+        import numpy as np
+        arrs = [np.ascontiguousarray(getattr(lw, n), dtype=np.float32)
+                for n in ("wq", "wk", "wv", "wo", "w1", "w3", "w2", "gamma1", "gamma2")]
+        call("hb_model_upload_layer", self.handle, layer, *[a.ctypes.data for a in arrs])
+
+    def upload_embed(self, embed, gamma_final) -> None:
+        import numpy as np
+        e = np.ascontiguousarray(embed, dtype=np.float32)
+        g = np.ascontiguousarray(gamma_final, dtype=np.float32)
+        call("hb_model_upload_embed", self.handle, e.ctypes.data, g.ctypes.data)
+
+    def init_synthetic(self, seed: int, std: float = 0.02) -> None:
+        call("hb_model_init_synthetic", self.handle, seed, std)
+
+    def weight_bytes(self) -> int:
+        n = C.c_uint64()
+        call("hb_model_weight_bytes", self.handle, C.byref(n))
+        return n.value
+
+    def reserve(self, B: int, S: int) -> None:
+        call("hb_model_reserve", self.handle, B, S)
+
+    def close(self) -> None:
+        if self.handle and not _exiting:
+            lib().hb_model_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KVCache:
+    """hb_kv: preallocated fp16 KV cache + decode state for `batch` sequences."""
+
+    def __init__(self, model: Model, batch: int, ctx_max: int):
+        h = _P()
+        call("hb_kv_create", model.handle, batch, ctx_max, C.byref(h))
+        self.handle = h
+        self.model = model
+        self.batch = batch
+        self.ctx_max = ctx_max
+
+    def length(self) -> int:
+        n = C.c_int()
+        call("hb_kv_length", self.handle, C.byref(n))
+        return n.value
+
+    def nbytes(self) -> int:
+        n = C.c_uint64()
+        call("hb_kv_bytes", self.handle, C.byref(n))
+        return n.value
+
+    def reset(self) -> None:
+        call("hb_kv_reset", self.handle)
+
+    def close(self) -> None:
+        if self.handle and not _exiting:
+            lib().hb_kv_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def synth_normal(seed: int, tensor_id: int, n: int, std: float = 0.02):
+    import numpy as np
+    out = np.empty(n, dtype=np.float32)
+    call("hb_synth_normal", seed, tensor_id, std, n, out.ctypes.data)
+    return out
+
+
+def synth_tokens(seed: int, stream: int, vocab: int, n: int):
+    import numpy as np
+    out = np.empty(n, dtype=np.uint32)
+    call("hb_synth_tokens", seed, stream, vocab, n, out.ctypes.data)
+    return out

@@ -1,0 +1,205 @@
+"""Kernel-level parity on the GPU, through the C ABI (per-kernel entry points).
+
+Each stage of the reference layer (RMSNorm -> sdpaFwd -> woFwd -> residual ->
+RMSNorm -> ffnFused, layer.rs:684-806) is run on the device and compared with
+the oracle on the same inputs. Inputs to fp16 kernels are rounded to fp16
+before they reach the oracle, so the comparison measures the kernels' own
+error (fp32 accumulate) rather than input rounding.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from rustane_amd import hip_bridge as hb
+from rustane_amd.engine import CompiledKernels, ModelWeights
+from tests._util import F32, f16_round, oracle_cfg, oracle_weights, tiny_config, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm_case(gpu, M, N, K, seed):
+    import torch
+    rng = np.random.default_rng(seed)
+    a = f16_round(rng.standard_normal((M, K)))
+    b = f16_round(rng.standard_normal((N, K)))
+    da, db = to_dev(a, torch.float16), to_dev(b, torch.float16)
+    dc = torch.full((M, N), float("nan"), device="cuda")
+    hb.call("hb_op_gemm_nt", gpu.handle, da.data_ptr(), db.data_ptr(), dc.data_ptr(), M, N, K)
+    torch.cuda.synchronize()
+    ref = a.astype(np.float64) @ b.astype(np.float64).T
+    return dc.cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (64, 64, 64),        # 64x64 tiles, single K slice
+    (37, 68, 192),       # ragged token and feature tails
+    (1024, 2048, 256),   # 128x128 tiles
+    (512, 16384, 128),   # 256x128 tiles, XCD remap with 256 tiles
+    (300, 1540, 320),    # tails + non power-of-two tile count
+])
+def test_gemm_nt_matches_float64(gpu, M, N, K):
+    print(f"gemm M={M} N={N} K={K}", flush=True)
+    c, ref = _gemm_case(gpu, M, N, K, seed=M + N + K)
+    assert np.isfinite(c).all()
+    err = np.abs(c - ref).max()
+    # fp16 inputs are exact; fp32 accumulation over K terms of size ~1.
+    assert err < 1e-4 * K, err
+
+
+def test_gemm_nt_mfma_layout_one_hot(gpu):
+    """A one-hot A row selects exactly one B row: catches any lane/register
+    layout mistake in the MFMA fragments independently of rounding."""
+    import torch
+    M, N, K = 64, 64, 64
+    a = np.zeros((M, K), F32)
+    for i in range(M):
+        a[i, (7 * i + 3) % K] = 1.0
+    b = f16_round(np.random.default_rng(0).standard_normal((N, K)))
+    dc = torch.zeros((M, N), device="cuda")
+    # keep the device tensors referenced until the kernel has run
+    da, db = to_dev(a, torch.float16), to_dev(b, torch.float16)
+    hb.call("hb_op_gemm_nt", gpu.handle, da.data_ptr(), db.data_ptr(), dc.data_ptr(), M, N, K)
+    torch.cuda.synchronize()
+    expect = np.stack([b[:, (7 * i + 3) % K] for i in range(M)])
+    np.testing.assert_array_equal(dc.cpu().numpy(), expect)
+
+
+def test_rmsnorm_op_matches_oracle(gpu):
+    import torch
+    T, dim = 37, 512
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((T, dim)) * 3).astype(F32)
+    g = (1 + 0.1 * rng.standard_normal(dim)).astype(F32)
+    out = torch.empty((T, dim), dtype=torch.float16, device="cuda")
+    rinv = torch.empty(T, device="cuda")
+    dx, dg = to_dev(x), to_dev(g)
+    hb.call("hb_op_rmsnorm", gpu.handle, dx.data_ptr(), dg.data_ptr(), T, dim, 1e-5,
+            out.data_ptr(), rinv.data_ptr())
+    torch.cuda.synchronize()
+    ref, ref_r = O.rmsnorm_channel_first(x.T.reshape(-1), g, dim, T)
+    np.testing.assert_allclose(rinv.cpu().numpy(), ref_r, rtol=2e-6)
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref.reshape(dim, T).T, rtol=1e-3, atol=1e-3)
+
+
+@pytest.fixture(scope="module")
+def tiny(gpu):
+    cfg = tiny_config()
+    k = CompiledKernels.compile(cfg)
+    k.ctx.set_stream(gpu.stream())
+    w = ModelWeights.synthetic(cfg, seed=1234, std=0.02)
+    k.ensure_weights(w)
+    return cfg, k, w
+
+
+def test_embedding_op_exact(tiny):
+    import torch
+    cfg, k, w = tiny
+    tok = np.array([0, 5, cfg.vocab - 1, 17, 5], np.uint32)
+    x = torch.empty((tok.size, cfg.dim), device="cuda")
+    dtok = to_dev(tok)
+    hb.call("hb_op_embedding", k.model.handle, dtok.data_ptr(), tok.size, x.data_ptr())
+    torch.cuda.synchronize()
+    ref = f16_round(O.embedding_forward(w.embed, cfg.dim, tok).reshape(tok.size, cfg.dim))
+    np.testing.assert_array_equal(x.cpu().numpy(), ref)
+
+
+def test_synthetic_init_is_bit_identical_to_host_upload(gpu):
+    cfg = tiny_config()
+    tok = np.arange(cfg.seq, dtype=np.uint32) * 7 % cfg.vocab
+    a = CompiledKernels.compile(cfg)
+    a.init_synthetic(77, 0.02)
+    b = CompiledKernels.compile(cfg)
+    b.ensure_weights(ModelWeights.synthetic(cfg, seed=77, std=0.02))
+    la = np.empty((cfg.seq, cfg.vocab), F32)
+    lb = np.empty_like(la)
+    for kk, out in ((a, la), (b, lb)):
+        hb.call("hb_forward", kk.model.handle, hb.ptr(tok), None, 1, cfg.seq, None, hb.ptr(out), None)
+    np.testing.assert_array_equal(la, lb)
+
+
+def _layer_inputs(cfg, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((cfg.seq, cfg.dim)) * 0.5).astype(F32)
+
+
+def test_layer_ops_match_oracle(tiny):
+    """sdpaFwd (QKV + RoPE + causal attention), woFwd + residual, ffnFused, each
+    against the oracle on identical (fp16-rounded) inputs."""
+    import torch
+    cfg, k, w = tiny
+    oc = oracle_cfg(cfg)
+    lw = oracle_weights(w).layers[0]
+    S = cfg.seq
+    x = _layer_inputs(cfg, 3)
+    # RMSNorm1 on the device, then feed the same fp16 xnorm to both sides.
+    dx = to_dev(x)
+    dxn = torch.empty((S, cfg.dim), dtype=torch.float16, device="cuda")
+    g1 = to_dev(lw.gamma1)
+    hb.call("hb_op_rmsnorm", k.ctx.handle, dx.data_ptr(), g1.data_ptr(), S, cfg.dim, 1e-5,
+            dxn.data_ptr(), None)
+    dattn = torch.empty((S, cfg.q_dim), dtype=torch.float16, device="cuda")
+    tap = torch.empty((S, cfg.q_dim + 2 * cfg.kv_dim), device="cuda")
+    hb.call("hb_op_sdpa_fwd", k.model.handle, 0, dxn.data_ptr(), 1, S, dattn.data_ptr(), tap.data_ptr())
+    torch.cuda.synchronize()
+    xn = dxn.float().cpu().numpy()
+    # weights as the device holds them (fp16)
+    r = lambda a: f16_round(a)
+    s = O.sdpa_fwd(oc, xn.T, r(lw.wq), r(lw.wk), r(lw.wv), S)
+    t = tap.cpu().numpy()
+    q, kv = cfg.q_dim, cfg.kv_dim
+    np.testing.assert_allclose(t[:, :q], s["q_rope"].T, atol=2e-3)
+    np.testing.assert_allclose(t[:, q:q + kv], s["k_rope"].T, atol=2e-3)
+    np.testing.assert_allclose(t[:, q + kv:], s["v"].T, atol=2e-3)
+    np.testing.assert_allclose(dattn.float().cpu().numpy(), s["attn"].T, atol=3e-3)
+
+    # woFwd + residual on the device's own attn output
+    attn = dattn.float().cpu().numpy()
+    dx2 = torch.empty((S, cfg.dim), device="cuda")
+    hb.call("hb_op_wo_fwd", k.model.handle, 0, dattn.data_ptr(), dx.data_ptr(), S, dx2.data_ptr())
+    torch.cuda.synchronize()
+    o = O.dyn_matmul(attn.T, r(lw.wo), cfg.q_dim, cfg.dim, S)
+    x2 = O.vsma(o.reshape(-1), oc.alpha(), x.T.reshape(-1)).reshape(cfg.dim, S).T
+    np.testing.assert_allclose(dx2.cpu().numpy(), x2, atol=1e-4)
+
+    # ffnFused on a device-normed x2
+    dx2n = torch.empty((S, cfg.dim), dtype=torch.float16, device="cuda")
+    g2 = to_dev(lw.gamma2)
+    hb.call("hb_op_rmsnorm", k.ctx.handle, dx2.data_ptr(), g2.data_ptr(), S, cfg.dim, 1e-5,
+            dx2n.data_ptr(), None)
+    dnext = torch.empty((S, cfg.dim), device="cuda")
+    dh13 = torch.empty((S, 2 * cfg.hidden), device="cuda")
+    dgate = torch.empty((S, cfg.hidden), dtype=torch.float16, device="cuda")
+    hb.call("hb_op_ffn_fused", k.model.handle, 0, dx2n.data_ptr(), dx2.data_ptr(), S,
+            dnext.data_ptr(), dh13.data_ptr(), dgate.data_ptr())
+    torch.cuda.synchronize()
+    x2n = dx2n.float().cpu().numpy()
+    x2d = dx2.cpu().numpy()
+    f = O.ffn_fused(oc, x2n.T, x2d.T, r(lw.w1), r(lw.w3), r(lw.w2), S)
+    h13 = dh13.cpu().numpy()
+    np.testing.assert_allclose(h13[:, :cfg.hidden], f["h1"].T, atol=1e-3)
+    np.testing.assert_allclose(h13[:, cfg.hidden:], f["h3"].T, atol=1e-3)
+    np.testing.assert_allclose(dgate.float().cpu().numpy(), f["gate"].T, atol=1e-3)
+    # x_next from the device gate (fp16) vs oracle recomputed on that gate
+    gate = dgate.float().cpu().numpy()
+    ffn = gate @ r(lw.w2).reshape(cfg.dim, cfg.hidden).T
+    np.testing.assert_allclose(dnext.cpu().numpy(), x2d + oc.alpha() * ffn, atol=1e-4)
+
+
+def test_logits_ce_op_matches_oracle(tiny):
+    import torch
+    cfg, k, w = tiny
+    T = 33
+    rng = np.random.default_rng(5)
+    xf = f16_round(rng.standard_normal((T, cfg.dim)))
+    tgt = rng.integers(0, cfg.vocab, T).astype(np.uint32)
+    dl = torch.empty((T, cfg.vocab), device="cuda")
+    dloss = torch.empty(T, device="cuda")
+    dxf, dtgt = to_dev(xf, torch.float16), to_dev(tgt)
+    hb.call("hb_op_logits_ce", k.model.handle, dxf.data_ptr(), dtgt.data_ptr(), T, dl.data_ptr(),
+            dloss.data_ptr())
+    torch.cuda.synchronize()
+    E = f16_round(w.embed)
+    ref = O.sgemm_at(xf, T, cfg.dim, E, cfg.vocab, np.zeros(T * cfg.vocab, F32))
+    np.testing.assert_allclose(dl.cpu().numpy(), ref, atol=2e-4)
+    _, losses = O.cross_entropy_batch(dl.cpu().numpy(), tgt, cfg.vocab)
+    np.testing.assert_allclose(dloss.cpu().numpy(), losses, rtol=1e-5, atol=1e-5)
