@@ -1,0 +1,174 @@
+// Prefill GEMM kernel (launch policy in gemm.hip).
+//
+// C^T tile = W_tile · X_tile^T on v_mfma_f32_32x32x16_f16:
+//   W [N, K] fp16, K contiguous (weights repacked output-major at upload)
+//   X [T, K] fp16, K contiguous (token-major activations)
+//   result(t, f) = sum_k X[t,k] * W[f,k], fp32 accumulate, handed to an epilogue.
+// MFMA rows are output features and MFMA columns are tokens, so each lane ends
+// up holding 4 consecutive features of one token — the shape every epilogue
+// (RoPE pairs, SwiGLU pairs, residual float4) wants.
+//
+// LDS rows are 128 B (64 halfs) of eight 16-byte chunks; chunk c of row r is
+// stored at c ^ swz(r), which keeps both the loaders' ds_write_b128 and the
+// MFMA operands' ds_read_b128 free of bank conflicts for 32- and 64-bank LDS.
+#pragma once
+#include "internal.hpp"
+
+namespace hb {
+
+HB_DEV int lds_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// LDS-only workgroup barrier: orders LDS accesses of the workgroup without
+// draining outstanding global loads (a full __syncthreads would wait for the
+// prefetches that are meant to stay in flight across it).
+HB_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Pipeline: slice k+1 of W and X is fetched into registers while the MFMAs
+// consume slice k from one of two LDS buffers (one barrier per 64-wide K
+// slice); the MFMA fragments of k-step s+1 are read from LDS while the MFMAs
+// of k-step s run. The loop body is a
+// single basic block (the next-slice load and store are unconditional; past
+// the last slice they re-read the last slice into the idle LDS buffer), and
+// sched_group_barrier fixes the order within it:
+//   global loads of slice k+1 | LDS reads of k-step 0 |
+//   for k-steps 0..2: MFMAs of step s interleaved one-to-one with the LDS
+//   reads of step s+1 | MFMAs of step 3 interleaved with the LDS writes of
+//   slice k+1.
+// so LDS latency is always covered by MFMAs of the previous k-step.
+template <int FT, int TT, int WF, int WT, class Epi>
+__global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __restrict__ W,
+                                                                 const f16* __restrict__ X, int N,
+                                                                 int T, int K, Epi epi) {
+  constexpr int NT = WF * WT * 64;
+  constexpr int WFT = FT / WF, WTT = TT / WT;
+  constexpr int FM = WFT / 32, TM = WTT / 32;
+  constexpr int WL = FT * 8 / NT, XL = TT * 8 / NT;
+  constexpr int RSTEP = NT / 8;
+  constexpr int NMF = FM * TM, NRD = FM + TM, NLD = WL + XL;
+  static_assert(FM >= 1 && TM >= 1, "wave tile must be at least 32x32");
+  static_assert(WL * NT == FT * 8 && XL * NT == TT * 8, "loader coverage");
+  static_assert(RSTEP % 16 == 0, "loader passes must keep the LDS swizzle phase");
+
+  __shared__ f16x8 sW[2][FT * 8];
+  __shared__ f16x8 sX[2][TT * 8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wf = wave / WT, wt = wave - wf * WT;
+  const int nft = (N + FT - 1) / FT, ntt = (T + TT - 1) / TT;
+  const int tile = xcd_remap(blockIdx.x, nft * ntt);
+  const int ft = tile / ntt, tt = tile - ft * ntt;
+  const int f_base = ft * FT, t_base = tt * TT;
+
+  const int r0 = tid >> 3, c0 = tid & 7;
+  const int ldst = r0 * 8 + (c0 ^ lds_swz(r0));
+  const f16* wb = W + c0 * 8;
+  const f16* xb = X + c0 * 8;
+  int woff[WL], xoff[XL];
+#pragma unroll
+  for (int i = 0; i < WL; ++i) woff[i] = min(f_base + r0 + RSTEP * i, N - 1) * K;
+#pragma unroll
+  for (int i = 0; i < XL; ++i) xoff[i] = min(t_base + r0 + RSTEP * i, T - 1) * K;
+
+  f16x8 wreg[WL], xreg[XL];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < WL; ++i) wreg[i] = *(const f16x8*)(wb + woff[i] + k0);
+#pragma unroll
+    for (int i = 0; i < XL; ++i) xreg[i] = *(const f16x8*)(xb + xoff[i] + k0);
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < WL; ++i) sW[buf][ldst + RSTEP * 8 * i] = wreg[i];
+#pragma unroll
+    for (int i = 0; i < XL; ++i) sX[buf][ldst + RSTEP * 8 * i] = xreg[i];
+  };
+
+  f32x16 acc[FM][TM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
+
+  const int khalf = lane >> 5;
+  const int arow = wf * WFT + (lane & 31), brow = wt * WTT + (lane & 31);
+  const int aswz = lds_swz(arow), bswz = lds_swz(brow);
+  struct Frag {
+    f16x8 a[FM], b[TM];
+  };
+  auto fread = [&](Frag& F, int buf, int ks) {
+    const int c = ks * 2 + khalf;
+    const int aoff = arow * 8 + (c ^ aswz), boff = brow * 8 + (c ^ bswz);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) F.a[i] = sW[buf][aoff + i * 256];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) F.b[j] = sX[buf][boff + j * 256];
+  };
+  auto mfmas = [&](const Frag& F) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
+  };
+
+  const int nk = K / 64;
+  gload(0);
+  sstore(0);
+  lds_barrier();
+  Frag F0, F1;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    gload(min(kt + 1, nk - 1) * 64);
+    fread(F0, cur, 0);
+    fread(F1, cur, 1);
+    mfmas(F0);
+    fread(F0, cur, 2);
+    mfmas(F1);
+    fread(F1, cur, 3);
+    mfmas(F0);
+    mfmas(F1);
+    sstore(cur ^ 1);
+    // schedule: loads, step-0 reads, then MFMA/read pairs, then MFMA/write pairs
+    __builtin_amdgcn_sched_group_barrier(0x020, NLD, 0);  // VMEM read
+    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // DS read (step 0)
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+#pragma unroll
+      for (int m = 0; m < NMF; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
+        if (m < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NMF; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // MFMA
+      if (m < NLD) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+    }
+    lds_barrier();
+  }
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int t = t_base + wt * WTT + j * 32 + (lane & 31);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int f = f_base + wf * WFT + i * 32 + 8 * g + 4 * khalf;
+        if (t < T && f < N) {
+          f32x4 v;
+          v.x = acc[i][j][4 * g + 0];
+          v.y = acc[i][j][4 * g + 1];
+          v.z = acc[i][j][4 * g + 2];
+          v.w = acc[i][j][4 * g + 3];
+          epi(t, f, v);
+        }
+      }
+    }
+}
+
+}  // namespace hb
