@@ -152,7 +152,7 @@ def main():
         f"{achieved:.1f} TFLOP/s ({achieved/2500*100:.1f}% of dense fp16 peak)")
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": 2500.0, "unit": "TFLOP/s",
                 "frac": round(achieved / 2500.0, 4), "traffic": None,
-                "kernel": "gemm_nt_kernel<256,128,2,2,EpiSwiGLU>",
+                "kernel": "gemm_nt_kernel<256,256,4,2,EpiSwiGLU>",
                 "flop_per_launch": up_flops, "us_per_launch": round(up_ms * 1e3, 2)}
 
     extra = {}

@@ -112,6 +112,9 @@ int hb_ctx_synchronize(hb_ctx* ctx);
  * kv_dim == kv_heads*hd; heads % kv_heads == 0; dtype == HB_DTYPE_F16.
  */
 int hb_model_create(hb_ctx* ctx, const hb_model_config* cfg, int dtype, hb_model** out);
+/* The same validation without a device: fills the defaulted fields of *cfg in
+ * place and returns HB_OK or HB_E_CONFIG. */
+int hb_config_validate(hb_model_config* cfg);
 int hb_model_destroy(hb_model* model);
 /* The effective config (defaults filled in). */
 int hb_model_get_config(const hb_model* model, hb_model_config* out);

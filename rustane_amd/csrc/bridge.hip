@@ -445,6 +445,17 @@ extern "C" int hb_ctx_synchronize(hb_ctx* c) {
 // ---------------------------------------------------------------------------
 // model
 // ---------------------------------------------------------------------------
+extern "C" int hb_config_validate(hb_model_config* c) {
+  HB_INJECT_CHECK();
+  if (!c) return fail(HB_E_INVALID, "null config");
+  if (c->rope_theta == 0.f) c->rope_theta = 10000.0f;
+  if (c->norm_eps == 0.f) c->norm_eps = 1e-5f;
+  if (c->residual_alpha == 0.f && c->nlayers > 0)
+    c->residual_alpha = 1.0f / sqrtf(2.0f * (float)c->nlayers);
+  if (!(c->softcap >= 0.f)) return fail(HB_E_CONFIG, "softcap must be >= 0");
+  return validate_config(*c);
+}
+
 extern "C" int hb_model_create(hb_ctx* ctx, const hb_model_config* cfg_in, int dtype,
                                hb_model** out) {
   HB_INJECT_CHECK();
@@ -452,11 +463,7 @@ extern "C" int hb_model_create(hb_ctx* ctx, const hb_model_config* cfg_in, int d
   *out = nullptr;
   if (dtype != HB_DTYPE_F16) return fail(HB_E_CONFIG, "unsupported dtype %d", dtype);
   hb_model_config c = *cfg_in;
-  if (c.rope_theta == 0.f) c.rope_theta = 10000.0f;
-  if (c.norm_eps == 0.f) c.norm_eps = 1e-5f;
-  if (c.residual_alpha == 0.f && c.nlayers > 0)
-    c.residual_alpha = 1.0f / sqrtf(2.0f * (float)c.nlayers);
-  TRY(validate_config(c));
+  TRY(hb_config_validate(&c));
   DeviceGuard g(ctx->device);
 
   const size_t d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden, V = c.vocab;

@@ -86,6 +86,7 @@ SIGNATURES = {
     "hb_ctx_synchronize": [_P],
     "hb_model_create": [_P, C.POINTER(hb_model_config), _I, C.POINTER(_P)],
     "hb_model_destroy": [_P],
+    "hb_config_validate": [C.POINTER(hb_model_config)],
     "hb_model_get_config": [_P, C.POINTER(hb_model_config)],
     "hb_model_weight_bytes": [_P, C.POINTER(C.c_uint64)],
     "hb_model_set_softcap": [_P, _F],
