@@ -69,6 +69,8 @@ def main():
     ap.add_argument("--decode-b16", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the dominant kernel (timed) and a 1 GiB device copy, for counter runs")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -106,6 +108,17 @@ def main():
         hb.call("hb_forward_device", k.model.handle, d_tok.data_ptr(), d_tgt.data_ptr(), B, S,
                 d_loss.data_ptr(), None, d_mean.data_ptr())
 
+    if args.kernel_only:
+        # Reference transfer of known size (read 1 GiB + write 1 GiB) for scaling
+        # the FETCH_SIZE / WRITE_SIZE counters, then the dominant kernel alone.
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        roofline, _ = time_dominant_kernel(k, cfg, B * S, args.kernel_launches, stream)
+        print(json.dumps({"kernel_only": roofline}), flush=True)
+        return
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -128,32 +141,7 @@ def main():
         f"{tok_s:,.0f} tok/s, {flops/(ms_wall/1e3)/1e12:.1f} TFLOP/s, loss {loss:.4f} "
         f"(ln V = {math.log(cfg.vocab):.4f})")
 
-    # ---- dominant kernel alone: FFN up GEMM (W1|W3 + SwiGLU epilogue) ----
-    T = B * S
-    xn = (torch.randn(T, cfg.dim, device="cuda") * 0.5).to(torch.float16)
-    gate = torch.empty(T, cfg.hidden, dtype=torch.float16, device="cuda")
-
-    def up():
-        hb.call("hb_op_ffn_up", k.model.handle, 0, xn.data_ptr(), T, gate.data_ptr(), None)
-
-    for _ in range(5):
-        up()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.kernel_launches):
-        up()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    up_ms = e0.elapsed_time(e1) / args.kernel_launches
-    up_flops = 2.0 * T * (2 * cfg.hidden) * cfg.dim
-    achieved = up_flops / (up_ms / 1e3) / 1e12
-    log(f"[bench] ffn-up GEMM {T}x{2*cfg.hidden}x{cfg.dim}: {up_ms*1e3:.1f} us/launch, "
-        f"{achieved:.1f} TFLOP/s ({achieved/2500*100:.1f}% of dense fp16 peak)")
-    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": 2500.0, "unit": "TFLOP/s",
-                "frac": round(achieved / 2500.0, 4), "traffic": None,
-                "kernel": "gemm_nt_kernel<256,256,4,2,EpiSwiGLU>",
-                "flop_per_launch": up_flops, "us_per_launch": round(up_ms * 1e3, 2)}
+    roofline, _ = time_dominant_kernel(k, cfg, B * S, args.kernel_launches, stream)
 
     extra = {}
     # ---- batch 8 prefill ----
@@ -242,6 +230,51 @@ def main():
     if "cpu_baseline" in extra:
         line["cpu_baseline"] = extra["cpu_baseline"]
     print(json.dumps(line), flush=True)
+
+
+# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs of
+# `bench.py --kernel-only` (FETCH_SIZE, then WRITE_SIZE), each scaled by the
+# counter's reading for the 1 GiB reference copy in the same run (FETCH_SIZE
+# reads 0.5x the copied bytes, WRITE_SIZE 1.0x): 2 * 106599 KiB + 11405 KiB.
+# Algorithmic bytes of one launch: W1|W3 180.4 MB + X 4.2 MB read, gate 11.3 MB
+# written = 195.8 MB.
+DOMINANT_TRAFFIC_BYTES = 229_993_472
+
+
+def time_dominant_kernel(k, cfg, T, launches, stream):
+    """The FFN up-projection GEMM (W1|W3 with the SwiGLU epilogue, one launch)
+    on layer 0 at T tokens, timed with HIP events on the stream it runs on."""
+    import torch
+    from rustane_amd import hip_bridge as hb
+    xn = (torch.randn(T, cfg.dim, device="cuda") * 0.5).to(torch.float16)
+    gate = torch.empty(T, cfg.hidden, dtype=torch.float16, device="cuda")
+
+    def up():
+        hb.call("hb_op_ffn_up", k.model.handle, 0, xn.data_ptr(), T, gate.data_ptr(), None)
+
+    for _ in range(5):
+        up()
+    torch.cuda.synchronize()
+    # One event pair per launch on the kernel's own stream: each interval is the
+    # kernel's duration (host launch gaps between launches are excluded).
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(launches)]
+    for a, b in evs:
+        a.record(stream)
+        up()
+        b.record(stream)
+    torch.cuda.synchronize()
+    durs = sorted(a.elapsed_time(b) for a, b in evs)
+    up_ms = float(np.mean(durs))
+    up_flops = 2.0 * T * (2 * cfg.hidden) * cfg.dim
+    achieved = up_flops / (up_ms / 1e3) / 1e12
+    log(f"[bench] ffn-up GEMM {T}x{2*cfg.hidden}x{cfg.dim}: {up_ms*1e3:.1f} us/launch, "
+        f"{achieved:.1f} TFLOP/s ({achieved/2500*100:.1f}% of dense fp16 peak)")
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                "frac": round(achieved / 2500.0, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
+                "kernel": "gemm_nt_kernel<256,256,4,2,EpiSwiGLU> (FFN up, W1|W3 + SwiGLU)",
+                "flop_per_launch": up_flops, "us_per_launch": round(up_ms * 1e3, 2)}
+    return roofline, up_ms
 
 
 def cpu_baseline(cfg, S):
