@@ -255,17 +255,22 @@ def time_dominant_kernel(k, cfg, T, launches, stream):
     for _ in range(5):
         up()
     torch.cuda.synchronize()
-    # One event pair per launch on the kernel's own stream: each interval is the
-    # kernel's duration (host launch gaps between launches are excluded).
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(launches)]
-    for a, b in evs:
-        a.record(stream)
-        up()
-        b.record(stream)
+    # The launches are captured into one HIP graph on the kernel's own stream and
+    # the replay is timed with HIP events on that stream, so host dispatch gaps
+    # between launches do not count against the kernel.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(launches):
+            up()
+    graph.replay()
     torch.cuda.synchronize()
-    durs = sorted(a.elapsed_time(b) for a, b in evs)
-    up_ms = float(np.mean(durs))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    up_ms = e0.elapsed_time(e1) / launches
+    del graph
     up_flops = 2.0 * T * (2 * cfg.hidden) * cfg.dim
     achieved = up_flops / (up_ms / 1e3) / 1e12
     log(f"[bench] ffn-up GEMM {T}x{2*cfg.hidden}x{cfg.dim}: {up_ms*1e3:.1f} us/launch, "

@@ -122,124 +122,176 @@ hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-// ---- decode: split the context into 256-key chunks ------------------------------
-// Grid (chunk, head, sequence), 4 waves. hd/8 lanes cooperate on one key row
-// (16-byte loads; a wave instruction covers 64*16 B of consecutive key rows).
-// Each chunk writes its own (max, sum) and unnormalised output; a second kernel
-// merges the chunks of a head. Chunks past the current position exit at once,
-// so the launch shape does not depend on the position (graph-replayable).
-constexpr int DCHUNK = 256;
+// ---- decode: split the context into 128-key chunks ------------------------------
+// Grid (chunk, head, sequence), 4 waves per chunk, 32 keys per wave. hd/8 lanes
+// share one key row (16-byte loads; one wave instruction reads 1 KB of
+// consecutive key rows). Each lane issues all of its K and V loads before
+// using any (V does not depend on the scores), each wave keeps its own online
+// softmax state, and the four waves merge through LDS: there is no block-wide
+// barrier between the score and value passes. Chunks past the current position
+// exit at once, so the launch shape does not depend on the position (one HIP
+// graph replays every step). The last workgroup of a head to finish (atomic
+// ticket) merges the chunk partials into the output, so no separate combine
+// launch is needed. The partials travel through device-coherent (agent-scope)
+// stores and loads instead of a device-scope fence: on gfx950 such a fence is
+// an L2 write-back that costs more than the whole attention pass.
+constexpr int DCHUNK = 128;
 
 int attn_decode_chunks(int ctx_max) { return (ctx_max + DCHUNK - 1) / DCHUNK; }
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecode p) {
-  constexpr int LPK = HD / 8;    // lanes per key
-  constexpr int KPW = 64 / LPK;  // keys per wave instruction
-  constexpr int KPI = 4 * KPW;   // keys per block iteration
-  __shared__ float sc[DCHUNK];
-  __shared__ float red[4];
-  __shared__ float oacc[4][HD];
+  constexpr int LPK = HD / 8;        // lanes per key row
+  constexpr int KPW = 64 / LPK;      // keys per wave instruction
+  constexpr int WKEYS = DCHUNK / 4;  // keys per wave
+  constexpr int NIT = WKEYS / KPW;
+  __shared__ float s_m[4], s_l[4];
+  __shared__ float s_o[4][HD];
+  __shared__ int s_ticket;
 
   const int pos = *p.d_pos;
   const int c0 = blockIdx.x * DCHUNK;
   if (c0 > pos) return;
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (p.H / p.KVH);
-  const int nch = gridDim.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane / LPK, j = lane % LPK;
-  const int nkeys = min(DCHUNK, pos + 1 - c0);
 
   const f16x8 qv = *(const f16x8*)(p.q + ((size_t)b * p.H + h) * HD + 8 * j);
   float qf[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) qf[i] = (float)qv[i];
-  const f16* kb = p.k + b * p.bstride + kvh * p.hstride;
-  const f16* vb = p.v + b * p.bstride + kvh * p.hstride;
+  const f16* kb = p.k + b * p.bstride + kvh * p.hstride + 8 * j;
+  const f16* vb = p.v + b * p.bstride + kvh * p.hstride + 8 * j;
   const float sl2 = p.scale * HB_LOG2E;
 
-  for (int it = 0; it < DCHUNK; it += KPI) {
-    const int kk = it + wave * KPW + g;
-    float d = 0.f;
-    if (kk < nkeys) {
-      const f16x8 kv = *(const f16x8*)(kb + (size_t)(c0 + kk) * HD + 8 * j);
+  const int kbase = c0 + wave * WKEYS + g;
+  f16x8 kr[NIT], vr[NIT];
+  const f16x8 zero8 = {};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d += qf[i] * (float)kv[i];
-    }
+  for (int i = 0; i < NIT; ++i) {
+    const int kk = kbase + i * KPW;
+    kr[i] = kk <= pos ? *(const f16x8*)(kb + (size_t)kk * HD) : zero8;
+  }
+#pragma unroll
+  for (int i = 0; i < NIT; ++i) {
+    const int kk = kbase + i * KPW;
+    vr[i] = kk <= pos ? *(const f16x8*)(vb + (size_t)kk * HD) : zero8;
+  }
+  float sc[NIT];
+#pragma unroll
+  for (int i = 0; i < NIT; ++i) {
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d += qf[e] * (float)kr[i][e];
 #pragma unroll
     for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-    if (j == 0) sc[kk] = kk < nkeys ? d * sl2 : -INFINITY;
+    sc[i] = (kbase + i * KPW <= pos) ? d * sl2 : -INFINITY;
   }
-  __syncthreads();
-  float m = -INFINITY;
-  for (int i = tid; i < DCHUNK; i += 256) m = fmaxf(m, sc[i]);
-  m = block_max<4>(m, red);
-  float l = 0.f;
-  for (int i = tid; i < DCHUNK; i += 256) {
-    const float e = exp2f(sc[i] - m);
-    sc[i] = e;
-    l += e;
-  }
-  l = block_sum<4>(l, red);  // contains the barrier that publishes sc[]
-
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int it = 0; it < DCHUNK; it += KPI) {
-    const int kk = it + wave * KPW + g;
-    if (kk < nkeys) {
-      const float pk = sc[kk];
-      const f16x8 vv = *(const f16x8*)(vb + (size_t)(c0 + kk) * HD + 8 * j);
+  // wave-wide max over its keys (lanes of a group hold equal scores)
+  float m = sc[0];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += pk * (float)vv[i];
+  for (int i = 1; i < NIT; ++i) m = fmaxf(m, sc[i]);
+#pragma unroll
+  for (int o = LPK; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float l = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      const float pk = exp2f(sc[i] - m);
+      l += pk;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += pk * (float)vr[i][e];
     }
   }
 #pragma unroll
-  for (int o = LPK; o < 64; o <<= 1)
+  for (int o = LPK; o < 64; o <<= 1) {
+    l += __shfl_xor(l, o, 64);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += __shfl_xor(acc[i], o, 64);
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+  }
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
+  }
   if (g == 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) oacc[wave][8 * j + i] = acc[i];
+    for (int e = 0; e < 8; ++e) s_o[wave][8 * j + e] = acc[e];
   }
   __syncthreads();
-  const size_t slot = ((size_t)b * p.H + h) * nch + blockIdx.x;
+  float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  float w[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) w[v] = s_m[v] == -INFINITY ? 0.f : exp2f(s_m[v] - M);
+  const int nch = gridDim.x;
+  const size_t head = (size_t)b * p.H + h;
+  const size_t slot = head * nch + blockIdx.x;
+  // Partials are written with agent-scope (device-coherent) stores, so once
+  // they have completed they are visible to every XCD without an L2
+  // write-back; the workgroup barrier below waits for that completion.
   for (int e = tid; e < HD; e += 256)
-    p.part_o[slot * HD + e] = oacc[0][e] + oacc[1][e] + oacc[2][e] + oacc[3][e];
+    __hip_atomic_store(p.part_o + slot * HD + e,
+                       w[0] * s_o[0][e] + w[1] * s_o[1][e] + w[2] * s_o[2][e] + w[3] * s_o[3][e],
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (tid == 0) {
-    p.part_ml[slot * 2] = m;
-    p.part_ml[slot * 2 + 1] = l;
+    __hip_atomic_store(p.part_ml + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.part_ml + slot * 2 + 1,
+                       w[0] * s_l[0] + w[1] * s_l[1] + w[2] * s_l[2] + w[3] * s_l[3],
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
 
-template <int HD>
-__global__ __launch_bounds__(HD) void attn_decode_combine_kernel(AttnDecode p, int nch) {
-  const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
-  const int pos = *p.d_pos;
+  // The last chunk of this head to finish merges all chunks (its reads are
+  // agent-scope loads of the coherent partials). atomicInc wraps the counter
+  // back to 0 after the last arrival, ready for the next launch.
   const int nvalid = pos / DCHUNK + 1;
-  const size_t base = ((size_t)b * p.H + h) * nch;
-  float M = -INFINITY;
-  for (int c = 0; c < nvalid; ++c) M = fmaxf(M, p.part_ml[(base + c) * 2]);
-  float L = 0.f, O = 0.f;
-  for (int c = 0; c < nvalid; ++c) {
-    const float w = exp2f(p.part_ml[(base + c) * 2] - M);
-    L += w * p.part_ml[(base + c) * 2 + 1];
-    O += w * p.part_o[(base + c) * HD + e];
+  __syncthreads();
+  if (tid == 0)
+    s_ticket = (int)__builtin_amdgcn_atomic_inc32(p.counters + head, (unsigned)(nvalid - 1),
+                                                  __ATOMIC_RELAXED, "agent");
+  __syncthreads();
+  if (s_ticket != nvalid - 1) return;
+  // Merge in groups of MCH chunks: all threads load a group's partials into LDS
+  // at once (independent loads, one memory latency per group), then each
+  // output dimension folds the group into a running (max, sum, out) state.
+  constexpr int MCH = 32;
+  __shared__ float s_cml[MCH][2];
+  __shared__ float s_co[MCH][HD];
+  auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  const float* pml = p.part_ml + head * nch * 2;
+  const float* pso = p.part_o + head * nch * HD;
+  float Mx = -INFINITY, L = 0.f, O = 0.f;
+  for (int g0 = 0; g0 < nvalid; g0 += MCH) {
+    const int cnt = min(MCH, nvalid - g0);
+    for (int i = tid; i < cnt * HD; i += 256) s_co[i / HD][i % HD] = ld(pso + (size_t)(g0 + i / HD) * HD + i % HD);
+    if (tid < 2 * cnt) s_cml[tid >> 1][tid & 1] = ld(pml + (size_t)g0 * 2 + tid);
+    __syncthreads();
+    if (tid < HD) {
+      float gm = Mx;
+      for (int c = 0; c < cnt; ++c) gm = fmaxf(gm, s_cml[c][0]);
+      const float r = exp2f(Mx - gm);  // Mx = -inf on the first group: r = 0
+      L *= r;
+      O *= r;
+      for (int c = 0; c < cnt; ++c) {
+        const float wc = exp2f(s_cml[c][0] - gm);
+        L += wc * s_cml[c][1];
+        O += wc * s_co[c][tid];
+      }
+      Mx = gm;
+    }
+    __syncthreads();
   }
-  p.out[(size_t)b * p.H * HD + h * HD + e] = (f16)(O / L);
+  if (tid < HD) p.out[head * HD + tid] = (f16)(O / L);
 }
 
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
   const int nch = attn_decode_chunks(p.ctx_max);
   dim3 grid(nch, p.H, p.B);
-  if (p.hd == 128) {
+  if (p.hd == 128)
     hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, p);
-    hipLaunchKernelGGL(attn_decode_combine_kernel<128>, dim3(p.H, p.B), dim3(128), 0, st, p, nch);
-  } else if (p.hd == 64) {
+  else if (p.hd == 64)
     hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, st, p);
-    hipLaunchKernelGGL(attn_decode_combine_kernel<64>, dim3(p.H, p.B), dim3(64), 0, st, p, nch);
-  } else {
+  else
     return hipErrorInvalidValue;
-  }
   return hipGetLastError();
 }
 

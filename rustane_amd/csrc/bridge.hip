@@ -119,6 +119,7 @@ struct hb_kv {
   int *d_pos = nullptr, *d_pos0 = nullptr;
   uint32_t *d_tok = nullptr, *d_next = nullptr, *d_hist = nullptr;
   float *x = nullptr, *x2 = nullptr, *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
+  unsigned* counters = nullptr;  // decode attention arrival tickets [B][H]
   f16 *xn = nullptr, *qd = nullptr, *attn = nullptr, *gate = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -925,7 +926,7 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
     a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
     a.ctx_max = kv->ctx_cap; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
-    a.part_ml = kv->part_ml; a.out = kv->attn;
+    a.part_ml = kv->part_ml; a.counters = kv->counters; a.out = kv->attn;
     HIP_TRY(attention_decode(a, st));
     HIP_TRY(gemv_residual(L.wo, kv->attn, c.dim, B, c.q_dim, EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
     HIP_TRY(rmsnorm(kv->x2, c.dim, L.g2, B, c.dim, c.norm_eps, kv->xn, nullptr, st));
@@ -1014,6 +1015,7 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   const size_t o_x = take(B * c.dim * 4), o_x2 = take(B * c.dim * 4);
   const size_t o_logits = take(B * c.vocab * 4);
   const size_t o_po = take(B * c.heads * kv->nch * c.hd * 4), o_pml = take(B * c.heads * kv->nch * 8);
+  const size_t o_cnt = take(B * c.heads * 4);
   const size_t o_xn = take(B * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(B * c.q_dim * 2);
   const size_t o_gate = take(B * c.hidden * 2);
   char* sb = nullptr;
@@ -1034,6 +1036,7 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   kv->logits = (float*)(sb + o_logits);
   kv->part_o = (float*)(sb + o_po);
   kv->part_ml = (float*)(sb + o_pml);
+  kv->counters = (unsigned*)(sb + o_cnt);
   kv->xn = (f16*)(sb + o_xn);
   kv->qd = (f16*)(sb + o_qd);
   kv->attn = (f16*)(sb + o_attn);

@@ -51,6 +51,7 @@ struct AttnDecode {
   float scale;
   float* part_o;   // [B][H][nchunks][hd]
   float* part_ml;  // [B][H][nchunks][2]
+  unsigned* counters;  // [B][H] arrival tickets, zero between launches
   f16* out;        // [B][H*hd]
 };
 int attn_decode_chunks(int ctx_max);

@@ -87,6 +87,7 @@ def m48(gpu):
     cfg = ModelConfig.llama_48m()
     w = ModelWeights.synthetic(cfg, seed=1234, std=0.02)
     k = CompiledKernels.compile(cfg)
+    k.ensure_weights(w)  # decode-only selections must not depend on a prior forward
     return cfg, w, k
 
 
