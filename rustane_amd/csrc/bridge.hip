@@ -76,6 +76,8 @@ struct LayerW {
   float* g1 = nullptr;
   float* g2 = nullptr;
   bool uploaded = false;
+  // decode copies of the four matrices in fragment-tiled order (gemv.hip)
+  f16 *t_wqkv = nullptr, *t_wo = nullptr, *t_w13 = nullptr, *t_w2 = nullptr;
 };
 
 // Prefill activations. Q/K/V^T rows are padded per sequence to S_pad (multiple
@@ -106,6 +108,12 @@ struct hb_model {
   size_t staging_floats = 0;
   Workspace ws;
   int graph_epoch = 0;  // bumped when a captured decode graph goes stale
+  // Decode copy of every matrix (fragment-tiled), allocated on first decode
+  // use and rebuilt from the row-major weights after any upload.
+  void* dbase = nullptr;
+  size_t dbytes = 0;
+  f16* t_embed = nullptr;
+  bool dec_stale = true;
 };
 
 struct hb_kv {
@@ -120,6 +128,7 @@ struct hb_kv {
   uint32_t *d_tok = nullptr, *d_next = nullptr, *d_hist = nullptr;
   float *x = nullptr, *x2 = nullptr, *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
   unsigned* counters = nullptr;  // decode attention arrival tickets [B][H]
+  unsigned* norm_counter = nullptr;  // arrival ticket of the GEMV RMSNorm tails
   f16 *xn = nullptr, *qd = nullptr, *attn = nullptr, *gate = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -262,6 +271,50 @@ bool weights_ready(hb_model* m) {
   for (auto& l : m->layers)
     if (!l.uploaded) return false;
   return true;
+}
+
+// The decode GEMVs read fragment-tiled copies of the weights. They cost one
+// more copy of the matrices in HBM (13.5 GB for the 7B shape) and are only
+// allocated once a decode path runs; an upload marks them stale and the next
+// decode call re-tiles on the stream, ahead of its own launches.
+int ensure_decode_weights(hb_model* m) {
+  const hb_model_config& c = m->cfg;
+  const size_t d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden, V = c.vocab;
+  if (!m->dbase) {
+    const size_t per_layer = align256((q + 2 * kv) * d * 2) + align256(d * q * 2) +
+                             align256(2 * h * d * 2) + align256(d * h * 2);
+    const size_t total = per_layer * c.nlayers + align256(V * d * 2);
+    HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
+    char* base = nullptr;
+    hipError_t e = hipMalloc(&base, total);
+    if (e != hipSuccess)
+      return fail(e == hipErrorOutOfMemory ? HB_E_OOM : HB_E_DEVICE,
+                  "decode weight copy of %zu bytes: %s", total, hipGetErrorString(e));
+    m->dbase = base;
+    m->dbytes = total;
+    size_t off = 0;
+    for (auto& L : m->layers) {
+      L.t_wqkv = (f16*)(base + off); off += align256((q + 2 * kv) * d * 2);
+      L.t_wo = (f16*)(base + off); off += align256(d * q * 2);
+      L.t_w13 = (f16*)(base + off); off += align256(2 * h * d * 2);
+      L.t_w2 = (f16*)(base + off); off += align256(d * h * 2);
+    }
+    m->t_embed = (f16*)(base + off);
+    m->dec_stale = true;
+    m->graph_epoch++;
+  }
+  if (m->dec_stale) {
+    hipStream_t st = m->ctx->stream();
+    for (auto& L : m->layers) {
+      HIP_TRY(tile_decode(L.wqkv, L.t_wqkv, (int)(q + 2 * kv), (int)d, st));
+      HIP_TRY(tile_decode(L.wo, L.t_wo, (int)d, (int)q, st));
+      HIP_TRY(tile_decode(L.w13, L.t_w13, (int)(2 * h), (int)d, st));
+      HIP_TRY(tile_decode(L.w2, L.t_w2, (int)d, (int)h, st));
+    }
+    HIP_TRY(tile_decode(m->embed, m->t_embed, (int)V, (int)d, st));
+    m->dec_stale = false;
+  }
+  return HB_OK;
 }
 
 // One transformer layer over T = B*S token rows (layer.rs:684-806 order).
@@ -513,6 +566,7 @@ extern "C" int hb_model_destroy(hb_model* m) {
   DeviceGuard g(m->device);
   (void)hipDeviceSynchronize();
   (void)hipFree(m->wbase);
+  if (m->dbase) (void)hipFree(m->dbase);
   if (m->rope) (void)hipFree(m->rope);
   if (m->staging) (void)hipFree(m->staging);
   if (m->ws.base) (void)hipFree(m->ws.base);
@@ -586,6 +640,7 @@ extern "C" int hb_model_upload_layer(hb_model* m, int layer, const float* wq, co
   TRY(upload_f32(m, g1, d, L.g1));
   TRY(upload_f32(m, g2, d, L.g2));
   L.uploaded = true;
+  m->dec_stale = true;
   return HB_OK;
 }
 
@@ -602,6 +657,7 @@ extern "C" int hb_model_upload_embed(hb_model* m, const float* embed, const floa
   }
   TRY(upload_f32(m, gamma_final, c.dim, m->gamma_f));
   m->embed_uploaded = true;
+  m->dec_stale = true;
   return HB_OK;
 }
 
@@ -646,6 +702,7 @@ extern "C" int hb_model_init_synthetic(hb_model* m, uint64_t seed, float std) {
   HIP_TRY(fill_f32(m->gamma_f, 1.0f, d, st));
   HIP_TRY(hipStreamSynchronize(st));
   m->embed_uploaded = true;
+  m->dec_stale = true;
   return HB_OK;
 }
 
@@ -910,31 +967,37 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
   const hb_model_config& c = m->cfg;
   const int B = kv->B;
   const float alpha = alpha_of(c);
-  HIP_TRY(embedding(m->embed, kv->d_tok, B, c.dim, c.vocab, kv->x, m->ctx->d_err, st));
+  // Five launches per layer: every RMSNorm runs inside the launch that
+  // produces its input (the embedding, then the tails of the two residual
+  // projections), and xn always holds the normalised input of the next GEMV.
+  HIP_TRY(embedding_norm(m->embed, kv->d_tok, B, c.dim, c.vocab, kv->x, m->layers[0].g1,
+                         c.norm_eps, kv->xn, m->ctx->d_err, st));
   for (int l = 0; l < c.nlayers; ++l) {
     const LayerW& L = m->layers[l];
     const KVTarget t = cache_target(kv, l);
-    HIP_TRY(rmsnorm(kv->x, c.dim, L.g1, B, c.dim, c.norm_eps, kv->xn, nullptr, st));
+    const float* g_next = l + 1 < c.nlayers ? m->layers[l + 1].g1 : m->gamma_f;
     EpiQKV e{};
     e.q_dim = c.q_dim; e.kv_dim = c.kv_dim; e.hd = c.hd; e.S = 1; e.heads = c.heads;
     e.kv_heads = c.kv_heads; e.rope = m->rope; e.d_pos = kv->d_pos; e.q = kv->qd; e.q_rows = 1;
     e.k = t.k; e.k_bstride = t.k_bstride; e.k_hstride = t.k_hstride;
     e.v = t.v; e.v_bstride = t.v_bstride; e.v_hstride = t.v_hstride; e.vt = nullptr; e.vt_ld = 0;
     e.tap = nullptr;
-    HIP_TRY(gemv_qkv(L.wqkv, kv->xn, c.q_dim + 2 * c.kv_dim, B, c.dim, e, st));
+    HIP_TRY(gemv_qkv(L.t_wqkv, kv->xn, c.q_dim + 2 * c.kv_dim, B, c.dim, e, st));
     AttnDecode a{};
     a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
     a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
     a.ctx_max = kv->ctx_cap; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
     a.part_ml = kv->part_ml; a.counters = kv->counters; a.out = kv->attn;
     HIP_TRY(attention_decode(a, st));
-    HIP_TRY(gemv_residual(L.wo, kv->attn, c.dim, B, c.q_dim, EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
-    HIP_TRY(rmsnorm(kv->x2, c.dim, L.g2, B, c.dim, c.norm_eps, kv->xn, nullptr, st));
-    HIP_TRY(gemv_swiglu(L.w13, kv->xn, 2 * c.hidden, B, c.dim, EpiSwiGLU{kv->gate, nullptr, c.hidden}, st));
-    HIP_TRY(gemv_residual(L.w2, kv->gate, c.dim, B, c.hidden, EpiResidual{kv->x2, kv->x, c.dim, alpha}, st));
+    HIP_TRY(gemv_residual_norm(L.t_wo, kv->attn, c.dim, B, c.q_dim,
+                               EpiResidual{kv->x, kv->x2, c.dim, alpha},
+                               NormTail{kv->x2, L.g2, c.norm_eps, kv->xn, kv->norm_counter}, st));
+    HIP_TRY(gemv_swiglu(L.t_w13, kv->xn, 2 * c.hidden, B, c.dim, EpiSwiGLU{kv->gate, nullptr, c.hidden}, st));
+    HIP_TRY(gemv_residual_norm(L.t_w2, kv->gate, c.dim, B, c.hidden,
+                               EpiResidual{kv->x2, kv->x, c.dim, alpha},
+                               NormTail{kv->x, g_next, c.norm_eps, kv->xn, kv->norm_counter}, st));
   }
-  HIP_TRY(rmsnorm(kv->x, c.dim, m->gamma_f, B, c.dim, c.norm_eps, kv->xn, nullptr, st));
-  HIP_TRY(gemv_logits(m->embed, kv->xn, c.vocab, B, c.dim, EpiLogits{kv->logits, c.vocab, c.softcap}, st));
+  HIP_TRY(gemv_logits(m->t_embed, kv->xn, c.vocab, B, c.dim, EpiLogits{kv->logits, c.vocab, c.softcap}, st));
   HIP_TRY(cross_entropy(kv->logits, nullptr, B, c.vocab, nullptr, kv->d_next, nullptr, st));
   HIP_TRY(decode_advance(kv->d_next, kv->d_tok, kv->d_hist, kv->d_pos, kv->d_pos0, B, st));
   return HB_OK;
@@ -1015,7 +1078,7 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   const size_t o_x = take(B * c.dim * 4), o_x2 = take(B * c.dim * 4);
   const size_t o_logits = take(B * c.vocab * 4);
   const size_t o_po = take(B * c.heads * kv->nch * c.hd * 4), o_pml = take(B * c.heads * kv->nch * 8);
-  const size_t o_cnt = take(B * c.heads * 4);
+  const size_t o_cnt = take(B * c.heads * 4), o_ncnt = take(4);
   const size_t o_xn = take(B * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(B * c.q_dim * 2);
   const size_t o_gate = take(B * c.hidden * 2);
   char* sb = nullptr;
@@ -1037,6 +1100,7 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   kv->part_o = (float*)(sb + o_po);
   kv->part_ml = (float*)(sb + o_pml);
   kv->counters = (unsigned*)(sb + o_cnt);
+  kv->norm_counter = (unsigned*)(sb + o_ncnt);
   kv->xn = (f16*)(sb + o_xn);
   kv->qd = (f16*)(sb + o_qd);
   kv->attn = (f16*)(sb + o_attn);
@@ -1106,6 +1170,7 @@ extern "C" int hb_prefill(hb_model* m, hb_kv* kv, const uint32_t* tokens, int S,
   TRY(check_ids(tokens, T, c.vocab, "tokens"));
   TRY(ensure_rope(m, kv->ctx_cap));
   TRY(ensure_workspace(m, T, (long)B * S_pad_of(S)));
+  TRY(ensure_decode_weights(m));
   Workspace& w = m->ws;
   hipStream_t st = m->ctx->stream();
   HIP_TRY(hipMemcpyAsync(w.tok, tokens, T * 4, hipMemcpyHostToDevice, st));
@@ -1114,7 +1179,7 @@ extern "C" int hb_prefill(hb_model* m, hb_kv* kv, const uint32_t* tokens, int S,
   // Last position of each sequence -> logits and greedy token.
   HIP_TRY(rmsnorm(w.x + (size_t)(S - 1) * c.dim, (long)S * c.dim, m->gamma_f, B, c.dim, c.norm_eps,
                   kv->xn, nullptr, st));
-  HIP_TRY(gemv_logits(m->embed, kv->xn, c.vocab, B, c.dim, EpiLogits{kv->logits, c.vocab, c.softcap}, st));
+  HIP_TRY(gemv_logits(m->t_embed, kv->xn, c.vocab, B, c.dim, EpiLogits{kv->logits, c.vocab, c.softcap}, st));
   HIP_TRY(cross_entropy(kv->logits, nullptr, B, c.vocab, nullptr, kv->d_next, nullptr, st));
   HIP_TRY(set_int(kv->d_pos, S, st));
   if (h_logits) HIP_TRY(hipMemcpyAsync(h_logits, kv->logits, (size_t)B * c.vocab * 4, hipMemcpyDeviceToHost, st));
@@ -1135,6 +1200,7 @@ extern "C" int hb_decode_step(hb_model* m, hb_kv* kv, const uint32_t* tokens, fl
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
   TRY(check_ids(tokens, kv->B, c.vocab, "tokens"));
+  TRY(ensure_decode_weights(m));
   hipStream_t st = m->ctx->stream();
   HIP_TRY(hipMemcpyAsync(kv->d_tok, tokens, (size_t)kv->B * 4, hipMemcpyHostToDevice, st));
   HIP_TRY(set_int(kv->d_pos0, kv->len, st));
@@ -1158,6 +1224,7 @@ extern "C" int hb_decode_greedy(hb_model* m, hb_kv* kv, const uint32_t* first, i
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
   TRY(check_ids(first, kv->B, c.vocab, "first tokens"));
+  TRY(ensure_decode_weights(m));
   hipStream_t st = m->ctx->stream();
   HIP_TRY(hipMemcpyAsync(kv->d_tok, first, (size_t)kv->B * 4, hipMemcpyHostToDevice, st));
   HIP_TRY(set_int(kv->d_pos0, kv->len, st));

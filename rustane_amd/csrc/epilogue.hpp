@@ -35,6 +35,22 @@ struct EpiResidual {
   }
 };
 
+// EpiResidual whose stores are device-coherent (agent scope): another
+// workgroup of the same launch, on any XCD, can read the rows back with
+// agent-scope loads once this workgroup's stores have completed.
+struct EpiResidualCoherent {
+  EpiResidual e;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    const size_t o = (size_t)t * e.ld + f0;
+    const f32x4 r = *(const f32x4*)(e.res + o);
+    float* p = e.out + o;
+    __hip_atomic_store(p, v.x * e.alpha + r.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 1, v.y * e.alpha + r.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 2, v.z * e.alpha + r.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 3, v.w * e.alpha + r.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+};
+
 // W1 and W3 are packed row-interleaved in groups of four: packed rows 4j..4j+3
 // are W1 column 2j, W1 column 2j+1, W3 column 2j, W3 column 2j+1. A lane's
 // 4 consecutive features are therefore (h1[u], h1[u+1], h3[u], h3[u+1]) with

@@ -17,15 +17,29 @@ hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQK
                     hipStream_t st);
 
 // ---- decode GEMV (gemv.hip): rows of X are the B <= 16 sequences ----
-hipError_t gemv_residual(const f16* W, const f16* X, int N, int B, int K, const EpiResidual& e,
+// W arguments are decode copies in fragment-tiled order (tile_decode); N is a
+// multiple of 16 and K of 32.
+hipError_t tile_decode(const f16* W, f16* Wt, int N, int K, hipStream_t st);
+// RMSNorm of the rows an epilogue just wrote, done by the launch's last
+// workgroup. counter is zero between launches (the ticket wraps back to 0).
+struct NormTail {
+  const float* x;  // [B, N] rows written by the epilogue (must be its output)
+  const float* gamma;
+  float eps;
+  f16* out;  // [B, N]
+  unsigned* counter;
+};
+hipError_t gemv_residual(const f16* Wt, const f16* X, int N, int B, int K, const EpiResidual& e,
                          hipStream_t st);
-hipError_t gemv_swiglu(const f16* W, const f16* X, int N, int B, int K, const EpiSwiGLU& e,
+hipError_t gemv_residual_norm(const f16* Wt, const f16* X, int N, int B, int K,
+                              const EpiResidual& e, const NormTail& nt, hipStream_t st);
+hipError_t gemv_swiglu(const f16* Wt, const f16* X, int N, int B, int K, const EpiSwiGLU& e,
                        hipStream_t st);
-hipError_t gemv_logits(const f16* W, const f16* X, int N, int B, int K, const EpiLogits& e,
+hipError_t gemv_logits(const f16* Wt, const f16* X, int N, int B, int K, const EpiLogits& e,
                        hipStream_t st);
-hipError_t gemv_qkv(const f16* W, const f16* X, int N, int B, int K, const EpiQKV& e,
+hipError_t gemv_qkv(const f16* Wt, const f16* X, int N, int B, int K, const EpiQKV& e,
                     hipStream_t st);
-hipError_t gemv_store(const f16* W, const f16* X, int N, int B, int K, float* C, hipStream_t st);
+hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st);
 
 // ---- attention (attention.hip) ----
 struct AttnPrefill {
@@ -60,6 +74,9 @@ hipError_t attention_decode(const AttnDecode& p, hipStream_t st);
 // ---- elementwise / reductions (elementwise.hip) ----
 hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
                      int* err, hipStream_t st);
+// embedding + RMSNorm of each row into xn (fp16) in the same launch.
+hipError_t embedding_norm(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
+                          const float* gamma, float eps, f16* xn, int* err, hipStream_t st);
 // Rows r < T of x at x + r*row_stride (floats), dim contiguous.
 hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
                    f16* out, float* rms_inv, hipStream_t st);
