@@ -128,7 +128,8 @@ struct hb_kv {
   uint32_t *d_tok = nullptr, *d_next = nullptr, *d_hist = nullptr;
   float *x = nullptr, *x2 = nullptr, *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
   unsigned* counters = nullptr;  // decode attention arrival tickets [B][H]
-  unsigned* norm_counter = nullptr;  // arrival ticket of the GEMV RMSNorm tails
+  float* amax_val = nullptr;  // greedy argmax partials [B][vocab/16]
+  int* amax_idx = nullptr;
   f16 *xn = nullptr, *qd = nullptr, *attn = nullptr, *gate = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -967,39 +968,46 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
   const hb_model_config& c = m->cfg;
   const int B = kv->B;
   const float alpha = alpha_of(c);
-  // Five launches per layer: every RMSNorm runs inside the launch that
-  // produces its input (the embedding, then the tails of the two residual
-  // projections), and xn always holds the normalised input of the next GEMV.
-  HIP_TRY(embedding_norm(m->embed, kv->d_tok, B, c.dim, c.vocab, kv->x, m->layers[0].g1,
-                         c.norm_eps, kv->xn, m->ctx->d_err, st));
+  // Every RMSNorm runs inside the GEMV that consumes it while the staged rows
+  // fit in LDS (B <= 3 at dim 4096): five launches per layer. Otherwise a
+  // separate rmsnorm launch writes xn before each of those GEMVs.
+  const bool fused = gemv_norm_fits(B, c.dim);
+  auto prep_norm = [&](const float* x, const float* gamma, NormIn& n) -> hipError_t {
+    n = NormIn{x, gamma, c.norm_eps};
+    return fused ? hipSuccess : rmsnorm(x, c.dim, gamma, B, c.dim, c.norm_eps, kv->xn, nullptr, st);
+  };
+  HIP_TRY(embedding(m->embed, kv->d_tok, B, c.dim, c.vocab, kv->x, m->ctx->d_err, st));
   for (int l = 0; l < c.nlayers; ++l) {
     const LayerW& L = m->layers[l];
     const KVTarget t = cache_target(kv, l);
-    const float* g_next = l + 1 < c.nlayers ? m->layers[l + 1].g1 : m->gamma_f;
+    NormIn n1, n2;
+    HIP_TRY(prep_norm(kv->x, L.g1, n1));
     EpiQKV e{};
     e.q_dim = c.q_dim; e.kv_dim = c.kv_dim; e.hd = c.hd; e.S = 1; e.heads = c.heads;
     e.kv_heads = c.kv_heads; e.rope = m->rope; e.d_pos = kv->d_pos; e.q = kv->qd; e.q_rows = 1;
     e.k = t.k; e.k_bstride = t.k_bstride; e.k_hstride = t.k_hstride;
     e.v = t.v; e.v_bstride = t.v_bstride; e.v_hstride = t.v_hstride; e.vt = nullptr; e.vt_ld = 0;
     e.tap = nullptr;
-    HIP_TRY(gemv_qkv(L.t_wqkv, kv->xn, c.q_dim + 2 * c.kv_dim, B, c.dim, e, st));
+    HIP_TRY(gemv_qkv(L.t_wqkv, kv->xn, fused ? &n1 : nullptr, c.q_dim + 2 * c.kv_dim, B, c.dim, e, st));
     AttnDecode a{};
     a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
     a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
     a.ctx_max = kv->ctx_cap; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
     a.part_ml = kv->part_ml; a.counters = kv->counters; a.out = kv->attn;
     HIP_TRY(attention_decode(a, st));
-    HIP_TRY(gemv_residual_norm(L.t_wo, kv->attn, c.dim, B, c.q_dim,
-                               EpiResidual{kv->x, kv->x2, c.dim, alpha},
-                               NormTail{kv->x2, L.g2, c.norm_eps, kv->xn, kv->norm_counter}, st));
-    HIP_TRY(gemv_swiglu(L.t_w13, kv->xn, 2 * c.hidden, B, c.dim, EpiSwiGLU{kv->gate, nullptr, c.hidden}, st));
-    HIP_TRY(gemv_residual_norm(L.t_w2, kv->gate, c.dim, B, c.hidden,
-                               EpiResidual{kv->x2, kv->x, c.dim, alpha},
-                               NormTail{kv->x, g_next, c.norm_eps, kv->xn, kv->norm_counter}, st));
+    HIP_TRY(gemv_residual(L.t_wo, kv->attn, c.dim, B, c.q_dim, EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
+    HIP_TRY(prep_norm(kv->x2, L.g2, n2));
+    HIP_TRY(gemv_swiglu(L.t_w13, kv->xn, fused ? &n2 : nullptr, 2 * c.hidden, B, c.dim, EpiSwiGLU{kv->gate, nullptr, c.hidden}, st));
+    HIP_TRY(gemv_residual(L.t_w2, kv->gate, c.dim, B, c.hidden, EpiResidual{kv->x2, kv->x, c.dim, alpha}, st));
   }
-  HIP_TRY(gemv_logits(m->t_embed, kv->xn, c.vocab, B, c.dim, EpiLogits{kv->logits, c.vocab, c.softcap}, st));
-  HIP_TRY(cross_entropy(kv->logits, nullptr, B, c.vocab, nullptr, kv->d_next, nullptr, st));
-  HIP_TRY(decode_advance(kv->d_next, kv->d_tok, kv->d_hist, kv->d_pos, kv->d_pos0, B, st));
+  NormIn nf;
+  HIP_TRY(prep_norm(kv->x, m->gamma_f, nf));
+  EpiLogits el{kv->logits, c.vocab, c.softcap};
+  el.part_val = kv->amax_val;
+  el.part_idx = kv->amax_idx;
+  HIP_TRY(gemv_logits(m->t_embed, kv->xn, fused ? &nf : nullptr, c.vocab, B, c.dim, el, st));
+  HIP_TRY(argmax_reduce(kv->amax_val, kv->amax_idx, c.vocab / 16, B, kv->d_next, kv->d_tok,
+                        kv->d_hist, kv->d_pos, kv->d_pos0, st));
   return HB_OK;
 }
 
@@ -1078,7 +1086,8 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   const size_t o_x = take(B * c.dim * 4), o_x2 = take(B * c.dim * 4);
   const size_t o_logits = take(B * c.vocab * 4);
   const size_t o_po = take(B * c.heads * kv->nch * c.hd * 4), o_pml = take(B * c.heads * kv->nch * 8);
-  const size_t o_cnt = take(B * c.heads * 4), o_ncnt = take(4);
+  const size_t o_cnt = take(B * c.heads * 4);
+  const size_t o_aval = take(B * (c.vocab / 16) * 4), o_aidx = take(B * (c.vocab / 16) * 4);
   const size_t o_xn = take(B * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(B * c.q_dim * 2);
   const size_t o_gate = take(B * c.hidden * 2);
   char* sb = nullptr;
@@ -1100,7 +1109,8 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   kv->part_o = (float*)(sb + o_po);
   kv->part_ml = (float*)(sb + o_pml);
   kv->counters = (unsigned*)(sb + o_cnt);
-  kv->norm_counter = (unsigned*)(sb + o_ncnt);
+  kv->amax_val = (float*)(sb + o_aval);
+  kv->amax_idx = (int*)(sb + o_aidx);
   kv->xn = (f16*)(sb + o_xn);
   kv->qd = (f16*)(sb + o_qd);
   kv->attn = (f16*)(sb + o_attn);
@@ -1179,8 +1189,12 @@ extern "C" int hb_prefill(hb_model* m, hb_kv* kv, const uint32_t* tokens, int S,
   // Last position of each sequence -> logits and greedy token.
   HIP_TRY(rmsnorm(w.x + (size_t)(S - 1) * c.dim, (long)S * c.dim, m->gamma_f, B, c.dim, c.norm_eps,
                   kv->xn, nullptr, st));
-  HIP_TRY(gemv_logits(m->t_embed, kv->xn, c.vocab, B, c.dim, EpiLogits{kv->logits, c.vocab, c.softcap}, st));
-  HIP_TRY(cross_entropy(kv->logits, nullptr, B, c.vocab, nullptr, kv->d_next, nullptr, st));
+  EpiLogits el{kv->logits, c.vocab, c.softcap};
+  el.part_val = kv->amax_val;
+  el.part_idx = kv->amax_idx;
+  HIP_TRY(gemv_logits(m->t_embed, kv->xn, nullptr, c.vocab, B, c.dim, el, st));
+  HIP_TRY(argmax_reduce(kv->amax_val, kv->amax_idx, c.vocab / 16, B, kv->d_next, nullptr, nullptr,
+                        nullptr, nullptr, st));
   HIP_TRY(set_int(kv->d_pos, S, st));
   if (h_logits) HIP_TRY(hipMemcpyAsync(h_logits, kv->logits, (size_t)B * c.vocab * 4, hipMemcpyDeviceToHost, st));
   if (h_next) HIP_TRY(hipMemcpyAsync(h_next, kv->d_next, (size_t)B * 4, hipMemcpyDeviceToHost, st));

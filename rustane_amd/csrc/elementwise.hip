@@ -6,30 +6,20 @@
 namespace hb {
 
 // ---- embedding (cpu/embedding.rs:8-16): x[t,:] = E[tok[t],:] -------------------
-// With NORM the same workgroup also writes the RMSNorm of the row
-// (cpu/rmsnorm.rs:149-183) into xn: the decode step's first norm needs no
-// launch of its own.
-template <bool NORM>
 __global__ __launch_bounds__(256) void embedding_kernel(const f16* __restrict__ E,
                                                         const uint32_t* __restrict__ tok, int dim,
                                                         int vocab, float* __restrict__ x,
-                                                        const float* __restrict__ gamma, float eps,
-                                                        f16* __restrict__ xn, int* err) {
-  __shared__ float red[4];
+                                                        int* err) {
   const int t = blockIdx.x;
   const uint32_t id = tok[t];
   float* xr = x + (size_t)t * dim;
   if (id >= (uint32_t)vocab) {
     // Never read outside E; report through the error word.
-    for (int c = threadIdx.x * 4; c < dim; c += 256 * 4) {
-      *(f32x4*)(xr + c) = f32x4{};
-      if (NORM) *(f16x4*)(xn + (size_t)t * dim + c) = f16x4{};
-    }
+    for (int c = threadIdx.x * 4; c < dim; c += 256 * 4) *(f32x4*)(xr + c) = f32x4{};
     if (threadIdx.x == 0 && err) atomicOr(err, 1);
     return;
   }
   const f16* er = E + (size_t)id * dim;
-  float ss = 0.f;
   for (int c = threadIdx.x * 8; c < dim; c += 256 * 8) {
     const f16x8 v = *(const f16x8*)(er + c);
     f32x4 a, b;
@@ -37,37 +27,13 @@ __global__ __launch_bounds__(256) void embedding_kernel(const f16* __restrict__ 
     b.x = (float)v[4]; b.y = (float)v[5]; b.z = (float)v[6]; b.w = (float)v[7];
     *(f32x4*)(xr + c) = a;
     *(f32x4*)(xr + c + 4) = b;
-    if (NORM)
-      ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z +
-            b.w * b.w;
-  }
-  if constexpr (NORM) {
-    ss = block_sum<4>(ss, red);
-    const float r = 1.0f / sqrtf(ss * (1.0f / (float)dim) + eps);
-    f16* orow = xn + (size_t)t * dim;
-    for (int c = threadIdx.x * 8; c < dim; c += 256 * 8) {
-      const f16x8 v = *(const f16x8*)(er + c);
-      f16x8 o;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (f16)((float)v[i] * r * gamma[c + i]);
-      *(f16x8*)(orow + c) = o;
-    }
   }
 }
 
 hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
                      int* err, hipStream_t st) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(embedding_kernel<false>, dim3(T), dim3(256), 0, st, E, tok, dim, vocab, x,
-                     nullptr, 0.f, nullptr, err);
-  return hipGetLastError();
-}
-
-hipError_t embedding_norm(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
-                          const float* gamma, float eps, f16* xn, int* err, hipStream_t st) {
-  if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(embedding_kernel<true>, dim3(T), dim3(256), 0, st, E, tok, dim, vocab, x,
-                     gamma, eps, xn, err);
+  hipLaunchKernelGGL(embedding_kernel, dim3(T), dim3(256), 0, st, E, tok, dim, vocab, x, err);
   return hipGetLastError();
 }
 
@@ -203,25 +169,6 @@ __global__ __launch_bounds__(256) void mean_kernel(const float* __restrict__ v, 
 
 hipError_t mean_reduce(const float* v, int n, float* out, hipStream_t st) {
   hipLaunchKernelGGL(mean_kernel, dim3(1), dim3(256), 0, st, v, n, out);
-  return hipGetLastError();
-}
-
-__global__ void decode_advance_kernel(const uint32_t* next, uint32_t* tok, uint32_t* hist,
-                                      int* d_pos, const int* d_pos0, int B) {
-  const int b = threadIdx.x;
-  const int pos = *d_pos;
-  if (b < B) {
-    tok[b] = next[b];
-    if (hist) hist[(size_t)(pos - *d_pos0) * B + b] = next[b];
-  }
-  __syncthreads();
-  if (b == 0) *d_pos = pos + 1;
-}
-
-hipError_t decode_advance(const uint32_t* next, uint32_t* tok, uint32_t* hist, int* d_pos,
-                          const int* d_pos0, int B, hipStream_t st) {
-  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(64), 0, st, next, tok, hist, d_pos,
-                     d_pos0, B);
   return hipGetLastError();
 }
 

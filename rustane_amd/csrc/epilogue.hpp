@@ -35,21 +35,6 @@ struct EpiResidual {
   }
 };
 
-// EpiResidual whose stores are device-coherent (agent scope): another
-// workgroup of the same launch, on any XCD, can read the rows back with
-// agent-scope loads once this workgroup's stores have completed.
-struct EpiResidualCoherent {
-  EpiResidual e;
-  HB_DEV void operator()(int t, int f0, f32x4 v) const {
-    const size_t o = (size_t)t * e.ld + f0;
-    const f32x4 r = *(const f32x4*)(e.res + o);
-    float* p = e.out + o;
-    __hip_atomic_store(p, v.x * e.alpha + r.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 1, v.y * e.alpha + r.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 2, v.z * e.alpha + r.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 3, v.w * e.alpha + r.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-};
 
 // W1 and W3 are packed row-interleaved in groups of four: packed rows 4j..4j+3
 // are W1 column 2j, W1 column 2j+1, W3 column 2j, W3 column 2j+1. A lane's
@@ -77,11 +62,15 @@ struct EpiSwiGLU {
 };
 
 // Tied-embedding logits with optional softcap (full_model.rs:228-239).
+// The decode GEMV can also emit per-row-block argmax partials of the stored
+// values (part_val/part_idx [B][N/16], nullable; see gemv.hip).
 struct EpiLogits {
   float* logits;
   int vocab;
   float softcap;  // 0 = off
-  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+  float* part_val = nullptr;
+  int* part_idx = nullptr;
+  HB_DEV f32x4 capped(f32x4 v) const {
     if (softcap > 0.f) {
       const float ic = 1.0f / softcap;
       v.x = softcap * tanhf(v.x * ic);
@@ -89,7 +78,10 @@ struct EpiLogits {
       v.z = softcap * tanhf(v.z * ic);
       v.w = softcap * tanhf(v.w * ic);
     }
-    *(f32x4*)(logits + (size_t)t * vocab + f0) = v;
+    return v;
+  }
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    *(f32x4*)(logits + (size_t)t * vocab + f0) = capped(v);
   }
 };
 

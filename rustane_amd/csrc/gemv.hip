@@ -14,15 +14,22 @@
 // K range is one contiguous run, read with nontemporal loads (the stream is
 // never reused within a step, so it should not evict the activations and the
 // KV cache from L2). Measured on the 7B shapes this reaches 5.5-6.5 TB/s, 20%
-// above the row-major kernel it replaced.
+// above a row-major kernel of the same structure.
 //
 // A workgroup owns one 16-row block; its KS waves split K (deterministic LDS
 // reduction at the end).
 //
-// Optional RMSNorm tail (decode residual projections): the epilogue writes the
-// new fp32 residual rows with device-coherent (agent-scope) stores, and the
-// last workgroup to finish (atomic ticket) normalises those rows into the fp16
-// input of the next projection. This replaces a separate launch per norm.
+// Prologue RMSNorm (NORM): the projections that consume a normalised input
+// (QKV, W1|W3, logits) can take the fp32 residual rows instead and normalise
+// them themselves (cpu/rmsnorm.rs:149-183: r = 1/sqrt(sum(x^2)/K + eps),
+// xn = x * r * gamma, rounded to fp16). Every workgroup reads whole rows of x
+// anyway, so each computes the sums of squares of the B rows itself, stages xn
+// in LDS and takes its B operand from there. The first weight loads are issued
+// before the prologue, so the x reads overlap the HBM latency. This removes a
+// launch per norm without putting any extra memory round trip on the critical
+// path; it is used while the B staged rows fit in GEMV_NORM_LDS bytes.
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace hb {
@@ -48,105 +55,91 @@ hipError_t tile_decode(const f16* W, f16* Wt, int N, int K, hipStream_t st) {
   return hipGetLastError();
 }
 
-// RMSNorm of the B rows [B, N] just written by the epilogue (cpu/rmsnorm.rs:
-// 149-183: r = 1/sqrt(sum(x^2)/N + eps), y = x * r * gamma), run by the last
-// workgroup. Rows are spread over the waves: G waves per row (G = KS/B rounded
-// down to a power of two, at least 1), so B = 1 uses the whole workgroup and
-// B >= KS one wave per row. Reads use agent-scope loads: the rows were written
-// by other workgroups, possibly on other XCDs, with agent-scope stores.
-//
-// The tail sits on the critical path of the decode step, so it is built for
-// latency: a lane issues all loads of a batch of up to CH 4-float chunks (and
-// the matching gamma chunks) before using any, and when the row fits in one
-// batch (N <= 1024*G: 8192 at B = 1) the output pass reuses those registers,
-// leaving one memory round trip after the ticket. CH is small because the
-// tail's registers count against the occupancy of the weight-streaming loop.
-template <int KS>
-HB_DEV void norm_tail(const NormTail& nt, int N, int B) {
-  constexpr int CH = 4;
-  __shared__ float s_red[KS];
+// Row stride (in halves) of the staged xn rows: +8 halves keeps the B <= 4
+// rows of one ds_read_b128 on different banks.
+HB_DEV int xn_ld(int K) { return K + 8; }
+
+// xn[b][k] = fp16(x[b][k] * r_b * gamma[k]) for b < B into LDS, by all NT
+// threads of the workgroup. K % 8 == 0.
+template <int NT>
+HB_DEV void stage_norm(const NormIn& nin, int B, int K, f16* s_x) {
+  constexpr int NW = NT / 64;
+  __shared__ float s_part[NW][GEMV_NORM_MAXB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int G = KS;
-  while (G > 1 && G * B > KS) G >>= 1;
-  const int rows_per_pass = KS / G;
-  const int part = wave % G;
-  const int stride = G * 256;  // floats between a lane's consecutive chunks
-  const int first = (part * 64 + lane) * 4;
-  const bool one_batch = N <= stride * CH;
-  auto ld = [](const float* a) {
-    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
-  f32x4 v[CH], g[CH];
-  for (int row0 = 0; row0 < B; row0 += rows_per_pass) {
-    const int row = row0 + wave / G;
-    const bool ok = row < B;
-    const float* xr = nt.x + (size_t)(ok ? row : 0) * N;
-    float ss = 0.f;
-    for (int c0 = first; c0 < N; c0 += stride * CH) {
+  float ss[GEMV_NORM_MAXB];
 #pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        const int c = c0 + i * stride;
-        if (ok && c < N) {
-          v[i].x = ld(xr + c);
-          v[i].y = ld(xr + c + 1);
-          v[i].z = ld(xr + c + 2);
-          v[i].w = ld(xr + c + 3);
-          g[i] = *(const f32x4*)(nt.gamma + c);
-        } else {
-          v[i] = f32x4{};
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < CH; ++i)
-        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-    }
-    ss = wave_sum(ss);
-    __syncthreads();  // s_red reuse across passes
-    if (lane == 0) s_red[wave] = ss;
-    __syncthreads();
-    if (ok) {
-      float tot = 0.f;
-      const int w0 = (wave / G) * G;
-      for (int w = 0; w < G; ++w) tot += s_red[w0 + w];
-      const float r = 1.0f / sqrtf(tot * (1.0f / (float)N) + nt.eps);
-      f16* orow = nt.out + (size_t)row * N;
-      for (int c0 = first; c0 < N; c0 += stride * CH) {
-        if (!one_batch) {
-#pragma unroll
-          for (int i = 0; i < CH; ++i) {
-            const int c = c0 + i * stride;
-            if (c < N) {
-              v[i].x = ld(xr + c);
-              v[i].y = ld(xr + c + 1);
-              v[i].z = ld(xr + c + 2);
-              v[i].w = ld(xr + c + 3);
-              g[i] = *(const f32x4*)(nt.gamma + c);
-            }
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-          const int c = c0 + i * stride;
-          if (c < N) {
-            f16x4 o;
-            o.x = (f16)(v[i].x * r * g[i].x);
-            o.y = (f16)(v[i].y * r * g[i].y);
-            o.z = (f16)(v[i].z * r * g[i].z);
-            o.w = (f16)(v[i].w * r * g[i].w);
-            *(f16x4*)(orow + c) = o;
-          }
-        }
+  for (int b = 0; b < GEMV_NORM_MAXB; ++b) {
+    ss[b] = 0.f;
+    if (b < B) {
+      const float* xr = nin.x + (size_t)b * K;
+      for (int c = tid * 8; c < K; c += NT * 8) {
+        const f32x4 u = *(const f32x4*)(xr + c), v = *(const f32x4*)(xr + c + 4);
+        ss[b] += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w + v.x * v.x + v.y * v.y +
+                 v.z * v.z + v.w * v.w;
       }
     }
+    ss[b] = wave_sum(ss[b]);
+    if (lane == 0) s_part[wave][b] = ss[b];
+  }
+  __syncthreads();
+  const int ld = xn_ld(K);
+  for (int b = 0; b < B; ++b) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += s_part[w][b];
+    const float r = 1.0f / sqrtf(tot * (1.0f / (float)K) + nin.eps);
+    const float* xr = nin.x + (size_t)b * K;
+    for (int c = tid * 8; c < K; c += NT * 8) {
+      const f32x4 u = *(const f32x4*)(xr + c), v = *(const f32x4*)(xr + c + 4);
+      const f32x4 g = *(const f32x4*)(nin.gamma + c), h = *(const f32x4*)(nin.gamma + c + 4);
+      f16x8 o;
+      o[0] = (f16)(u.x * r * g.x);
+      o[1] = (f16)(u.y * r * g.y);
+      o[2] = (f16)(u.z * r * g.z);
+      o[3] = (f16)(u.w * r * g.w);
+      o[4] = (f16)(v.x * r * h.x);
+      o[5] = (f16)(v.y * r * h.y);
+      o[6] = (f16)(v.z * r * h.z);
+      o[7] = (f16)(v.w * r * h.w);
+      *(f16x8*)(s_x + b * ld + c) = o;
+    }
+  }
+  __syncthreads();
+}
+
+// Greedy-decode argmax partials of the logits epilogue: the first index of
+// the maximum of each sequence's 16 logits of this row block, with the
+// cross-entropy kernel's rules (NaN never wins, ties go to the lower index).
+HB_DEV void argmax_partial(const EpiLogits& e, f32x4 v, int f0, int col, int B) {
+  const f32x4 y = e.capped(v);
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  if (y.x > best) { best = y.x; idx = f0; }
+  if (y.y > best) { best = y.y; idx = f0 + 1; }
+  if (y.z > best) { best = y.z; idx = f0 + 2; }
+  if (y.w > best) { best = y.w; idx = f0 + 3; }
+#pragma unroll
+  for (int o = 16; o < 64; o <<= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (ob > best || (ob == best && oi < idx)) {
+      best = ob;
+      idx = oi;
+    }
+  }
+  if ((threadIdx.x & 63) < 16 && col < B) {
+    const size_t slot = (size_t)col * gridDim.x + blockIdx.x;
+    e.part_val[slot] = best;
+    e.part_idx[slot] = idx;
   }
 }
 
-template <int KS, int U, class Epi, bool TAIL>
+template <int KS, int U, class Epi, bool NORM>
 __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__ Wt,
                                                        const f16* __restrict__ X, int N, int B,
-                                                       int K, Epi epi, NormTail nt) {
+                                                       int K, Epi epi, NormIn nin) {
+  extern __shared__ f16x8 s_dyn[];  // NORM: xn rows [B][xn_ld(K)]
   __shared__ f32x4 red[KS][64];
-  __shared__ int s_ticket;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rb = blockIdx.x;
   const int col = lane & 15, kq = 8 * (lane >> 4);
@@ -154,25 +147,43 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
   const int s_begin = (nsteps * wave) / KS, s_end = (nsteps * (wave + 1)) / KS;
   const f16x8* wp = Wt + (size_t)rb * nsteps * 64 + lane;
   const bool xok = col < B;
-  const f16* xrow = X + (size_t)(xok ? col : 0) * K + kq;
+  const f16* s_x = (const f16*)s_dyn;
+  const f16* xrow =
+      NORM ? s_x + (xok ? col : 0) * xn_ld(K) + kq : X + (size_t)(xok ? col : 0) * K + kq;
+  auto bop = [&](int s) -> f16x8 {
+    const f16x8 zero8 = {};
+    return xok ? *(const f16x8*)(xrow + (size_t)s * 32) : zero8;
+  };
 
   f32x4 acc = {};
-  const f16x8 zero8 = {};
   int s = s_begin;
+  if constexpr (NORM) {
+    // First weight batch in flight before the prologue.
+    f16x8 a[U];
+    const bool full = s + U <= s_end;
+    if (full)
+#pragma unroll
+      for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(wp + (size_t)(s + u) * 64);
+    stage_norm<KS * 64>(nin, B, K, (f16*)s_dyn);
+    if (full) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bop(s + u), acc, 0, 0, 0);
+      s += U;
+    }
+  }
   for (; s + U <= s_end; s += U) {
     f16x8 a[U], bx[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       a[u] = __builtin_nontemporal_load(wp + (size_t)(s + u) * 64);
-      bx[u] = xok ? *(const f16x8*)(xrow + (size_t)(s + u) * 32) : zero8;
+      bx[u] = bop(s + u);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bx[u], acc, 0, 0, 0);
   }
   for (; s < s_end; ++s) {
     const f16x8 a = __builtin_nontemporal_load(wp + (size_t)s * 64);
-    const f16x8 bx = xok ? *(const f16x8*)(xrow + (size_t)s * 32) : zero8;
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop(s), acc, 0, 0, 0);
   }
 
   red[wave][lane] = acc;
@@ -184,17 +195,9 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
     for (int w = 1; w < KS; ++w) v += red[w][lane];
     const int f0 = rb * 16 + 4 * (lane >> 4);
     if (col < B) epi(col, f0, v);
-  }
-  if constexpr (TAIL) {
-    // Every store of this workgroup has completed before the ticket is taken.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0)
-      s_ticket = (int)__builtin_amdgcn_atomic_inc32(nt.counter, gridDim.x - 1, __ATOMIC_RELAXED,
-                                                    "agent");
-    __syncthreads();
-    if (s_ticket != (int)gridDim.x - 1) return;
-    norm_tail<KS>(nt, N, B);
+    if constexpr (std::is_same_v<Epi, EpiLogits>) {
+      if (epi.part_val) argmax_partial(epi, v, f0, col, B);
+    }
   }
 }
 
@@ -202,39 +205,107 @@ namespace {
 constexpr int GEMV_KS = 8;  // waves per workgroup (K split)
 constexpr int GEMV_U = 4;   // 1 KB weight loads in flight per wave
 
-template <class Epi, bool TAIL = false>
-hipError_t launch_gemv(const f16* Wt, const f16* X, int N, int B, int K, const Epi& epi,
-                       const NormTail& nt, hipStream_t st) {
+template <class Epi>
+hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
+                       const Epi& epi, hipStream_t st) {
   if (B < 1 || B > 16 || N % 16 || K % 32) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, TAIL>), dim3(N / 16), dim3(GEMV_KS * 64), 0,
-                     st, (const f16x8*)Wt, X, N, B, K, epi, nt);
+  const dim3 grid(N / 16), block(GEMV_KS * 64);
+  // Only the projections fed by a norm (QKV, W1|W3, logits) have a NORM variant.
+  constexpr bool kNorm = !std::is_same_v<Epi, EpiResidual> && !std::is_same_v<Epi, EpiStore>;
+  if (nin) {
+    if constexpr (kNorm) {
+      if (!gemv_norm_fits(B, K)) return hipErrorInvalidValue;
+      const size_t lds = (size_t)B * (K + 8) * 2;
+      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, true>), grid, block, lds, st,
+                         (const f16x8*)Wt, nullptr, N, B, K, epi, *nin);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else {
+    hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, false>), grid, block, 0, st,
+                       (const f16x8*)Wt, X, N, B, K, epi, NormIn{});
+  }
   return hipGetLastError();
 }
 }  // namespace
 
+bool gemv_norm_fits(int B, int K) {
+  return B >= 1 && B <= GEMV_NORM_MAXB && (size_t)B * (K + 8) * 2 <= GEMV_NORM_LDS;
+}
+
 hipError_t gemv_residual(const f16* Wt, const f16* X, int N, int B, int K, const EpiResidual& e,
                          hipStream_t st) {
-  return launch_gemv(Wt, X, N, B, K, e, NormTail{}, st);
+  return launch_gemv(Wt, X, nullptr, N, B, K, e, st);
 }
-hipError_t gemv_residual_norm(const f16* Wt, const f16* X, int N, int B, int K,
-                              const EpiResidual& e, const NormTail& nt, hipStream_t st) {
-  if (nt.x != e.out || !nt.gamma || !nt.out || !nt.counter) return hipErrorInvalidValue;
-  return launch_gemv<EpiResidualCoherent, true>(Wt, X, N, B, K, EpiResidualCoherent{e}, nt, st);
+hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
+                       const EpiSwiGLU& e, hipStream_t st) {
+  return launch_gemv(Wt, X, nin, N, B, K, e, st);
 }
-hipError_t gemv_swiglu(const f16* Wt, const f16* X, int N, int B, int K, const EpiSwiGLU& e,
-                       hipStream_t st) {
-  return launch_gemv(Wt, X, N, B, K, e, NormTail{}, st);
+hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
+                       const EpiLogits& e, hipStream_t st) {
+  return launch_gemv(Wt, X, nin, N, B, K, e, st);
 }
-hipError_t gemv_logits(const f16* Wt, const f16* X, int N, int B, int K, const EpiLogits& e,
-                       hipStream_t st) {
-  return launch_gemv(Wt, X, N, B, K, e, NormTail{}, st);
-}
-hipError_t gemv_qkv(const f16* Wt, const f16* X, int N, int B, int K, const EpiQKV& e,
-                    hipStream_t st) {
-  return launch_gemv(Wt, X, N, B, K, e, NormTail{}, st);
+hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
+                    const EpiQKV& e, hipStream_t st) {
+  return launch_gemv(Wt, X, nin, N, B, K, e, st);
 }
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st) {
-  return launch_gemv(Wt, X, N, B, K, EpiStore{C, N}, NormTail{}, st);
+  return launch_gemv(Wt, X, nullptr, N, B, K, EpiStore{C, N}, st);
+}
+
+// ---- greedy token: reduce the argmax partials, advance the decode state ----
+// One workgroup; wave w reduces sequences w, w+4, ... (B <= 16) with the same
+// rules as argmax_partial. With tok/d_pos set it also does the decode-step
+// bookkeeping: the token becomes the next step's input, is appended to the
+// history at row (pos - pos0), and the position advances.
+__global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* __restrict__ pval,
+                                                            const int* __restrict__ pidx, int nblk,
+                                                            int B, uint32_t* __restrict__ next,
+                                                            uint32_t* tok, uint32_t* hist,
+                                                            int* d_pos, const int* d_pos0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int pos = d_pos ? *d_pos : 0;
+  for (int b = wave; b < B; b += 4) {
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = lane; i < nblk; i += 64) {
+      const float v = pval[(size_t)b * nblk + i];
+      const int j = pidx[(size_t)b * nblk + i];
+      if (v > best || (v == best && j < idx)) {
+        best = v;
+        idx = j;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o, 64);
+      const int oi = __shfl_xor(idx, o, 64);
+      if (ob > best || (ob == best && oi < idx)) {
+        best = ob;
+        idx = oi;
+      }
+    }
+    if (lane == 0) {
+      next[b] = (uint32_t)idx;
+      if (tok) {
+        tok[b] = (uint32_t)idx;
+        if (hist) hist[(size_t)(pos - *d_pos0) * B + b] = (uint32_t)idx;
+      }
+    }
+  }
+  if (d_pos) {
+    __syncthreads();  // every wave has read *d_pos
+    if (threadIdx.x == 0) *d_pos = pos + 1;
+  }
+}
+
+hipError_t argmax_reduce(const float* pval, const int* pidx, int nblk, int B, uint32_t* next,
+                         uint32_t* tok, uint32_t* hist, int* d_pos, const int* d_pos0,
+                         hipStream_t st) {
+  if (B < 1 || B > 16 || nblk < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(256), 0, st, pval, pidx, nblk, B, next,
+                     tok, hist, d_pos, d_pos0);
+  return hipGetLastError();
 }
 
 }  // namespace hb

@@ -20,26 +20,31 @@ hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQK
 // W arguments are decode copies in fragment-tiled order (tile_decode); N is a
 // multiple of 16 and K of 32.
 hipError_t tile_decode(const f16* W, f16* Wt, int N, int K, hipStream_t st);
-// RMSNorm of the rows an epilogue just wrote, done by the launch's last
-// workgroup. counter is zero between launches (the ticket wraps back to 0).
-struct NormTail {
-  const float* x;  // [B, N] rows written by the epilogue (must be its output)
+// Input RMSNorm done inside the GEMV (nin != NULL): the B rows of x [B, K]
+// fp32 are normalised with gamma [K] and staged in LDS; X is then unused.
+struct NormIn {
+  const float* x;
   const float* gamma;
   float eps;
-  f16* out;  // [B, N]
-  unsigned* counter;
 };
+constexpr int GEMV_NORM_MAXB = 8;
+constexpr size_t GEMV_NORM_LDS = 32768;  // bytes of staged fp16 rows
+bool gemv_norm_fits(int B, int K);
 hipError_t gemv_residual(const f16* Wt, const f16* X, int N, int B, int K, const EpiResidual& e,
                          hipStream_t st);
-hipError_t gemv_residual_norm(const f16* Wt, const f16* X, int N, int B, int K,
-                              const EpiResidual& e, const NormTail& nt, hipStream_t st);
-hipError_t gemv_swiglu(const f16* Wt, const f16* X, int N, int B, int K, const EpiSwiGLU& e,
-                       hipStream_t st);
-hipError_t gemv_logits(const f16* Wt, const f16* X, int N, int B, int K, const EpiLogits& e,
-                       hipStream_t st);
-hipError_t gemv_qkv(const f16* Wt, const f16* X, int N, int B, int K, const EpiQKV& e,
-                    hipStream_t st);
+hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
+                       const EpiSwiGLU& e, hipStream_t st);
+hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
+                       const EpiLogits& e, hipStream_t st);
+hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
+                    const EpiQKV& e, hipStream_t st);
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st);
+// Greedy token from the logits GEMV's argmax partials ([B][nblk] each). With
+// tok != NULL it also feeds the token back (tok, hist row pos - *d_pos0) and
+// advances *d_pos.
+hipError_t argmax_reduce(const float* pval, const int* pidx, int nblk, int B, uint32_t* next,
+                         uint32_t* tok, uint32_t* hist, int* d_pos, const int* d_pos0,
+                         hipStream_t st);
 
 // ---- attention (attention.hip) ----
 struct AttnPrefill {
@@ -74,9 +79,6 @@ hipError_t attention_decode(const AttnDecode& p, hipStream_t st);
 // ---- elementwise / reductions (elementwise.hip) ----
 hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
                      int* err, hipStream_t st);
-// embedding + RMSNorm of each row into xn (fp16) in the same launch.
-hipError_t embedding_norm(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
-                          const float* gamma, float eps, f16* xn, int* err, hipStream_t st);
 // Rows r < T of x at x + r*row_stride (floats), dim contiguous.
 hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
                    f16* out, float* rms_inv, hipStream_t st);
@@ -84,9 +86,6 @@ hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, i
 hipError_t cross_entropy(const float* logits, const uint32_t* targets, int T, int vocab,
                          float* loss, uint32_t* argmax, int* err, hipStream_t st);
 hipError_t mean_reduce(const float* v, int n, float* out, hipStream_t st);
-// Decode bookkeeping: tok[b] = next[b]; hist[(pos - pos0)*B + b] = next[b]; pos += 1.
-hipError_t decode_advance(const uint32_t* next, uint32_t* tok, uint32_t* hist, int* d_pos,
-                          const int* d_pos0, int B, hipStream_t st);
 hipError_t set_int(int* d, int value, hipStream_t st);
 
 // Weight repacking: src fp32 [R][C] row-major (device), dst fp16.

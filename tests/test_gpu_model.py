@@ -189,6 +189,24 @@ def test_decode_batch_rows_match_batch_one(m48):
         assert np.abs(lb2[b] - l12[0]).max() < 1e-3
 
 
+def test_decode_separate_norm_path_matches_fused(m48):
+    """Batch 12 at dim 512 is past the in-GEMV RMSNorm limit (8 staged rows), so
+    its decode step runs separate norm launches; its rows must agree with
+    batch-1 decoders, which normalise inside the GEMVs."""
+    cfg, w, k = m48
+    B, P = 12, 24
+    tok = tokens_for(cfg, B * (P + 2), seed=61).reshape(B, P + 2)
+    db = E.Decoder(k, batch=B, ctx_max=P + 2)
+    db.prefill(tok[:, :P])
+    lb, nb = db.step(tok[:, P])
+    for b in (0, 5, 11):
+        d1 = E.Decoder(k, batch=1, ctx_max=P + 2)
+        d1.prefill(tok[b, :P])
+        l1, n1 = d1.step([tok[b, P]])
+        assert np.abs(lb[b] - l1[0]).max() < 1e-3
+        assert int(nb[b]) == int(l1[0].argmax())
+
+
 def test_error_paths(gpu):
     cfg = tiny_config()
     k = CompiledKernels.compile(cfg)
