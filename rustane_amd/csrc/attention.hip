@@ -122,31 +122,41 @@ hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-// ---- decode: split the context into 128-key chunks ------------------------------
-// Grid (chunk, head, sequence), 4 waves per chunk, 32 keys per wave. hd/8 lanes
-// share one key row (16-byte loads; one wave instruction reads 1 KB of
+// ---- decode: split the context into 512-key chunks ------------------------------
+// Grid (chunk, head, sequence), 16 waves per chunk, 32 keys per wave. hd/8
+// lanes share one key row (16-byte loads; one wave instruction reads 1 KB of
 // consecutive key rows). Each lane issues all of its K and V loads before
 // using any (V does not depend on the scores), each wave keeps its own online
-// softmax state, and the four waves merge through LDS: there is no block-wide
-// barrier between the score and value passes. Chunks past the current position
+// softmax state, and the 16 waves merge through LDS into one partial
+// (max, sum, unnormalised output) per chunk. Chunks past the current position
 // exit at once, so the launch shape does not depend on the position (one HIP
-// graph replays every step). The last workgroup of a head to finish (atomic
-// ticket) merges the chunk partials into the output, so no separate combine
-// launch is needed. The partials travel through device-coherent (agent-scope)
-// stores and loads instead of a device-scope fence: on gfx950 such a fence is
-// an L2 write-back that costs more than the whole attention pass.
-constexpr int DCHUNK = 128;
+// graph replays every step). Measured on MI355X, 512-key chunks on 16 waves
+// stream the cache as fast as 128-key chunks on 4 waves while leaving 4x fewer
+// partials to combine.
+//
+// The partials are combined either by the consumer -- the Wo GEMV prologue
+// (gemv.hip), when B * chunks is small -- or here (MERGE): the last workgroup
+// of a head to finish (atomic ticket) merges the chunk partials into the
+// output. The in-kernel merge puts three memory round trips on the critical
+// path (agent-scope stores, ticket, agent-scope loads: partials travel through
+// device-coherent accesses instead of a device-scope fence, which on gfx950 is
+// an L2 write-back costing more than the whole pass), about 5 us on the 7B
+// shape, which is why the consumer combine is preferred.
+constexpr int DCHUNK = 512;
+constexpr int DWAVES = 16;
 
 int attn_decode_chunks(int ctx_max) { return (ctx_max + DCHUNK - 1) / DCHUNK; }
+int attn_decode_chunk_keys() { return DCHUNK; }
 
-template <int HD>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecode p) {
-  constexpr int LPK = HD / 8;        // lanes per key row
-  constexpr int KPW = 64 / LPK;      // keys per wave instruction
-  constexpr int WKEYS = DCHUNK / 4;  // keys per wave
+template <int HD, bool MERGE>
+__global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) {
+  constexpr int NT = DWAVES * 64;
+  constexpr int LPK = HD / 8;             // lanes per key row
+  constexpr int KPW = 64 / LPK;           // keys per wave instruction
+  constexpr int WKEYS = DCHUNK / DWAVES;  // keys per wave
   constexpr int NIT = WKEYS / KPW;
-  __shared__ float s_m[4], s_l[4];
-  __shared__ float s_o[4][HD];
+  __shared__ float s_m[DWAVES], s_l[DWAVES];
+  __shared__ float s_o[DWAVES][HD];
   __shared__ int s_ticket;
 
   const int pos = *p.d_pos;
@@ -219,79 +229,101 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecode p) {
     for (int e = 0; e < 8; ++e) s_o[wave][8 * j + e] = acc[e];
   }
   __syncthreads();
-  float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
-  float w[4];
+  float M = s_m[0];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) w[v] = s_m[v] == -INFINITY ? 0.f : exp2f(s_m[v] - M);
+  for (int v = 1; v < DWAVES; ++v) M = fmaxf(M, s_m[v]);
   const int nch = gridDim.x;
   const size_t head = (size_t)b * p.H + h;
   const size_t slot = head * nch + blockIdx.x;
-  // Partials are written with agent-scope (device-coherent) stores, so once
-  // they have completed they are visible to every XCD without an L2
-  // write-back; the workgroup barrier below waits for that completion.
-  for (int e = tid; e < HD; e += 256)
-    __hip_atomic_store(p.part_o + slot * HD + e,
-                       w[0] * s_o[0][e] + w[1] * s_o[1][e] + w[2] * s_o[2][e] + w[3] * s_o[3][e],
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Wave weights exp2(m_w - M); a wave whose keys are all past pos has
+  // m_w = -inf and weight 0.
+  auto wt = [&](int v) { return s_m[v] == -INFINITY ? 0.f : exp2f(s_m[v] - M); };
+  for (int e = tid; e < HD; e += NT) {
+    float o = 0.f;
+#pragma unroll
+    for (int v = 0; v < DWAVES; ++v) o += wt(v) * s_o[v][e];
+    if (MERGE)
+      __hip_atomic_store(p.part_o + slot * HD + e, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      p.part_o[slot * HD + e] = o;
+  }
   if (tid == 0) {
-    __hip_atomic_store(p.part_ml + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.part_ml + slot * 2 + 1,
-                       w[0] * s_l[0] + w[1] * s_l[1] + w[2] * s_l[2] + w[3] * s_l[3],
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-  // The last chunk of this head to finish merges all chunks (its reads are
-  // agent-scope loads of the coherent partials). atomicInc wraps the counter
-  // back to 0 after the last arrival, ready for the next launch.
-  const int nvalid = pos / DCHUNK + 1;
-  __syncthreads();
-  if (tid == 0)
-    s_ticket = (int)__builtin_amdgcn_atomic_inc32(p.counters + head, (unsigned)(nvalid - 1),
-                                                  __ATOMIC_RELAXED, "agent");
-  __syncthreads();
-  if (s_ticket != nvalid - 1) return;
-  // Merge in groups of MCH chunks: all threads load a group's partials into LDS
-  // at once (independent loads, one memory latency per group), then each
-  // output dimension folds the group into a running (max, sum, out) state.
-  constexpr int MCH = 32;
-  __shared__ float s_cml[MCH][2];
-  __shared__ float s_co[MCH][HD];
-  auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-  const float* pml = p.part_ml + head * nch * 2;
-  const float* pso = p.part_o + head * nch * HD;
-  float Mx = -INFINITY, L = 0.f, O = 0.f;
-  for (int g0 = 0; g0 < nvalid; g0 += MCH) {
-    const int cnt = min(MCH, nvalid - g0);
-    for (int i = tid; i < cnt * HD; i += 256) s_co[i / HD][i % HD] = ld(pso + (size_t)(g0 + i / HD) * HD + i % HD);
-    if (tid < 2 * cnt) s_cml[tid >> 1][tid & 1] = ld(pml + (size_t)g0 * 2 + tid);
-    __syncthreads();
-    if (tid < HD) {
-      float gm = Mx;
-      for (int c = 0; c < cnt; ++c) gm = fmaxf(gm, s_cml[c][0]);
-      const float r = exp2f(Mx - gm);  // Mx = -inf on the first group: r = 0
-      L *= r;
-      O *= r;
-      for (int c = 0; c < cnt; ++c) {
-        const float wc = exp2f(s_cml[c][0] - gm);
-        L += wc * s_cml[c][1];
-        O += wc * s_co[c][tid];
-      }
-      Mx = gm;
+    float L = 0.f;
+#pragma unroll
+    for (int v = 0; v < DWAVES; ++v) L += wt(v) * s_l[v];
+    if (MERGE) {
+      __hip_atomic_store(p.part_ml + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.part_ml + slot * 2 + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      p.part_ml[slot * 2] = M;
+      p.part_ml[slot * 2 + 1] = L;
     }
-    __syncthreads();
   }
-  if (tid < HD) p.out[head * HD + tid] = (f16)(O / L);
+  if constexpr (MERGE) {
+    // The last chunk of this head to finish merges all chunks (its reads are
+    // agent-scope loads of the coherent partials). atomicInc wraps the
+    // counter back to 0 after the last arrival, ready for the next launch.
+    const int nvalid = pos / DCHUNK + 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this workgroup's partial stores have completed
+    __syncthreads();
+    if (tid == 0)
+      s_ticket = (int)__builtin_amdgcn_atomic_inc32(p.counters + head, (unsigned)(nvalid - 1),
+                                                    __ATOMIC_RELAXED, "agent");
+    __syncthreads();
+    if (s_ticket != nvalid - 1) return;
+    // Merge in groups of MCH chunks: all threads load a group's partials into
+    // LDS at once (independent loads, one memory latency per group), then each
+    // output dimension folds the group into a running (max, sum, out) state.
+    constexpr int MCH = 32;
+    __shared__ float s_cml[MCH][2];
+    __shared__ float s_co[MCH][HD];
+    auto ld = [](const float* a) {
+      return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    const float* pml = p.part_ml + head * nch * 2;
+    const float* pso = p.part_o + head * nch * HD;
+    float Mx = -INFINITY, L = 0.f, O = 0.f;
+    for (int g0 = 0; g0 < nvalid; g0 += MCH) {
+      const int cnt = min(MCH, nvalid - g0);
+      for (int i = tid; i < cnt * HD; i += NT)
+        s_co[i / HD][i % HD] = ld(pso + (size_t)(g0 + i / HD) * HD + i % HD);
+      if (tid < 2 * cnt) s_cml[tid >> 1][tid & 1] = ld(pml + (size_t)g0 * 2 + tid);
+      __syncthreads();
+      if (tid < HD) {
+        float gm = Mx;
+        for (int c = 0; c < cnt; ++c) gm = fmaxf(gm, s_cml[c][0]);
+        const float r = exp2f(Mx - gm);  // Mx = -inf on the first group: r = 0
+        L *= r;
+        O *= r;
+        for (int c = 0; c < cnt; ++c) {
+          const float wc = exp2f(s_cml[c][0] - gm);
+          L += wc * s_cml[c][1];
+          O += wc * s_co[c][tid];
+        }
+        Mx = gm;
+      }
+      __syncthreads();
+    }
+    if (tid < HD) p.out[head * HD + tid] = (f16)(O / L);
+  }
 }
 
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
   const int nch = attn_decode_chunks(p.ctx_max);
-  dim3 grid(nch, p.H, p.B);
-  if (p.hd == 128)
-    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, p);
-  else if (p.hd == 64)
-    hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, st, p);
-  else
+  dim3 grid(nch, p.H, p.B), block(DWAVES * 64);
+  if (p.hd == 128) {
+    if (p.merge)
+      hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, block, 0, st, p);
+  } else if (p.hd == 64) {
+    if (p.merge)
+      hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, block, 0, st, p);
+  } else {
     return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

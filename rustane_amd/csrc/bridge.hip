@@ -128,6 +128,7 @@ struct hb_kv {
   uint32_t *d_tok = nullptr, *d_next = nullptr, *d_hist = nullptr;
   float *x = nullptr, *x2 = nullptr, *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
   unsigned* counters = nullptr;  // decode attention arrival tickets [B][H]
+  bool attn_in_wo = false;       // chunk partials combined by the Wo GEMV
   float* amax_val = nullptr;  // greedy argmax partials [B][vocab/16]
   int* amax_idx = nullptr;
   f16 *xn = nullptr, *qd = nullptr, *attn = nullptr, *gate = nullptr;
@@ -993,12 +994,15 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
     a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
     a.ctx_max = kv->ctx_cap; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
-    a.part_ml = kv->part_ml; a.counters = kv->counters; a.out = kv->attn;
+    a.part_ml = kv->part_ml; a.merge = !kv->attn_in_wo; a.counters = kv->counters; a.out = kv->attn;
     HIP_TRY(attention_decode(a, st));
-    HIP_TRY(gemv_residual(L.t_wo, kv->attn, c.dim, B, c.q_dim, EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
+    const AttnIn ain{kv->part_o, kv->part_ml, kv->d_pos, c.heads, c.hd, kv->nch, attn_decode_chunk_keys()};
+    HIP_TRY(gemv_residual(L.t_wo, kv->attn, kv->attn_in_wo ? &ain : nullptr, c.dim, B, c.q_dim,
+                          EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
     HIP_TRY(prep_norm(kv->x2, L.g2, n2));
     HIP_TRY(gemv_swiglu(L.t_w13, kv->xn, fused ? &n2 : nullptr, 2 * c.hidden, B, c.dim, EpiSwiGLU{kv->gate, nullptr, c.hidden}, st));
-    HIP_TRY(gemv_residual(L.t_w2, kv->gate, c.dim, B, c.hidden, EpiResidual{kv->x2, kv->x, c.dim, alpha}, st));
+    HIP_TRY(gemv_residual(L.t_w2, kv->gate, nullptr, c.dim, B, c.hidden,
+                          EpiResidual{kv->x2, kv->x, c.dim, alpha}, st));
   }
   NormIn nf;
   HIP_TRY(prep_norm(kv->x, m->gamma_f, nf));
@@ -1062,6 +1066,7 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   kv->ctx_max = ctx_max;
   kv->ctx_cap = (ctx_max + 63) & ~63;
   kv->nch = attn_decode_chunks(kv->ctx_cap);
+  kv->attn_in_wo = gemv_attn_fits(batch, m->cfg.q_dim, kv->nch);
   int r = ensure_rope(m, kv->ctx_cap);
   if (r != HB_OK) {
     delete kv;

@@ -28,6 +28,15 @@
 // before the prologue, so the x reads overlap the HBM latency. This removes a
 // launch per norm without putting any extra memory round trip on the critical
 // path; it is used while the B staged rows fit in GEMV_NORM_LDS bytes.
+//
+// Attention prologue (Wo only): the decode attention leaves one partial
+// (max, sum, unnormalised output) per 512-key chunk, and every Wo workgroup
+// merges them into the fp16 attention rows it needs (all of them) in the same
+// way. With B * chunks <= GEMV_ATTN_MAXCH that is at most 8 x 130 floats per
+// (sequence, head) -- 133 KB per workgroup on the 7B shape at 4096 context --
+// fetched in one round trip while the first weight loads are in flight,
+// instead of the three dependent round trips of a merge inside the attention
+// launch.
 #include <type_traits>
 
 #include "internal.hpp"
@@ -107,6 +116,65 @@ HB_DEV void stage_norm(const NormIn& nin, int B, int K, f16* s_x) {
   __syncthreads();
 }
 
+// attn[b][h*hd + e] = fp16(sum_c w_c o_c[e] / sum_c w_c l_c), w_c = exp2(m_c - M),
+// M = max_c m_c over the chunks c <= *d_pos / chunk of attention_decode -- the
+// arithmetic and chunk order of its in-kernel merge. One 8-dim group of one
+// (sequence, head) per thread and pass, every chunk load of a group issued
+// before any is used (one memory round trip).
+template <int NT>
+HB_DEV void stage_attn(const AttnIn& ai, int B, int K, f16* s_x) {
+  constexpr int MAXCH = GEMV_ATTN_MAXCH;
+  const int nvalid = min(*ai.d_pos / ai.chunk + 1, ai.nch);
+  const int gph = ai.hd / 8;
+  const int ngroups = B * ai.H * gph;
+  const int ld = xn_ld(K);
+  for (int gi = threadIdx.x; gi < ngroups; gi += NT) {
+    const int e0 = (gi % gph) * 8;
+    const int bh = gi / gph;  // b * H + h
+    const int b = bh / ai.H, h = bh - b * ai.H;
+    const float* pml = ai.part_ml + (size_t)bh * ai.nch * 2;
+    const float* po = ai.part_o + (size_t)bh * ai.nch * ai.hd + e0;
+    float m[MAXCH], l[MAXCH];
+    f32x4 u[MAXCH], v[MAXCH];
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c) {
+      if (c < nvalid) {
+        m[c] = pml[2 * c];
+        l[c] = pml[2 * c + 1];
+        u[c] = *(const f32x4*)(po + (size_t)c * ai.hd);
+        v[c] = *(const f32x4*)(po + (size_t)c * ai.hd + 4);
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c)
+      if (c < nvalid) M = fmaxf(M, m[c]);
+    float L = 0.f;
+    f32x4 O0 = {}, O1 = {};
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c) {
+      if (c < nvalid) {
+        const float w = exp2f(m[c] - M);
+        L += w * l[c];
+        O0 += w * u[c];
+        O1 += w * v[c];
+      }
+    }
+    const float iL = 1.0f / L;
+    f16x8 o;
+    o[0] = (f16)(O0.x * iL);
+    o[1] = (f16)(O0.y * iL);
+    o[2] = (f16)(O0.z * iL);
+    o[3] = (f16)(O0.w * iL);
+    o[4] = (f16)(O1.x * iL);
+    o[5] = (f16)(O1.y * iL);
+    o[6] = (f16)(O1.z * iL);
+    o[7] = (f16)(O1.w * iL);
+    *(f16x8*)(s_x + b * ld + h * ai.hd + e0) = o;
+  }
+  __syncthreads();
+}
+
 // Greedy-decode argmax partials of the logits epilogue: the first index of
 // the maximum of each sequence's 16 logits of this row block, with the
 // cross-entropy kernel's rules (NaN never wins, ties go to the lower index).
@@ -134,11 +202,15 @@ HB_DEV void argmax_partial(const EpiLogits& e, f32x4 v, int f0, int col, int B) 
   }
 }
 
-template <int KS, int U, class Epi, bool NORM>
+// Prologue kinds: the B operand comes from X (PRO_NONE) or from rows staged
+// in LDS by stage_norm (PRO_NORM) or stage_attn (PRO_ATTN).
+enum { PRO_NONE = 0, PRO_NORM = 1, PRO_ATTN = 2 };
+
+template <int KS, int U, class Epi, int PRO>
 __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__ Wt,
                                                        const f16* __restrict__ X, int N, int B,
-                                                       int K, Epi epi, NormIn nin) {
-  extern __shared__ f16x8 s_dyn[];  // NORM: xn rows [B][xn_ld(K)]
+                                                       int K, Epi epi, NormIn nin, AttnIn ain) {
+  extern __shared__ f16x8 s_dyn[];  // staged B-operand rows [B][xn_ld(K)]
   __shared__ f32x4 red[KS][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rb = blockIdx.x;
@@ -148,8 +220,8 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
   const f16x8* wp = Wt + (size_t)rb * nsteps * 64 + lane;
   const bool xok = col < B;
   const f16* s_x = (const f16*)s_dyn;
-  const f16* xrow =
-      NORM ? s_x + (xok ? col : 0) * xn_ld(K) + kq : X + (size_t)(xok ? col : 0) * K + kq;
+  const f16* xrow = PRO != PRO_NONE ? s_x + (xok ? col : 0) * xn_ld(K) + kq
+                                     : X + (size_t)(xok ? col : 0) * K + kq;
   auto bop = [&](int s) -> f16x8 {
     const f16x8 zero8 = {};
     return xok ? *(const f16x8*)(xrow + (size_t)s * 32) : zero8;
@@ -157,19 +229,24 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
 
   f32x4 acc = {};
   int s = s_begin;
-  if constexpr (NORM) {
-    // First weight batch in flight before the prologue.
-    f16x8 a[U];
-    const bool full = s + U <= s_end;
-    if (full)
+  if constexpr (PRO != PRO_NONE) {
+    // Keep the weight stream busy through the prologue: up to PF fragments
+    // per wave are in flight before it starts. Wo (attention prologue) runs
+    // one workgroup per CU, so it can hold its whole 7B slice (16 steps).
+    constexpr int PF = PRO == PRO_ATTN ? 16 : 8;
+    f16x8 a[PF];
+    const int npf = min(PF, s_end - s);
 #pragma unroll
-      for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(wp + (size_t)(s + u) * 64);
-    stage_norm<KS * 64>(nin, B, K, (f16*)s_dyn);
-    if (full) {
+    for (int u = 0; u < PF; ++u)
+      if (u < npf) a[u] = __builtin_nontemporal_load(wp + (size_t)(s + u) * 64);
+    if constexpr (PRO == PRO_NORM)
+      stage_norm<KS * 64>(nin, B, K, (f16*)s_dyn);
+    else
+      stage_attn<KS * 64>(ain, B, K, (f16*)s_dyn);
 #pragma unroll
-      for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bop(s + u), acc, 0, 0, 0);
-      s += U;
-    }
+    for (int u = 0; u < PF; ++u)
+      if (u < npf) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bop(s + u), acc, 0, 0, 0);
+    s += npf;
   }
   for (; s + U <= s_end; s += U) {
     f16x8 a[U], bx[U];
@@ -206,24 +283,34 @@ constexpr int GEMV_KS = 8;  // waves per workgroup (K split)
 constexpr int GEMV_U = 4;   // 1 KB weight loads in flight per wave
 
 template <class Epi>
-hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const Epi& epi, hipStream_t st) {
+hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, const AttnIn* ain, int N,
+                       int B, int K, const Epi& epi, hipStream_t st) {
   if (B < 1 || B > 16 || N % 16 || K % 32) return hipErrorInvalidValue;
   const dim3 grid(N / 16), block(GEMV_KS * 64);
-  // Only the projections fed by a norm (QKV, W1|W3, logits) have a NORM variant.
+  const size_t lds = (size_t)B * (K + 8) * 2;
+  // Only the projections fed by a norm (QKV, W1|W3, logits) have a norm
+  // prologue, and only Wo (residual epilogue) the attention combine.
   constexpr bool kNorm = !std::is_same_v<Epi, EpiResidual> && !std::is_same_v<Epi, EpiStore>;
+  constexpr bool kAttn = std::is_same_v<Epi, EpiResidual>;
   if (nin) {
     if constexpr (kNorm) {
       if (!gemv_norm_fits(B, K)) return hipErrorInvalidValue;
-      const size_t lds = (size_t)B * (K + 8) * 2;
-      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, true>), grid, block, lds, st,
-                         (const f16x8*)Wt, nullptr, N, B, K, epi, *nin);
+      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NORM>), grid, block, lds, st,
+                         (const f16x8*)Wt, nullptr, N, B, K, epi, *nin, AttnIn{});
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (ain) {
+    if constexpr (kAttn) {
+      if (!gemv_attn_fits(B, K, ain->nch) || ain->H * ain->hd != K || ain->hd % 8) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_ATTN>), grid, block, lds, st,
+                         (const f16x8*)Wt, nullptr, N, B, K, epi, NormIn{}, *ain);
     } else {
       return hipErrorInvalidValue;
     }
   } else {
-    hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, false>), grid, block, 0, st,
-                       (const f16x8*)Wt, X, N, B, K, epi, NormIn{});
+    hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE>), grid, block, 0, st,
+                       (const f16x8*)Wt, X, N, B, K, epi, NormIn{}, AttnIn{});
   }
   return hipGetLastError();
 }
@@ -232,71 +319,90 @@ hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, int N, in
 bool gemv_norm_fits(int B, int K) {
   return B >= 1 && B <= GEMV_NORM_MAXB && (size_t)B * (K + 8) * 2 <= GEMV_NORM_LDS;
 }
+bool gemv_attn_fits(int B, int K, int nch) {
+  return B >= 1 && nch >= 1 && B * nch <= GEMV_ATTN_MAXCH &&
+         (size_t)B * (K + 8) * 2 <= GEMV_NORM_LDS;
+}
 
-hipError_t gemv_residual(const f16* Wt, const f16* X, int N, int B, int K, const EpiResidual& e,
-                         hipStream_t st) {
-  return launch_gemv(Wt, X, nullptr, N, B, K, e, st);
+hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, int B, int K,
+                         const EpiResidual& e, hipStream_t st) {
+  return launch_gemv(Wt, X, nullptr, ain, N, B, K, e, st);
 }
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                        const EpiSwiGLU& e, hipStream_t st) {
-  return launch_gemv(Wt, X, nin, N, B, K, e, st);
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st);
 }
 hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                        const EpiLogits& e, hipStream_t st) {
-  return launch_gemv(Wt, X, nin, N, B, K, e, st);
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st);
 }
 hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                     const EpiQKV& e, hipStream_t st) {
-  return launch_gemv(Wt, X, nin, N, B, K, e, st);
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st);
 }
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st) {
-  return launch_gemv(Wt, X, nullptr, N, B, K, EpiStore{C, N}, st);
+  return launch_gemv(Wt, X, nullptr, nullptr, N, B, K, EpiStore{C, N}, st);
 }
 
 // ---- greedy token: reduce the argmax partials, advance the decode state ----
-// One workgroup; wave w reduces sequences w, w+4, ... (B <= 16) with the same
-// rules as argmax_partial. With tok/d_pos set it also does the decode-step
-// bookkeeping: the token becomes the next step's input, is appended to the
-// history at row (pos - pos0), and the position advances.
+// One workgroup of 256 threads per call; for each sequence every thread folds
+// a strided share of the partials (8 loads in flight per batch), then the
+// block reduces through LDS, with the same rules as argmax_partial. With
+// tok/d_pos set it also does the decode-step bookkeeping: the token becomes
+// the next step's input, is appended to the history at row (pos - pos0), and
+// the position advances.
+HB_DEV void amax_fold(float& best, int& idx, float v, int j) {
+  if (v > best || (v == best && j < idx)) {
+    best = v;
+    idx = j;
+  }
+}
+
 __global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* __restrict__ pval,
                                                             const int* __restrict__ pidx, int nblk,
                                                             int B, uint32_t* __restrict__ next,
                                                             uint32_t* tok, uint32_t* hist,
                                                             int* d_pos, const int* d_pos0) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int NB = 8;
+  __shared__ float s_v[4];
+  __shared__ int s_i[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = d_pos ? *d_pos : 0;
-  for (int b = wave; b < B; b += 4) {
+  for (int b = 0; b < B; ++b) {
+    const float* pv = pval + (size_t)b * nblk;
+    const int* pi = pidx + (size_t)b * nblk;
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = lane; i < nblk; i += 64) {
-      const float v = pval[(size_t)b * nblk + i];
-      const int j = pidx[(size_t)b * nblk + i];
-      if (v > best || (v == best && j < idx)) {
-        best = v;
-        idx = j;
+    for (int i0 = tid; i0 < nblk; i0 += 256 * NB) {
+      float v[NB];
+      int j[NB];
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int i = i0 + u * 256;
+        v[u] = i < nblk ? pv[i] : -INFINITY;
+        j[u] = i < nblk ? pi[i] : 0x7fffffff;
       }
+#pragma unroll
+      for (int u = 0; u < NB; ++u) amax_fold(best, idx, v[u], j[u]);
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(best, o, 64);
-      const int oi = __shfl_xor(idx, o, 64);
-      if (ob > best || (ob == best && oi < idx)) {
-        best = ob;
-        idx = oi;
-      }
-    }
+    for (int o = 32; o > 0; o >>= 1) amax_fold(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
     if (lane == 0) {
+      s_v[wave] = best;
+      s_i[wave] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < 4; ++w) amax_fold(best, idx, s_v[w], s_i[w]);
       next[b] = (uint32_t)idx;
       if (tok) {
         tok[b] = (uint32_t)idx;
         if (hist) hist[(size_t)(pos - *d_pos0) * B + b] = (uint32_t)idx;
       }
     }
+    __syncthreads();  // s_v reuse
   }
-  if (d_pos) {
-    __syncthreads();  // every wave has read *d_pos
-    if (threadIdx.x == 0) *d_pos = pos + 1;
-  }
+  if (d_pos && tid == 0) *d_pos = pos + 1;  // every thread read *d_pos before the first barrier
 }
 
 hipError_t argmax_reduce(const float* pval, const int* pidx, int nblk, int B, uint32_t* next,

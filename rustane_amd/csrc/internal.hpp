@@ -30,8 +30,19 @@ struct NormIn {
 constexpr int GEMV_NORM_MAXB = 8;
 constexpr size_t GEMV_NORM_LDS = 32768;  // bytes of staged fp16 rows
 bool gemv_norm_fits(int B, int K);
-hipError_t gemv_residual(const f16* Wt, const f16* X, int N, int B, int K, const EpiResidual& e,
-                         hipStream_t st);
+// Decode-attention chunk combine done inside the Wo GEMV (ain != NULL): the
+// B x H heads' chunk partials of attention_decode (merge = false) are merged
+// into the fp16 attention rows [B, H*hd], staged in LDS; X is then unused.
+struct AttnIn {
+  const float* part_o;   // [B][H][nch][hd]
+  const float* part_ml;  // [B][H][nch][2]
+  const int* d_pos;      // chunks 0..*d_pos/chunk hold keys
+  int H, hd, nch, chunk;
+};
+constexpr int GEMV_ATTN_MAXCH = 8;  // B * nch limit of the in-GEMV combine
+bool gemv_attn_fits(int B, int K, int nch);
+hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, int B, int K,
+                         const EpiResidual& e, hipStream_t st);
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                        const EpiSwiGLU& e, hipStream_t st);
 hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
@@ -68,12 +79,17 @@ struct AttnDecode {
   const int* d_pos;  // keys 0..*d_pos are attended
   int B, H, KVH, hd, ctx_max;
   float scale;
-  float* part_o;   // [B][H][nchunks][hd]
-  float* part_ml;  // [B][H][nchunks][2]
-  unsigned* counters;  // [B][H] arrival tickets, zero between launches
+  float* part_o;   // [B][H][nchunks][hd] unnormalised chunk outputs
+  float* part_ml;  // [B][H][nchunks][2] chunk (max, sum) in log2 units
+  // merge: combine the chunks in this launch into out (counters: [B][H]
+  // arrival tickets, zero between launches); otherwise only the partials of
+  // chunks 0..*d_pos/chunk_keys are written and the Wo GEMV combines them.
+  bool merge;
+  unsigned* counters;
   f16* out;        // [B][H*hd]
 };
 int attn_decode_chunks(int ctx_max);
+int attn_decode_chunk_keys();
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st);
 
 // ---- elementwise / reductions (elementwise.hip) ----
