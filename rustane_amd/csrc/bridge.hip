@@ -114,6 +114,9 @@ struct hb_model {
   size_t dbytes = 0;
   f16* t_embed = nullptr;
   bool dec_stale = true;
+  // split-K partial sums of the prefill residual GEMMs (gemm_splits)
+  float* splitk = nullptr;
+  size_t splitk_floats = 0;
 };
 
 struct hb_kv {
@@ -268,6 +271,25 @@ int ensure_workspace(hb_model* m, long T, long Tpad) {
 
 int S_pad_of(int S) { return (S + 31) & ~31; }
 
+// Scratch for a residual GEMM of this shape: grown on demand (outside any
+// capture: prefill is never captured), empty when the shape does not split.
+int residual_scratch(hb_model* m, int N, int T, int K, GemmScratch& out) {
+  out = GemmScratch{m->splitk, m->splitk_floats};
+  const int S = gemm_splits(N, T, K);
+  if (S <= 1) return HB_OK;
+  const size_t need = (size_t)S * T * N;
+  if (need > m->splitk_floats) {
+    HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
+    if (m->splitk) HIP_TRY(hipFree(m->splitk));
+    m->splitk = nullptr;
+    m->splitk_floats = 0;
+    HIP_TRY(hipMalloc(&m->splitk, need * 4));
+    m->splitk_floats = need;
+  }
+  out = GemmScratch{m->splitk, m->splitk_floats};
+  return HB_OK;
+}
+
 bool weights_ready(hb_model* m) {
   if (!m->embed_uploaded) return false;
   for (auto& l : m->layers)
@@ -378,10 +400,13 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
   a.hd = c.hd;
   a.scale = 1.0f / sqrtf((float)c.hd);
   HIP_TRY(attention_prefill(a, st));
-  HIP_TRY(gemm_residual(L.wo, w.attn, c.dim, T, c.q_dim, EpiResidual{w.x, w.x2, c.dim, alpha}, st));
+  GemmScratch so, s2;
+  TRY(residual_scratch(m, c.dim, T, c.q_dim, so));
+  HIP_TRY(gemm_residual(L.wo, w.attn, c.dim, T, c.q_dim, EpiResidual{w.x, w.x2, c.dim, alpha}, &so, st));
   HIP_TRY(rmsnorm(w.x2, c.dim, L.g2, T, c.dim, c.norm_eps, w.xn, nullptr, st));
   HIP_TRY(gemm_swiglu(L.w13, w.xn, 2 * c.hidden, T, c.dim, EpiSwiGLU{w.gate, nullptr, c.hidden}, st));
-  HIP_TRY(gemm_residual(L.w2, w.gate, c.dim, T, c.hidden, EpiResidual{w.x2, w.x, c.dim, alpha}, st));
+  TRY(residual_scratch(m, c.dim, T, c.hidden, s2));
+  HIP_TRY(gemm_residual(L.w2, w.gate, c.dim, T, c.hidden, EpiResidual{w.x2, w.x, c.dim, alpha}, &s2, st));
   return HB_OK;
 }
 
@@ -569,6 +594,7 @@ extern "C" int hb_model_destroy(hb_model* m) {
   (void)hipDeviceSynchronize();
   (void)hipFree(m->wbase);
   if (m->dbase) (void)hipFree(m->dbase);
+  if (m->splitk) (void)hipFree(m->splitk);
   if (m->rope) (void)hipFree(m->rope);
   if (m->staging) (void)hipFree(m->staging);
   if (m->ws.base) (void)hipFree(m->ws.base);
@@ -875,8 +901,10 @@ extern "C" int hb_op_wo_fwd(hb_model* m, int layer, const void* attn, const floa
   if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
+  GemmScratch so;
+  TRY(residual_scratch(m, c.dim, T, c.q_dim, so));
   HIP_TRY(gemm_residual(m->layers[layer].wo, (const f16*)attn, c.dim, T, c.q_dim,
-                        EpiResidual{x, x2, c.dim, alpha_of(c)}, m->ctx->stream()));
+                        EpiResidual{x, x2, c.dim, alpha_of(c)}, &so, m->ctx->stream()));
   return HB_OK;
 }
 
@@ -897,7 +925,9 @@ extern "C" int hb_op_ffn_fused(hb_model* m, int layer, const void* x2norm, const
   hipStream_t st = m->ctx->stream();
   const LayerW& L = m->layers[layer];
   HIP_TRY(gemm_swiglu(L.w13, (const f16*)x2norm, 2 * c.hidden, T, c.dim, EpiSwiGLU{gate, h13_tap, c.hidden}, st));
-  HIP_TRY(gemm_residual(L.w2, gate, c.dim, T, c.hidden, EpiResidual{x2, x_next, c.dim, alpha_of(c)}, st));
+  GemmScratch s2;
+  TRY(residual_scratch(m, c.dim, T, c.hidden, s2));
+  HIP_TRY(gemm_residual(L.w2, gate, c.dim, T, c.hidden, EpiResidual{x2, x_next, c.dim, alpha_of(c)}, &s2, st));
   return HB_OK;
 }
 

@@ -16,6 +16,18 @@ struct EpiStore {
   }
 };
 
+// Split-K partial sums of the prefill GEMM: split blockIdx.y writes
+// p[blockIdx.y * split_stride + t * ld + f0 ..]; splitk_reduce (gemm.hip) adds
+// the splits in order and applies the real epilogue.
+struct EpiSplit {
+  float* p;
+  int ld;
+  size_t split_stride;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    *(f32x4*)(p + blockIdx.y * split_stride + (size_t)t * ld + f0) = v;
+  }
+};
+
 // out = res + alpha * v (fp32 residual stream). woFwd + vsma (layer.rs:784) and
 // the ffnFused residual (kernels/ffn_fused.rs:74-77).
 struct EpiResidual {

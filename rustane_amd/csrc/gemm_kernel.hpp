@@ -39,10 +39,14 @@ HB_DEV void lds_barrier() {
 //   reads of step s+1 | MFMAs of step 3 interleaved with the LDS writes of
 //   slice k+1.
 // so LDS latency is always covered by MFMAs of the previous k-step.
+//
+// Split-K: blockIdx.y selects one of gridDim.y contiguous ranges of 64-wide K
+// slices (kq slices each, the last one shorter); with gridDim.y = 1 the range
+// is all of K. Each split hands its partial sums to the epilogue (EpiSplit).
 template <int FT, int TT, int WF, int WT, class Epi>
 __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __restrict__ W,
                                                                  const f16* __restrict__ X, int N,
-                                                                 int T, int K, Epi epi) {
+                                                                 int T, int K, int kq, Epi epi) {
   constexpr int NT = WF * WT * 64;
   constexpr int WFT = FT / WF, WTT = TT / WT;
   constexpr int FM = WFT / 32, TM = WTT / 32;
@@ -115,14 +119,15 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
   };
 
-  const int nk = K / 64;
-  gload(0);
+  const int kt0 = blockIdx.y * kq;
+  const int nk = min(kq, K / 64 - kt0);
+  gload(kt0 * 64);
   sstore(0);
   lds_barrier();
   Frag F0, F1;
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    gload(min(kt + 1, nk - 1) * 64);
+    gload((kt0 + min(kt + 1, nk - 1)) * 64);
     fread(F0, cur, 0);
     fread(F1, cur, 1);
     mfmas(F0);

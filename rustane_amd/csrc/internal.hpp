@@ -6,9 +6,18 @@
 namespace hb {
 
 // ---- prefill GEMM (gemm.hip) ----
+// Scratch for split-K partial sums (fp32); see gemm_splits.
+struct GemmScratch {
+  float* p;
+  size_t floats;
+};
+constexpr int GEMM_MAX_SPLITS = 8;
+// Number of K splits the residual GEMM uses for this shape when given scratch
+// (1 = none); it needs splits * T * N floats.
+int gemm_splits(int N, int T, int K);
 hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st);
 hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
-                         hipStream_t st);
+                         const GemmScratch* scr, hipStream_t st);
 hipError_t gemm_swiglu(const f16* W, const f16* X, int N, int T, int K, const EpiSwiGLU& e,
                        hipStream_t st);
 hipError_t gemm_logits(const f16* W, const f16* X, int N, int T, int K, const EpiLogits& e,

@@ -203,3 +203,36 @@ def test_logits_ce_op_matches_oracle(tiny):
     np.testing.assert_allclose(dl.cpu().numpy(), ref, atol=2e-4)
     _, losses = O.cross_entropy_batch(dl.cpu().numpy(), tgt, cfg.vocab)
     np.testing.assert_allclose(dloss.cpu().numpy(), losses, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("T", [128, 200])
+def test_residual_gemm_split_k_matches_float64(gpu, T):
+    """Wo of a 2048-wide model at <= 256 tokens has few output tiles and a long
+    K, so the residual GEMM splits K (4 ways at 128 tokens) and reduces the
+    fp32 partials in split order before the residual epilogue. Checked against
+    float64 on fp16-exact inputs, and repeat launches must agree bit for bit."""
+    import torch
+    from rustane_amd.engine import ModelConfig
+    cfg = ModelConfig.make(dim=2048, hidden=256, heads=16, nlayers=1, seq=T, vocab=256, hd=128)
+    k = CompiledKernels.compile(cfg)
+    k.ctx.set_stream(gpu.stream())
+    w = ModelWeights.synthetic(cfg, seed=3, std=0.02)
+    k.ensure_weights(w)
+    print(f"split-K Wo: T={T} N={cfg.dim} K={cfg.q_dim}", flush=True)
+    rng = np.random.default_rng(T)
+    attn = f16_round(rng.standard_normal((T, cfg.q_dim)))
+    x = rng.standard_normal((T, cfg.dim)).astype(F32)
+    dattn, dx = to_dev(attn, torch.float16), to_dev(x)
+    outs = []
+    for _ in range(2):
+        dx2 = torch.empty((T, cfg.dim), device="cuda")
+        hb.call("hb_op_wo_fwd", k.model.handle, 0, dattn.data_ptr(), dx.data_ptr(), T, dx2.data_ptr())
+        torch.cuda.synchronize()
+        outs.append(dx2.cpu().numpy())
+    wo = f16_round(oracle_weights(w).layers[0].wo).reshape(cfg.q_dim, cfg.dim)
+    alpha = oracle_cfg(cfg).alpha()
+    ref = x.astype(np.float64) + alpha * (attn.astype(np.float64) @ wo.astype(np.float64))
+    err = np.abs(outs[0] - ref).max()
+    print(f"max|err| {err:.2e}", flush=True)
+    assert err < 1e-4
+    np.testing.assert_array_equal(outs[0], outs[1])
