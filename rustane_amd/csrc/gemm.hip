@@ -36,15 +36,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-// Tile choice (measured on MI355X over the 7B-shape projections): the largest
-// tile that still gives most CUs a tile. 256x256 (8 waves of 64x128) when it
-// yields >= 160 tiles, then 256x128 (8 waves of 64x64), then 128x128
-// (4 waves), else 64x128 (4 waves of 32x64).
+// Tile choice: maximise (relative per-tile throughput) x (fraction of the 256
+// CUs kept busy over the launch's rounds). Relative throughputs are measured
+// on MI355X with many rounds of tiles (7B shapes at 4096 tokens): 256x256
+// (8 waves of 64x128) 1.00, 192x256 (8 waves of 96x64) 0.90, 192x128
+// (4 waves of 96x64) 0.85, 256x128 (8 waves of 64x64) 0.79, 128x128
+// (4 waves of 64x64) 0.77, 64x128 (4 waves of 32x64) 0.55. At 512 tokens
+// this picks 192x256 for W1|W3 (230 tiles instead of 172) and 192x128 for
+// QKV (256 tiles instead of 192).
 //
 // Long-K problems with few 256x256 tiles (Wo and W2 at 512 tokens: 32 tiles)
 // instead split K over up to GEMM_MAX_SPLITS ranges of >= 8 slices so that
 // ~256 workgroups run the efficient 256x256 tile; the partials go through the
 // caller's scratch and splitk_reduce applies the epilogue.
+constexpr int GEMM_CUS = 256;  // MI355X compute units
 static long ntiles(int N, int T, int ft, int tt) { return (long)((N + ft - 1) / ft) * ((T + tt - 1) / tt); }
 
 int gemm_splits(int N, int T, int K) {
@@ -72,10 +77,31 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
                        stride, epi);
     return hipGetLastError();
   }
-  if (ntiles(N, T, 256, 256) >= 160) return launch_tile<256, 256, 4, 2>(W, X, N, T, K, epi, st);
-  if (ntiles(N, T, 256, 128) >= 160) return launch_tile<256, 128, 4, 2>(W, X, N, T, K, epi, st);
-  if (ntiles(N, T, 128, 128) >= 200) return launch_tile<128, 128, 2, 2>(W, X, N, T, K, epi, st);
-  return launch_tile<64, 128, 2, 2>(W, X, N, T, K, epi, st);
+  struct Cand {
+    int ft, tt;
+    float rel;
+  };
+  static constexpr Cand cands[] = {{256, 256, 1.00f}, {192, 256, 0.90f}, {192, 128, 0.85f},
+                                   {256, 128, 0.79f}, {128, 128, 0.77f}, {64, 128, 0.55f}};
+  int best = 0;
+  float best_score = -1.f;
+  for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
+    const long n = ntiles(N, T, cands[i].ft, cands[i].tt);
+    const long rounds = (n + GEMM_CUS - 1) / GEMM_CUS;
+    const float score = cands[i].rel * (float)n / (float)(rounds * GEMM_CUS);
+    if (score > best_score + 1e-6f) {
+      best_score = score;
+      best = i;
+    }
+  }
+  switch (best) {
+    case 0: return launch_tile<256, 256, 4, 2>(W, X, N, T, K, epi, st);
+    case 1: return launch_tile<192, 256, 2, 4>(W, X, N, T, K, epi, st);
+    case 2: return launch_tile<192, 128, 2, 2>(W, X, N, T, K, epi, st);
+    case 3: return launch_tile<256, 128, 4, 2>(W, X, N, T, K, epi, st);
+    case 4: return launch_tile<128, 128, 2, 2>(W, X, N, T, K, epi, st);
+    default: return launch_tile<64, 128, 2, 2>(W, X, N, T, K, epi, st);
+  }
 }
 
 hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st) {

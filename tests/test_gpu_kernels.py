@@ -36,6 +36,9 @@ def _gemm_case(gpu, M, N, K, seed):
     (1024, 2048, 256),   # 128x128 tiles
     (512, 16384, 128),   # 256x128 tiles, XCD remap with 256 tiles
     (300, 1540, 320),    # tails + non power-of-two tile count
+    (512, 22016, 64),    # 192x256 tiles (8 waves of 96x64), partial last row tile
+    (300, 12288, 128),   # 192x128 tiles (4 waves of 96x64), ragged tokens
+    (4096, 4096, 128),   # 256x256 tiles
 ])
 def test_gemm_nt_matches_float64(gpu, M, N, K):
     print(f"gemm M={M} N={N} K={K}", flush=True)
