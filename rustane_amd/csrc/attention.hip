@@ -7,7 +7,7 @@
 
 namespace hb {
 
-// ---- prefill: one wave per (32 queries, head, sequence) -------------------------
+// ---- prefill: one workgroup of PW waves per (32 queries, head, sequence) --------
 // S^T = K · Q^T on v_mfma_f32_32x32x16_f16 (rows = keys, cols = queries): lane l
 // owns query l%32 and keys 8*(r/4) + 4*(l/32) + r%4 of the 32-key block, so the
 // online-softmax statistics of a query live in one lane pair (l, l^32).
@@ -15,11 +15,22 @@ namespace hb {
 // order permuted identically on both operands, lane half h supplies keys
 // {16j+4h..16j+4h+3, 16j+8+4h..16j+8+4h+3} for k-step j — exactly the registers
 // 8j..8j+7 it already holds — and the A operand reads those keys from V^T.
+//
+// The causal key range of a query block is split over the PW waves of the
+// workgroup (wave w takes key blocks w, w+PW, ...), so the longest chain of
+// dependent key blocks is 1/PW of the row and the launch has PW x more waves
+// in flight; each wave keeps its own online-softmax state and waves 1..PW-1
+// hand theirs to wave 0 through LDS for one weighted merge (the same
+// rescaling an online softmax applies between blocks).
+constexpr int PW = 4;
+
 template <int HD>
-__global__ __launch_bounds__(64) void attn_prefill_kernel(AttnPrefill p) {
+__global__ __launch_bounds__(PW * 64) void attn_prefill_kernel(AttnPrefill p) {
   constexpr int KS = HD / 16;  // k-steps over head dim
   constexpr int MB = HD / 32;  // 32-row blocks of O^T
-  const int lane = threadIdx.x, h2 = lane >> 5, li = lane & 31;
+  __shared__ float s_o[PW - 1][MB * 16][64];
+  __shared__ float s_ml[PW - 1][2][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, li = lane & 31;
   const int nqb = (p.S + 31) / 32;
   const int qb = nqb - 1 - blockIdx.x;  // heaviest blocks first
   const int h = blockIdx.y, b = blockIdx.z;
@@ -41,7 +52,7 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnPrefill p) {
   for (int m = 0; m < MB; ++m) o[m] = f32x16{};
   float mrun = -INFINITY, lrun = 0.f;
 
-  for (int kb = 0; kb <= qb; ++kb) {
+  for (int kb = wave; kb <= qb; kb += PW) {
     const f16* kp = kbase + (size_t)(kb * 32 + li) * HD + 8 * h2;
     f32x16 s = {};
 #pragma unroll
@@ -94,8 +105,41 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnPrefill p) {
     }
   }
 
+  // Waves 1..PW-1 hand (o, m, l) to wave 0 (a wave with no key block has
+  // m = -inf and weight 0). Lane l of every wave holds the same (query, row)
+  // slots, so the exchange is one float per lane per register.
+  if (wave > 0) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s_o[wave - 1][m * 16 + r][lane] = o[m][r];
+    s_ml[wave - 1][0][lane] = mrun;
+    s_ml[wave - 1][1][lane] = lrun;
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  float M = mrun;
+#pragma unroll
+  for (int w = 0; w < PW - 1; ++w) M = fmaxf(M, s_ml[w][0][lane]);
+  const float c0 = exp2f(mrun - M);  // wave 0 always holds block 0, so mrun is finite
+  float L = lrun * c0;
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[m][r] *= c0;
+#pragma unroll
+  for (int w = 0; w < PW - 1; ++w) {
+    const float mw = s_ml[w][0][lane];
+    const float cw = mw == -INFINITY ? 0.f : exp2f(mw - M);
+    L += cw * s_ml[w][1][lane];
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[m][r] += cw * s_o[w][m * 16 + r][lane];
+  }
+
   if (qi < p.S) {
-    const float inv = 1.0f / lrun;
+    const float inv = 1.0f / L;
     f16* op = p.out + ((size_t)b * p.S + qi) * (p.H * HD) + h * HD;
 #pragma unroll
     for (int m = 0; m < MB; ++m)
@@ -114,9 +158,9 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(AttnPrefill p) {
 hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
   dim3 grid((p.S + 31) / 32, p.H, p.B);
   if (p.hd == 128)
-    hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(64), 0, st, p);
+    hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(PW * 64), 0, st, p);
   else if (p.hd == 64)
-    hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(64), 0, st, p);
+    hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(PW * 64), 0, st, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
