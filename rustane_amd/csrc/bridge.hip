@@ -353,7 +353,12 @@ struct KVTarget {
 
 int zero_vt_pad(hb_model* m, int B, int S, hipStream_t st);
 
-int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_tap) {
+// xn_ready: w.xn already holds RMSNorm1(x) (the previous layer's W2 produced
+// it). next_gamma != NULL: also leave RMSNorm(x_out, next_gamma) in w.xn for
+// the next layer (or the final norm); the norm is fused into the W2 split-K
+// reduction when that projection splits.
+int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_tap, bool xn_ready,
+              const float* next_gamma) {
   const hb_model_config& c = m->cfg;
   Workspace& w = m->ws;
   const LayerW& L = m->layers[l];
@@ -361,7 +366,7 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
   const int T = B * S, Sp = S_pad_of(S);
   const float alpha = alpha_of(c);
 
-  HIP_TRY(rmsnorm(w.x, c.dim, L.g1, T, c.dim, c.norm_eps, w.xn, nullptr, st));
+  if (!xn_ready) HIP_TRY(rmsnorm(w.x, c.dim, L.g1, T, c.dim, c.norm_eps, w.xn, nullptr, st));
   EpiQKV e{};
   e.q_dim = c.q_dim;
   e.kv_dim = c.kv_dim;
@@ -402,11 +407,15 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
   HIP_TRY(attention_prefill(a, st));
   GemmScratch so, s2;
   TRY(residual_scratch(m, c.dim, T, c.q_dim, so));
-  HIP_TRY(gemm_residual(L.wo, w.attn, c.dim, T, c.q_dim, EpiResidual{w.x, w.x2, c.dim, alpha}, &so, st));
-  HIP_TRY(rmsnorm(w.x2, c.dim, L.g2, T, c.dim, c.norm_eps, w.xn, nullptr, st));
+  HIP_TRY(gemm_residual_norm(L.wo, w.attn, c.dim, T, c.q_dim, EpiResidual{w.x, w.x2, c.dim, alpha},
+                             NormOut{L.g2, c.norm_eps, w.xn}, &so, st));
   HIP_TRY(gemm_swiglu(L.w13, w.xn, 2 * c.hidden, T, c.dim, EpiSwiGLU{w.gate, nullptr, c.hidden}, st));
   TRY(residual_scratch(m, c.dim, T, c.hidden, s2));
-  HIP_TRY(gemm_residual(L.w2, w.gate, c.dim, T, c.hidden, EpiResidual{w.x2, w.x, c.dim, alpha}, &s2, st));
+  const EpiResidual e2{w.x2, w.x, c.dim, alpha};
+  if (next_gamma)
+    HIP_TRY(gemm_residual_norm(L.w2, w.gate, c.dim, T, c.hidden, e2, NormOut{next_gamma, c.norm_eps, w.xn}, &s2, st));
+  else
+    HIP_TRY(gemm_residual(L.w2, w.gate, c.dim, T, c.hidden, e2, &s2, st));
   return HB_OK;
 }
 
@@ -791,8 +800,10 @@ static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint
   hipStream_t st = m->ctx->stream();
   HIP_TRY(embedding(m->embed, d_tokens, (int)T, c.dim, c.vocab, w.x, m->ctx->d_err, st));
   const KVTarget kv = scratch_kv(m, B, S);
-  for (int l = 0; l < c.nlayers; ++l) TRY(run_layer(m, l, B, S, kv, nullptr));
-  HIP_TRY(rmsnorm(w.x, c.dim, m->gamma_f, (int)T, c.dim, c.norm_eps, w.xn, nullptr, st));
+  // Each layer leaves the next norm (the final one after the last layer) in xn.
+  for (int l = 0; l < c.nlayers; ++l)
+    TRY(run_layer(m, l, B, S, kv, nullptr, l > 0,
+                  l + 1 < c.nlayers ? m->layers[l + 1].g1 : m->gamma_f));
   float* logits = d_logits ? d_logits : w.logits;
   HIP_TRY(gemm_logits(m->embed, w.xn, c.vocab, (int)T, c.dim, EpiLogits{logits, c.vocab, c.softcap}, st));
   if (d_targets) {
@@ -1220,7 +1231,9 @@ extern "C" int hb_prefill(hb_model* m, hb_kv* kv, const uint32_t* tokens, int S,
   hipStream_t st = m->ctx->stream();
   HIP_TRY(hipMemcpyAsync(w.tok, tokens, T * 4, hipMemcpyHostToDevice, st));
   HIP_TRY(embedding(m->embed, w.tok, (int)T, c.dim, c.vocab, w.x, m->ctx->d_err, st));
-  for (int l = 0; l < c.nlayers; ++l) TRY(run_layer(m, l, B, S, cache_target(kv, l), nullptr));
+  for (int l = 0; l < c.nlayers; ++l)
+    TRY(run_layer(m, l, B, S, cache_target(kv, l), nullptr, l > 0,
+                  l + 1 < c.nlayers ? m->layers[l + 1].g1 : nullptr));
   // Last position of each sequence -> logits and greedy token.
   HIP_TRY(rmsnorm(w.x + (size_t)(S - 1) * c.dim, (long)S * c.dim, m->gamma_f, B, c.dim, c.norm_eps,
                   kv->xn, nullptr, st));

@@ -36,6 +36,52 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
+// Split-K reduction fused with the RMSNorm that follows a residual projection
+// (cpu/rmsnorm.rs:149-183): one workgroup of 256 threads per token row adds the
+// splits in order, applies the residual epilogue (out = res + alpha * v), and
+// normalises the row into xn. The element-to-thread mapping and the block sum
+// are those of rmsnorm_kernel, so xn is bit-identical to reduce + rmsnorm.
+__global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __restrict__ P, int S,
+                                                                 int N, size_t stride,
+                                                                 EpiResidual e, NormOut no) {
+  constexpr int MAXS = GEMM_MAX_SPLITS;
+  __shared__ float red[4];
+  const int t = blockIdx.x;
+  const size_t row = (size_t)t * N;
+  float ss = 0.f;
+  for (int c = threadIdx.x * 4; c < N; c += 1024) {
+    f32x4 part[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s)
+      if (s < S) part[s] = *(const f32x4*)(P + s * stride + row + c);
+    f32x4 v = part[0];
+#pragma unroll
+    for (int s = 1; s < MAXS; ++s)
+      if (s < S) v += part[s];
+    const f32x4 r = *(const f32x4*)(e.res + row + c);
+    f32x4 y;
+    y.x = v.x * e.alpha + r.x;
+    y.y = v.y * e.alpha + r.y;
+    y.z = v.z * e.alpha + r.z;
+    y.w = v.w * e.alpha + r.w;
+    *(f32x4*)(e.out + row + c) = y;
+    ss += y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
+  }
+  ss = block_sum<4>(ss, red);
+  const float rinv = 1.0f / sqrtf(ss * (1.0f / (float)N) + no.eps);
+  f16* orow = no.xn + row;
+  for (int c = threadIdx.x * 4; c < N; c += 1024) {
+    const f32x4 y = *(const f32x4*)(e.out + row + c);  // this thread's own stores
+    const f32x4 g = *(const f32x4*)(no.gamma + c);
+    f16x4 o;
+    o.x = (f16)(y.x * rinv * g.x);
+    o.y = (f16)(y.y * rinv * g.y);
+    o.z = (f16)(y.z * rinv * g.z);
+    o.w = (f16)(y.w * rinv * g.w);
+    *(f16x4*)(orow + c) = o;
+  }
+}
+
 // Tile choice: maximise (relative per-tile throughput) x (fraction of the 256
 // CUs kept busy over the launch's rounds). Relative throughputs are measured
 // on MI355X with many rounds of tiles (7B shapes at 4096 tokens): 256x256
@@ -45,18 +91,21 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // this picks 192x256 for W1|W3 (230 tiles instead of 172) and 192x128 for
 // QKV (256 tiles instead of 192).
 //
-// Long-K problems with few 256x256 tiles (Wo and W2 at 512 tokens: 32 tiles)
-// instead split K over up to GEMM_MAX_SPLITS ranges of >= 8 slices so that
-// ~256 workgroups run the efficient 256x256 tile; the partials go through the
-// caller's scratch and splitk_reduce applies the epilogue.
+// Long-K problems with few output tiles (Wo and W2 at 512 tokens: 64 tiles of
+// 256x128) instead split K over up to GEMM_MAX_SPLITS ranges of >= 8 slices so
+// that ~256 workgroups run; the partials go through the caller's scratch and
+// splitk_reduce applies the epilogue. Measured at 512 tokens (GEMM + reduce):
+// Wo 36 us and W2 67 us with 256x128 x 4 splits, against 60 / 78 us with
+// 256x256 x 8 splits (short splits and twice the partial traffic) and 44 /
+// 106 us unsplit on 64x128 tiles.
 constexpr int GEMM_CUS = 256;  // MI355X compute units
 static long ntiles(int N, int T, int ft, int tt) { return (long)((N + ft - 1) / ft) * ((T + tt - 1) / tt); }
 
 int gemm_splits(int N, int T, int K) {
-  const long t256 = ntiles(N, T, 256, 256);
+  const long t = ntiles(N, T, 256, 128);
   const int nk = K / 64;
-  if (t256 >= 96 || nk < 32) return 1;
-  int S = (int)std::min<long>(GEMM_MAX_SPLITS, 256 / t256);
+  if (t >= GEMM_CUS / 2 || nk < 32) return 1;
+  int S = (int)std::min<long>(GEMM_MAX_SPLITS, GEMM_CUS / t);
   S = std::min(S, nk / 8);
   return S >= 2 ? S : 1;
 }
@@ -69,7 +118,7 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
   if (S > 1) {
     const size_t stride = (size_t)T * N;
     if (!scr->p || (size_t)S * stride > scr->floats) return hipErrorInvalidValue;
-    const hipError_t e = launch_tile<256, 256, 4, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
+    const hipError_t e = launch_tile<256, 128, 4, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
     if (e != hipSuccess) return e;
     const size_t n4 = stride / 4;
     const int grid = (int)std::min<size_t>((n4 + 255) / 256, 4096);
@@ -110,6 +159,22 @@ hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C,
 hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
                          const GemmScratch* scr, hipStream_t st) {
   return launch_gemm(W, X, N, T, K, e, scr, st);
+}
+hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
+                              const NormOut& no, const GemmScratch* scr, hipStream_t st) {
+  if (e.ld != N) return hipErrorInvalidValue;
+  const int S = scr ? gemm_splits(N, T, K) : 1;
+  if (S > 1) {
+    const size_t stride = (size_t)T * N;
+    if (!scr->p || (size_t)S * stride > scr->floats || (long)N * K >= (1L << 31)) return hipErrorInvalidValue;
+    const hipError_t err = launch_tile<256, 128, 4, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(splitk_reduce_norm_kernel, dim3(T), dim3(256), 0, st, scr->p, S, N, stride, e, no);
+    return hipGetLastError();
+  }
+  const hipError_t err = launch_gemm(W, X, N, T, K, e, nullptr, st);
+  if (err != hipSuccess) return err;
+  return rmsnorm(e.out, N, no.gamma, T, N, no.eps, no.xn, nullptr, st);
 }
 hipError_t gemm_swiglu(const f16* W, const f16* X, int N, int T, int K, const EpiSwiGLU& e,
                        hipStream_t st) {

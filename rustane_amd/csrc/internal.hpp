@@ -18,6 +18,15 @@ int gemm_splits(int N, int T, int K);
 hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st);
 hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
                          const GemmScratch* scr, hipStream_t st);
+// Residual projection followed by the RMSNorm of its output rows into xn
+// (fused into the split-K reduction when the shape splits).
+struct NormOut {
+  const float* gamma;
+  float eps;
+  f16* xn;  // [T, N]
+};
+hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
+                              const NormOut& no, const GemmScratch* scr, hipStream_t st);
 hipError_t gemm_swiglu(const f16* W, const f16* X, int N, int T, int K, const EpiSwiGLU& e,
                        hipStream_t st);
 hipError_t gemm_logits(const f16* W, const f16* X, int N, int T, int K, const EpiLogits& e,

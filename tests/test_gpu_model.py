@@ -80,6 +80,19 @@ def test_softcap_forward_matches_oracle(gpu):
     assert np.abs(res0.logits.reshape(-1) - raw["logits"].reshape(-1)).max() < LOGIT_ATOL
 
 
+def test_split_k_forward_matches_oracle(gpu):
+    """dim 2048 at 128 tokens: Wo (K = 2048) and W2 (K = 2048) have 8 output
+    tiles each, so both split K four ways and their reductions also produce
+    the following RMSNorm (norm2, the next layer's norm1, the final norm)."""
+    cfg = ModelConfig.make(dim=2048, hidden=2048, heads=16, nlayers=2, seq=128, vocab=256, hd=128)
+    w = ModelWeights.synthetic(cfg, seed=77, std=0.02)
+    k = CompiledKernels.compile(cfg)
+    err, rel, top1, res, ref = _compare_forward(cfg, w, k, B=1, S=cfg.seq, seed=9)
+    assert err < LOGIT_ATOL and rel < LOSS_RTOL and top1 >= TOP1_MIN
+    again = E.forward(cfg, k, w, *(lambda t: (t[:-1], t[1:]))(tokens_for(cfg, cfg.seq + 1, seed=9)))
+    np.testing.assert_array_equal(again.logits, res.logits.reshape(again.logits.shape))
+
+
 @pytest.fixture(scope="module")
 def m48(gpu):
     """The ~48M Llama-style workload: dim 512, SwiGLU 1536, 8 layers, 8x64 heads,
