@@ -9,6 +9,7 @@ static hipError_t launch_tile(const f16* W, const f16* X, int N, int T, int K, c
                               hipStream_t st, int splits = 1) {
   const int tiles = ((N + FT - 1) / FT) * ((T + TT - 1) / TT);
   const int nk = K / 64, kq = (nk + splits - 1) / splits;
+  if (nk < 1 || splits < 1 || (splits - 1) * kq >= nk) return hipErrorInvalidValue;  // empty split
   hipLaunchKernelGGL((gemm_nt_kernel<FT, TT, WF, WT, Epi>), dim3(tiles, splits), dim3(WF * WT * 64),
                      0, st, W, X, N, T, K, kq, epi);
   return hipGetLastError();
@@ -91,20 +92,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
 // this picks 192x256 for W1|W3 (230 tiles instead of 172) and 192x128 for
 // QKV (256 tiles instead of 192).
 //
-// Long-K problems with few output tiles (Wo and W2 at 512 tokens: 64 tiles of
-// 256x128) instead split K over up to GEMM_MAX_SPLITS ranges of >= 8 slices so
+// Long-K problems with few output tiles (Wo and W2 at 512 tokens: 128 tiles of
+// 128x128) instead split K over up to GEMM_MAX_SPLITS ranges of >= 8 slices so
 // that ~256 workgroups run; the partials go through the caller's scratch and
-// splitk_reduce applies the epilogue. Measured at 512 tokens (GEMM + reduce):
-// Wo 36 us and W2 67 us with 256x128 x 4 splits, against 60 / 78 us with
-// 256x256 x 8 splits (short splits and twice the partial traffic) and 44 /
-// 106 us unsplit on 64x128 tiles.
+// splitk_reduce applies the epilogue. Measured GEMM time at 512 tokens, 7B
+// shapes: Wo 25.5 us (128x128 x 2 splits) against 26.3 us (256x128 x 4) and
+// 32.6 us unsplit; W2 57.7 us (128x128 x 2) against 53.2 us (256x128 x 4) and
+// 79.5 us unsplit. Two splits halve the partial-sum traffic of the reduce.
 constexpr int GEMM_CUS = 256;  // MI355X compute units
 static long ntiles(int N, int T, int ft, int tt) { return (long)((N + ft - 1) / ft) * ((T + tt - 1) / tt); }
 
 int gemm_splits(int N, int T, int K) {
-  const long t = ntiles(N, T, 256, 128);
+  const long t = ntiles(N, T, 128, 128);
   const int nk = K / 64;
-  if (t >= GEMM_CUS / 2 || nk < 32) return 1;
+  if (t >= GEMM_CUS || nk < 32) return 1;
   int S = (int)std::min<long>(GEMM_MAX_SPLITS, GEMM_CUS / t);
   S = std::min(S, nk / 8);
   return S >= 2 ? S : 1;
@@ -118,7 +119,7 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
   if (S > 1) {
     const size_t stride = (size_t)T * N;
     if (!scr->p || (size_t)S * stride > scr->floats) return hipErrorInvalidValue;
-    const hipError_t e = launch_tile<256, 128, 4, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
+    const hipError_t e = launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
     if (e != hipSuccess) return e;
     const size_t n4 = stride / 4;
     const int grid = (int)std::min<size_t>((n4 + 255) / 256, 4096);
@@ -126,12 +127,16 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
                        stride, epi);
     return hipGetLastError();
   }
+  // rel: throughput per CU of each tile shape with every CU busy (7B shapes at
+  // 4096 tokens, time per full round of workgroups per tile area, 256x256 = 1);
+  // the score weighs it by the fraction of CU-rounds that hold a tile.
   struct Cand {
     int ft, tt;
     float rel;
   };
-  static constexpr Cand cands[] = {{256, 256, 1.00f}, {192, 256, 0.90f}, {192, 128, 0.85f},
-                                   {256, 128, 0.79f}, {128, 128, 0.77f}, {64, 128, 0.55f}};
+  static constexpr Cand cands[] = {{256, 256, 1.00f}, {192, 256, 0.93f}, {128, 256, 0.92f},
+                                   {192, 128, 0.88f}, {256, 128, 0.87f}, {128, 128, 0.77f},
+                                   {64, 128, 0.48f}};
   int best = 0;
   float best_score = -1.f;
   for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
@@ -144,11 +149,12 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
     }
   }
   switch (best) {
-    case 0: return launch_tile<256, 256, 4, 2>(W, X, N, T, K, epi, st);
-    case 1: return launch_tile<192, 256, 2, 4>(W, X, N, T, K, epi, st);
-    case 2: return launch_tile<192, 128, 2, 2>(W, X, N, T, K, epi, st);
-    case 3: return launch_tile<256, 128, 4, 2>(W, X, N, T, K, epi, st);
-    case 4: return launch_tile<128, 128, 2, 2>(W, X, N, T, K, epi, st);
+    case 0: return launch_tile<256, 256, 2, 2>(W, X, N, T, K, epi, st);
+    case 1: return launch_tile<192, 256, 2, 2>(W, X, N, T, K, epi, st);
+    case 2: return launch_tile<128, 256, 2, 2>(W, X, N, T, K, epi, st);
+    case 3: return launch_tile<192, 128, 2, 2>(W, X, N, T, K, epi, st);
+    case 4: return launch_tile<256, 128, 2, 2>(W, X, N, T, K, epi, st);
+    case 5: return launch_tile<128, 128, 2, 2>(W, X, N, T, K, epi, st);
     default: return launch_tile<64, 128, 2, 2>(W, X, N, T, K, epi, st);
   }
 }
@@ -167,7 +173,7 @@ hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, c
   if (S > 1) {
     const size_t stride = (size_t)T * N;
     if (!scr->p || (size_t)S * stride > scr->floats || (long)N * K >= (1L << 31)) return hipErrorInvalidValue;
-    const hipError_t err = launch_tile<256, 128, 4, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
+    const hipError_t err = launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(splitk_reduce_norm_kernel, dim3(T), dim3(256), 0, st, scr->p, S, N, stride, e, no);
     return hipGetLastError();

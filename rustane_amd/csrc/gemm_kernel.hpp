@@ -12,6 +12,8 @@
 // stored at c ^ swz(r), which keeps both the loaders' ds_write_b128 and the
 // MFMA operands' ds_read_b128 free of bank conflicts for 32- and 64-bank LDS.
 #pragma once
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace hb {
@@ -27,18 +29,20 @@ HB_DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Pipeline: slice k+1 of W and X is fetched into registers while the MFMAs
-// consume slice k from one of two LDS buffers (one barrier per 64-wide K
-// slice); the MFMA fragments of k-step s+1 are read from LDS while the MFMAs
-// of k-step s run. The loop body is a
-// single basic block (the next-slice load and store are unconditional; past
-// the last slice they re-read the last slice into the idle LDS buffer), and
-// sched_group_barrier fixes the order within it:
-//   global loads of slice k+1 | LDS reads of k-step 0 |
-//   for k-steps 0..2: MFMAs of step s interleaved one-to-one with the LDS
-//   reads of step s+1 | MFMAs of step 3 interleaved with the LDS writes of
-//   slice k+1.
-// so LDS latency is always covered by MFMAs of the previous k-step.
+// Pipeline: two 64-wide K slices are in flight in registers while the MFMAs
+// consume a third from LDS. Iteration k computes slice k from LDS buffer k&1,
+// issues the global loads of slice k+2 into register set k&1 and writes slice
+// k+1 (register set (k+1)&1, loaded one iteration earlier) into LDS buffer
+// (k+1)&1; one barrier per slice. The loop is unrolled by two so that both
+// register sets have static names. Within an iteration sched_group_barrier
+// fixes the order: LDS reads of k-step 0 first, then every MFMA is followed by
+// one LDS read of the next k-step (k-steps 0..2), and the global loads are
+// spread one per MFMA over k-steps 0..2 while the LDS writes are spread over
+// k-steps 1..3. Issuing the loads or the writes as a burst stalls the
+// wave's in-order issue behind the memory queues and leaves the MFMA pipe idle
+// (one wave per SIMD has nothing else to issue).
+// Past the last slice the loads re-read the last slice (clamped), so every
+// iteration has the same shape.
 //
 // Split-K: blockIdx.y selects one of gridDim.y contiguous ranges of 64-wide K
 // slices (kq slices each, the last one shorter); with gridDim.y = 1 the range
@@ -56,6 +60,7 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   static_assert(FM >= 1 && TM >= 1, "wave tile must be at least 32x32");
   static_assert(WL * NT == FT * 8 && XL * NT == TT * 8, "loader coverage");
   static_assert(RSTEP % 16 == 0, "loader passes must keep the LDS swizzle phase");
+  static_assert(NLD <= 3 * 3 * NMF, "at most three global loads per MFMA slot");
 
   __shared__ f16x8 sW[2][FT * 8];
   __shared__ f16x8 sX[2][TT * 8];
@@ -77,18 +82,22 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
 #pragma unroll
   for (int i = 0; i < XL; ++i) xoff[i] = min(t_base + r0 + RSTEP * i, T - 1) * K;
 
-  f16x8 wreg[WL], xreg[XL];
-  auto gload = [&](int k0) {
+  using R0 = std::integral_constant<int, 0>;
+  using R1 = std::integral_constant<int, 1>;
+  f16x8 wreg[2][WL], xreg[2][XL];
+  auto gload = [&](auto rs, int k0) {
+    constexpr int R = decltype(rs)::value;
 #pragma unroll
-    for (int i = 0; i < WL; ++i) wreg[i] = *(const f16x8*)(wb + woff[i] + k0);
+    for (int i = 0; i < WL; ++i) wreg[R][i] = *(const f16x8*)(wb + woff[i] + k0);
 #pragma unroll
-    for (int i = 0; i < XL; ++i) xreg[i] = *(const f16x8*)(xb + xoff[i] + k0);
+    for (int i = 0; i < XL; ++i) xreg[R][i] = *(const f16x8*)(xb + xoff[i] + k0);
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](auto rs) {
+    constexpr int R = decltype(rs)::value;
 #pragma unroll
-    for (int i = 0; i < WL; ++i) sW[buf][ldst + RSTEP * 8 * i] = wreg[i];
+    for (int i = 0; i < WL; ++i) sW[R][ldst + RSTEP * 8 * i] = wreg[R][i];
 #pragma unroll
-    for (int i = 0; i < XL; ++i) sX[buf][ldst + RSTEP * 8 * i] = xreg[i];
+    for (int i = 0; i < XL; ++i) sX[R][ldst + RSTEP * 8 * i] = xreg[R][i];
   };
 
   f32x16 acc[FM][TM];
@@ -121,40 +130,57 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
 
   const int kt0 = blockIdx.y * kq;
   const int nk = min(kq, K / 64 - kt0);
-  gload(kt0 * 64);
-  sstore(0);
-  lds_barrier();
+  auto kslice = [&](int i) { return (kt0 + min(i, nk - 1)) * 64; };
   Frag F0, F1;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    gload((kt0 + min(kt + 1, nk - 1)) * 64);
-    fread(F0, cur, 0);
-    fread(F1, cur, 1);
+  auto iter = [&](auto rs, int kt) {
+    constexpr int R = decltype(rs)::value;
+    gload(rs, kslice(kt + 2));
+    fread(F0, R, 0);
+    fread(F1, R, 1);
     mfmas(F0);
-    fread(F0, cur, 2);
+    fread(F0, R, 2);
     mfmas(F1);
-    fread(F1, cur, 3);
+    fread(F1, R, 3);
     mfmas(F0);
     mfmas(F1);
-    sstore(cur ^ 1);
-    // schedule: loads, step-0 reads, then MFMA/read pairs, then MFMA/write pairs
-    __builtin_amdgcn_sched_group_barrier(0x020, NLD, 0);  // VMEM read
-    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // DS read (step 0)
+    sstore(std::integral_constant<int, R ^ 1>{});
+    // MFMA slot s = 0..4*NMF-1 in issue order
+    constexpr int NSLOT = 4 * NMF, GSLOTS = 3 * NMF, WSLOTS = 3 * NMF;
+    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // DS read, k-step 0
 #pragma unroll
-    for (int s = 0; s < 3; ++s) {
-#pragma unroll
-      for (int m = 0; m < NMF; ++m) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
-        if (m < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    for (int s = 0; s < NSLOT; ++s) {
+      const int m = s % NMF;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (s < 3 * NMF && m < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (s < GSLOTS) {
+        const int g = (s + 1) * NLD / GSLOTS - s * NLD / GSLOTS;
+        if (g == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+        if (g == 2) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+        if (g == 3) __builtin_amdgcn_sched_group_barrier(0x020, 3, 0);
+      }
+      if (s >= NMF) {
+        const int q = s - NMF;
+        const int w = (q + 1) * NLD / WSLOTS - q * NLD / WSLOTS;
+        if (w == 1) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+        if (w == 2) __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+        if (w == 3) __builtin_amdgcn_sched_group_barrier(0x200, 3, 0);
       }
     }
-#pragma unroll
-    for (int m = 0; m < NMF; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // MFMA
-      if (m < NLD) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-    }
     lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // nk >= 1 for every split (the launcher checks (splits - 1) * kq < K / 64)
+  gload(R0{}, kslice(0));
+  gload(R1{}, kslice(1));
+  sstore(R0{});
+  lds_barrier();
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    iter(R0{}, kt);
+    iter(R1{}, kt + 1);
   }
+  if (kt < nk) iter(R0{}, kt);
 
 #pragma unroll
   for (int i = 0; i < FM; ++i)
