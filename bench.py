@@ -277,7 +277,7 @@ def time_dominant_kernel(k, cfg, T, launches, stream):
         f"{achieved:.1f} TFLOP/s ({achieved/2500*100:.1f}% of dense fp16 peak)")
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": 2500.0, "unit": "TFLOP/s",
                 "frac": round(achieved / 2500.0, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
-                "kernel": "gemm_nt_kernel<192,256,2,4,EpiSwiGLU> (FFN up, W1|W3 + SwiGLU)",
+                "kernel": "gemm_nt_kernel<192,256,2,2,EpiSwiGLU> (FFN up, W1|W3 + SwiGLU)",
                 "flop_per_launch": up_flops, "us_per_launch": round(up_ms * 1e3, 2)}
     return roofline, up_ms
 

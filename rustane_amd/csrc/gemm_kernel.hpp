@@ -20,6 +20,16 @@ namespace hb {
 
 HB_DEV int lds_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled by the template
+// expansion itself.
+template <int B, int E, class F>
+HB_DEV void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // LDS-only workgroup barrier: orders LDS accesses of the workgroup without
 // draining outstanding global loads (a full __syncthreads would wait for the
 // prefetches that are meant to stay in flight across it).
@@ -182,24 +192,24 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   }
   if (kt < nk) iter(R0{}, kt);
 
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < TM; ++j) {
-      const int t = t_base + wt * WTT + j * 32 + (lane & 31);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int f = f_base + wf * WFT + i * 32 + 8 * g + 4 * khalf;
-        if (t < T && f < N) {
-          f32x4 v;
-          v.x = acc[i][j][4 * g + 0];
-          v.y = acc[i][j][4 * g + 1];
-          v.z = acc[i][j][4 * g + 2];
-          v.w = acc[i][j][4 * g + 3];
-          epi(t, f, v);
-        }
-      }
+  // Epilogue over the FM x TM x 4 accumulator quads as straight-line code: a
+  // loop would be left rolled once the epilogue body is large (EpiQKV on
+  // 256x256 tiles), and indexing acc with a loop counter moves the whole
+  // accumulator array to scratch memory.
+  static_for<0, FM * TM * 4>([&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    constexpr int i = q / (TM * 4), j = (q / 4) % TM, g = q % 4;
+    const int t = t_base + wt * WTT + j * 32 + (lane & 31);
+    const int f = f_base + wf * WFT + i * 32 + 8 * g + 4 * khalf;
+    if (t < T && f < N) {
+      f32x4 v;
+      v.x = acc[i][j][4 * g + 0];
+      v.y = acc[i][j][4 * g + 1];
+      v.z = acc[i][j][4 * g + 2];
+      v.w = acc[i][j][4 * g + 3];
+      epi(t, f, v);
     }
+  });
 }
 
 }  // namespace hb
