@@ -8,13 +8,14 @@
 namespace hb {
 
 // ---- prefill: one workgroup of PW waves per (32 queries, head, sequence) --------
-// S^T = K · Q^T on v_mfma_f32_32x32x16_f16 (rows = keys, cols = queries): lane l
-// owns query l%32 and keys 8*(r/4) + 4*(l/32) + r%4 of the 32-key block, so the
-// online-softmax statistics of a query live in one lane pair (l, l^32).
-// O^T = V^T · P^T reuses the score registers as the B operand: with the key
-// order permuted identically on both operands, lane half h supplies keys
-// {16j+4h..16j+4h+3, 16j+8+4h..16j+8+4h+3} for k-step j — exactly the registers
-// 8j..8j+7 it already holds — and the A operand reads those keys from V^T.
+// S^T = K · Q^T on v_mfma_f32_32x32x16_f16 (rows = key slots, cols = queries):
+// lane l owns query l%32 and the key slots 8*(r/4) + 4*(l/32) + r%4 of the
+// 32-key block, so the online-softmax statistics of a query live in one lane
+// pair (l, l^32). Key slot R holds key swap23(R) (bits 2 and 3 of the slot
+// swapped), which makes the 8 score registers 8j..8j+7 of lane half h the
+// consecutive keys 16j+8h .. 16j+8h+7. O^T = V^T · P^T then reuses those
+// registers as the B operand, and the A operand (V^T row, the same 8 keys) is
+// one 16-byte read.
 //
 // The causal key range of a query block is split over the PW waves of the
 // workgroup (wave w takes key blocks w, w+PW, ...), so the longest chain of
@@ -22,14 +23,37 @@ namespace hb {
 // in flight; each wave keeps its own online-softmax state and waves 1..PW-1
 // hand theirs to wave 0 through LDS for one weighted merge (the same
 // rescaling an online softmax applies between blocks).
+//
+// Each wave stages its key block (K [32][hd] and V^T [hd][32]) in its own LDS
+// region: the global loads are 16 bytes per lane and 1 KB contiguous per wave
+// instruction for K (64 B per V^T row), issued one block ahead into registers,
+// and the MFMA fragments are read from XOR-swizzled LDS without bank
+// conflicts. (Fragment loads straight from global memory touch 32 cache lines
+// per wave instruction, and the L1's tag rate then bounds the kernel.) Only
+// the owning wave touches its region, so no workgroup barrier is needed
+// inside the loop; a wave's LDS operations execute in order.
 constexpr int PW = 4;
 
+HB_DEV int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+
+// Orders this wave's LDS accesses around a cross-lane LDS hand-off: waits for
+// its outstanding LDS operations and keeps the compiler from moving memory
+// accesses across.
+HB_DEV void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 template <int HD>
-__global__ __launch_bounds__(PW * 64) void attn_prefill_kernel(AttnPrefill p) {
-  constexpr int KS = HD / 16;  // k-steps over head dim
-  constexpr int MB = HD / 32;  // 32-row blocks of O^T
-  __shared__ float s_o[PW - 1][MB * 16][64];
+__global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p) {
+  constexpr int KS = HD / 16;   // k-steps over head dim
+  constexpr int MB = HD / 32;   // 32-row blocks of O^T
+  constexpr int NCH = HD / 8;   // 16-byte chunks per K row
+  constexpr int KT8 = 4 * HD;   // 16-byte chunks per K tile (= per V^T tile)
+  constexpr int NLD = HD / 16;  // 16-byte loads per lane per tile
+  // per wave: K tile (row r, chunk c at r*NCH + (c ^ (swap23(r) % NCH))), then
+  // the V^T tile (row e, chunk c at KT8 + e*4 + (c ^ ((e >> 2) & 3))); after the
+  // loop the same region holds the wave's unnormalised O for the merge
+  __shared__ f16x8 s_kv[PW][2 * KT8];
   __shared__ float s_ml[PW - 1][2][64];
+  static_assert(2 * KT8 * 16 >= MB * 16 * 64 * 4, "merge buffer fits in a wave's tiles");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, li = lane & 31;
   const int nqb = (p.S + 31) / 32;
   const int qb = nqb - 1 - blockIdx.x;  // heaviest blocks first
@@ -46,24 +70,56 @@ __global__ __launch_bounds__(PW * 64) void attn_prefill_kernel(AttnPrefill p) {
   const f16* kbase = p.k + b * p.k_bstride + kvh * p.k_hstride;
   const f16* vbase = p.vt + ((size_t)b * p.KVH + kvh) * HD * p.vt_ld;
   const float sl2 = p.scale * HB_LOG2E;
+  f16x8* sk = s_kv[wave];
+  f16x8* sv = s_kv[wave] + KT8;
+
+  f16x8 kreg[NLD], vreg[NLD];
+  auto gload = [&](int kb) {
+    const f16* kt = kbase + (size_t)kb * 32 * HD;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) kreg[i] = *(const f16x8*)(kt + (i * 64 + lane) * 8);
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int e = (i * 64 + lane) >> 2, c = lane & 3;
+      vreg[i] = *(const f16x8*)(vbase + (size_t)e * p.vt_ld + kb * 32 + c * 8);
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int x = i * 64 + lane, r = x / NCH, c = x % NCH;
+      sk[r * NCH + (c ^ (swap23(r) % NCH))] = kreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int x = i * 64 + lane, e = x >> 2, c = x & 3;
+      sv[e * 4 + (c ^ ((e >> 2) & 3))] = vreg[i];
+    }
+  };
 
   f32x16 o[MB];
 #pragma unroll
   for (int m = 0; m < MB; ++m) o[m] = f32x16{};
   float mrun = -INFINITY, lrun = 0.f;
 
+  const int krow = swap23(li);  // key held in this lane's slot
+  if (wave <= qb) gload(wave);
   for (int kb = wave; kb <= qb; kb += PW) {
-    const f16* kp = kbase + (size_t)(kb * 32 + li) * HD + 8 * h2;
+    wave_lds_sync();  // the previous block's fragment reads are done
+    lstore();
+    wave_lds_sync();  // the tiles are in LDS
+    if (kb + PW <= qb) gload(kb + PW);
+
     f32x16 s = {};
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      const f16x8 kf = *(const f16x8*)(kp + 16 * j);
+      const f16x8 kf = sk[krow * NCH + ((2 * j + h2) ^ (li % NCH))];
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[j], s, 0, 0, 0);
     }
     float mloc = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int key = kb * 32 + 8 * (r >> 2) + 4 * h2 + (r & 3);
+      const int key = kb * 32 + swap23(8 * (r >> 2) + 4 * h2 + (r & 3));
       float v = s[r] * sl2;
       if (kb == qb && key > qi) v = -INFINITY;
       s[r] = v;
@@ -94,12 +150,8 @@ __global__ __launch_bounds__(PW * 64) void attn_prefill_kernel(AttnPrefill p) {
       for (int i = 0; i < 8; ++i) pb[i] = (f16)s[8 * j + i];
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
-        const f16* vp = vbase + (size_t)(m * 32 + li) * p.vt_ld + kb * 32 + 16 * j + 4 * h2;
-        const f16x4 lo = *(const f16x4*)vp;
-        const f16x4 hi = *(const f16x4*)(vp + 8);
-        f16x8 va;
-        va[0] = lo[0]; va[1] = lo[1]; va[2] = lo[2]; va[3] = lo[3];
-        va[4] = hi[0]; va[5] = hi[1]; va[6] = hi[2]; va[7] = hi[3];
+        const int e = m * 32 + li;
+        const f16x8 va = sv[e * 4 + ((2 * j + h2) ^ ((e >> 2) & 3))];
         o[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[m], 0, 0, 0);
       }
     }
@@ -107,12 +159,15 @@ __global__ __launch_bounds__(PW * 64) void attn_prefill_kernel(AttnPrefill p) {
 
   // Waves 1..PW-1 hand (o, m, l) to wave 0 (a wave with no key block has
   // m = -inf and weight 0). Lane l of every wave holds the same (query, row)
-  // slots, so the exchange is one float per lane per register.
+  // slots, so the exchange is one float per lane per register; each wave
+  // writes its O into its own (now idle) tile region.
+  float* s_o = (float*)s_kv[wave];  // [MB*16][64]
   if (wave > 0) {
+    wave_lds_sync();
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s_o[wave - 1][m * 16 + r][lane] = o[m][r];
+      for (int r = 0; r < 16; ++r) s_o[(m * 16 + r) * 64 + lane] = o[m][r];
     s_ml[wave - 1][0][lane] = mrun;
     s_ml[wave - 1][1][lane] = lrun;
   }
@@ -131,11 +186,12 @@ __global__ __launch_bounds__(PW * 64) void attn_prefill_kernel(AttnPrefill p) {
   for (int w = 0; w < PW - 1; ++w) {
     const float mw = s_ml[w][0][lane];
     const float cw = mw == -INFINITY ? 0.f : exp2f(mw - M);
+    const float* ow = (const float*)s_kv[w + 1];
     L += cw * s_ml[w][1][lane];
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[m][r] += cw * s_o[w][m * 16 + r][lane];
+      for (int r = 0; r < 16; ++r) o[m][r] += cw * ow[(m * 16 + r) * 64 + lane];
   }
 
   if (qi < p.S) {

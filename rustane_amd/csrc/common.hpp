@@ -16,6 +16,20 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // 1/ln(2): softmax is evaluated as exp2((s - m) * log2(e)).
 #define HB_LOG2E 1.4426950408889634f
 
+// n / d for 0 <= n < 2^31 and a divisor d >= 1 fixed at launch, by
+// multiply-high (division by invariant integers, Granlund & Montgomery 1994):
+//   s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1, q = (mulhi(n, m) + n) >> s.
+// n + mulhi(n, m) < 2^32 because m < 2^32 and n < 2^31.
+struct FastDiv {
+  uint32_t d = 1, m = 1, s = 0;
+  FastDiv() = default;
+  __host__ explicit FastDiv(uint32_t dd) : d(dd) {
+    while ((1ull << s) < dd) ++s;
+    m = (uint32_t)(((1ull << 32) * ((1ull << s) - dd)) / dd + 1);
+  }
+  HB_DEV int div(int n) const { return (int)((__umulhi((uint32_t)n, m) + (uint32_t)n) >> s); }
+};
+
 // Wave-wide reductions (64 lanes). __shfl_xor lowers to DPP / ds_swizzle.
 HB_DEV float wave_sum(float v) {
 #pragma unroll

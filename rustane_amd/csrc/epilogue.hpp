@@ -29,24 +29,26 @@ struct EpiSplit {
 };
 
 // out = res + alpha * v (fp32 residual stream). woFwd + vsma (layer.rs:784) and
-// the ffnFused residual (kernels/ffn_fused.rs:74-77).
+// the ffnFused residual (kernels/ffn_fused.rs:74-77). The prefill GEMM loads
+// the residual quads (load) for a group of quads before storing any of them;
+// res may be the same buffer as out.
 struct EpiResidual {
   const float* res;
   float* out;
   int ld;
   float alpha;
-  HB_DEV void operator()(int t, int f0, f32x4 v) const {
-    const size_t o = (size_t)t * ld + f0;
-    const f32x4 r = *(const f32x4*)(res + o);
+  using Aux = f32x4;
+  HB_DEV f32x4 load(int t, int f0) const { return *(const f32x4*)(res + (size_t)t * ld + f0); }
+  HB_DEV void operator()(int t, int f0, f32x4 v, const f32x4& r) const {
     f32x4 y;
     y.x = v.x * alpha + r.x;
     y.y = v.y * alpha + r.y;
     y.z = v.z * alpha + r.z;
     y.w = v.w * alpha + r.w;
-    *(f32x4*)(out + o) = y;
+    *(f32x4*)(out + (size_t)t * ld + f0) = y;
   }
+  HB_DEV void operator()(int t, int f0, f32x4 v) const { (*this)(t, f0, v, load(t, f0)); }
 };
-
 
 // W1 and W3 are packed row-interleaved in groups of four: packed rows 4j..4j+3
 // are W1 column 2j, W1 column 2j+1, W3 column 2j, W3 column 2j+1. A lane's
@@ -121,28 +123,52 @@ struct EpiQKV {
   f16* vt;
   int vt_ld;
   float* tap;  // nullable [T, q+2kv] fp32 = Q_rope | K_rope | V
+  FastDiv div_S, div_hd;  // by S and hd; set by prepare() on the host
 
-  HB_DEV void operator()(int t, int f0, f32x4 v4) const {
-    int b, s;
+  __host__ void prepare() {
+    div_S = FastDiv((uint32_t)S);
+    div_hd = FastDiv((uint32_t)hd);
+  }
+  HB_DEV void pos_of(int t, int& b, int& s) const {
     if (d_pos) {
       b = t;
       s = *d_pos;
     } else {
-      b = t / S;
+      b = div_S.div(t);
       s = t - b * S;
     }
+  }
+  // RoPE (cos, sin) of the feature pairs (f0, f0+1) and (f0+2, f0+3) of token
+  // t; unused for V features.
+  struct Aux {
+    float2 c0, c1;
+  };
+  HB_DEV Aux load(int t, int f0) const {
+    Aux a{};
+    if (f0 < q_dim + kv_dim) {
+      int b, s;
+      pos_of(t, b, s);
+      const int f = f0 < q_dim ? f0 : f0 - q_dim;
+      const int e = f - div_hd.div(f) * hd;
+      const float2* rp = rope + (size_t)s * (hd >> 1) + (e >> 1);
+      a.c0 = rp[0];
+      a.c1 = rp[1];
+    }
+    return a;
+  }
+  HB_DEV void operator()(int t, int f0, f32x4 v4, const Aux& a) const {
+    int b, s;
+    pos_of(t, b, s);
     const int qkv = q_dim + 2 * kv_dim;
     if (f0 < q_dim + kv_dim) {
       const bool isq = f0 < q_dim;
       const int f = isq ? f0 : f0 - q_dim;
-      const int h = f / hd, e = f - h * hd;
-      const float2* rp = rope + (size_t)s * (hd >> 1) + (e >> 1);
-      const float2 c0 = rp[0], c1 = rp[1];
+      const int h = div_hd.div(f), e = f - h * hd;
       f32x4 o;
-      o.x = v4.x * c0.x - v4.y * c0.y;
-      o.y = v4.y * c0.x + v4.x * c0.y;
-      o.z = v4.z * c1.x - v4.w * c1.y;
-      o.w = v4.w * c1.x + v4.z * c1.y;
+      o.x = v4.x * a.c0.x - v4.y * a.c0.y;
+      o.y = v4.y * a.c0.x + v4.x * a.c0.y;
+      o.z = v4.z * a.c1.x - v4.w * a.c1.y;
+      o.w = v4.w * a.c1.x + v4.z * a.c1.y;
       f16x4 oh;
       oh.x = (f16)o.x;
       oh.y = (f16)o.y;
@@ -157,7 +183,7 @@ struct EpiQKV {
       if (tap) *(f32x4*)(tap + (size_t)t * qkv + f0) = o;
     } else {
       const int f = f0 - q_dim - kv_dim;
-      const int h = f / hd, e = f - h * hd;
+      const int h = div_hd.div(f), e = f - h * hd;
       f16x4 vh;
       vh.x = (f16)v4.x;
       vh.y = (f16)v4.y;
@@ -174,6 +200,7 @@ struct EpiQKV {
       if (tap) *(f32x4*)(tap + (size_t)t * qkv + f0) = v4;
     }
   }
+  HB_DEV void operator()(int t, int f0, f32x4 v4) const { (*this)(t, f0, v4, load(t, f0)); }
 };
 
 }  // namespace hb

@@ -192,7 +192,10 @@ hipError_t gemm_logits(const f16* W, const f16* X, int N, int T, int K, const Ep
 }
 hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQKV& e,
                     hipStream_t st) {
-  return launch_gemm(W, X, N, T, K, e, nullptr, st);
+  if (e.S < 1 || e.hd < 1) return hipErrorInvalidValue;
+  EpiQKV ep = e;
+  ep.prepare();
+  return launch_gemm(W, X, N, T, K, ep, nullptr, st);
 }
 
 }  // namespace hb

@@ -30,6 +30,21 @@ HB_DEV void static_for(F&& f) {
   }
 }
 
+// Epilogues that read memory declare `Aux`, `Aux load(t, f0)` and
+// `operator()(t, f0, v, aux)`; the others only `operator()(t, f0, v)`.
+template <class E, class = void>
+struct EpiAux {
+  struct type {};
+  static HB_DEV type load(const E&, int, int) { return {}; }
+  static HB_DEV void apply(const E& e, int t, int f0, f32x4 v, const type&) { e(t, f0, v); }
+};
+template <class E>
+struct EpiAux<E, std::void_t<typename E::Aux>> {
+  using type = typename E::Aux;
+  static HB_DEV type load(const E& e, int t, int f0) { return e.load(t, f0); }
+  static HB_DEV void apply(const E& e, int t, int f0, f32x4 v, const type& a) { e(t, f0, v, a); }
+};
+
 // LDS-only workgroup barrier: orders LDS accesses of the workgroup without
 // draining outstanding global loads (a full __syncthreads would wait for the
 // prefetches that are meant to stay in flight across it).
@@ -195,20 +210,40 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   // Epilogue over the FM x TM x 4 accumulator quads as straight-line code: a
   // loop would be left rolled once the epilogue body is large (EpiQKV on
   // 256x256 tiles), and indexing acc with a loop counter moves the whole
-  // accumulator array to scratch memory.
-  static_for<0, FM * TM * 4>([&](auto qc) {
-    constexpr int q = decltype(qc)::value;
-    constexpr int i = q / (TM * 4), j = (q / 4) % TM, g = q % 4;
-    const int t = t_base + wt * WTT + j * 32 + (lane & 31);
-    const int f = f_base + wf * WFT + i * 32 + 8 * g + 4 * khalf;
-    if (t < T && f < N) {
-      f32x4 v;
-      v.x = acc[i][j][4 * g + 0];
-      v.y = acc[i][j][4 * g + 1];
-      v.z = acc[i][j][4 * g + 2];
-      v.w = acc[i][j][4 * g + 3];
-      epi(t, f, v);
-    }
+  // accumulator array to scratch memory. Epilogues that read memory (the
+  // residual stream, the RoPE table) load the quads of accumulator row i+1
+  // before the quads of row i are stored: their loads cannot be moved above
+  // stores that might alias them, so a load-store-load chain per quad would
+  // expose the load latency once per quad.
+  using AX = EpiAux<Epi>;
+  typename AX::type aux[2][TM * 4];
+  auto tok = [&](int j) { return t_base + wt * WTT + j * 32 + (lane & 31); };
+  auto feat = [&](int i, int g) { return f_base + wf * WFT + i * 32 + 8 * g + 4 * khalf; };
+  auto load_row = [&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    static_for<0, TM * 4>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const int t = tok(q / 4), f = feat(i, q % 4);
+      if (t < T && f < N) aux[i & 1][q] = AX::load(epi, t, f);
+    });
+  };
+  load_row(std::integral_constant<int, 0>{});
+  static_for<0, FM>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    if constexpr (i + 1 < FM) load_row(std::integral_constant<int, i + 1>{});
+    static_for<0, TM * 4>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      constexpr int j = q / 4, g = q % 4;
+      const int t = tok(j), f = feat(i, g);
+      if (t < T && f < N) {
+        f32x4 v;
+        v.x = acc[i][j][4 * g + 0];
+        v.y = acc[i][j][4 * g + 1];
+        v.z = acc[i][j][4 * g + 2];
+        v.w = acc[i][j][4 * g + 3];
+        AX::apply(epi, t, f, v, aux[i & 1][q]);
+      }
+    });
   });
 }
 

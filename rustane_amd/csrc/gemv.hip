@@ -338,7 +338,10 @@ hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, in
 }
 hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                     const EpiQKV& e, hipStream_t st) {
-  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st);
+  if (e.S < 1 || e.hd < 1) return hipErrorInvalidValue;
+  EpiQKV ep = e;
+  ep.prepare();
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, ep, st);
 }
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st) {
   return launch_gemv(Wt, X, nullptr, nullptr, N, B, K, EpiStore{C, N}, st);
