@@ -189,7 +189,9 @@ int validate_config(const hb_model_config& c) {
 }
 
 // RoPE table exactly as kernels/sdpa_fwd.rs:18-33 computes it:
-// theta = p / base^(2i/hd) in f32; (cos, sin) per (p, i).
+// theta = p / base^(2i/hd) in f32; (cos, sin) per (i, p), stored pair-major
+// [hd/2][len] so that consecutive positions of one pair are adjacent (the
+// prefill GEMM epilogue reads one pair for 32 consecutive tokens at a time).
 int ensure_rope(hb_model* m, int len) {
   if (len <= m->rope_len) return HB_OK;
   const int half = m->cfg.hd / 2;
@@ -198,7 +200,7 @@ int ensure_rope(hb_model* m, int len) {
     for (int i = 0; i < half; ++i) {
       const float theta =
           (float)p / powf(m->cfg.rope_theta, 2.0f * (float)i / (float)m->cfg.hd);
-      tab[(size_t)p * half + i] = make_float2(cosf(theta), sinf(theta));
+      tab[(size_t)i * len + p] = make_float2(cosf(theta), sinf(theta));
     }
   HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
   if (m->rope) HIP_TRY(hipFree(m->rope));
@@ -375,6 +377,7 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
   e.heads = c.heads;
   e.kv_heads = c.kv_heads;
   e.rope = m->rope;
+  e.rope_ld = m->rope_len;
   e.d_pos = nullptr;
   e.q = w.q;
   e.q_rows = Sp;
@@ -891,7 +894,8 @@ extern "C" int hb_op_sdpa_fwd(hb_model* m, int layer, const void* xnorm, int B, 
   const KVTarget kv = scratch_kv(m, B, S);
   EpiQKV e{};
   e.q_dim = c.q_dim; e.kv_dim = c.kv_dim; e.hd = c.hd; e.S = S; e.heads = c.heads;
-  e.kv_heads = c.kv_heads; e.rope = m->rope; e.d_pos = nullptr; e.q = w.q; e.q_rows = Sp;
+  e.kv_heads = c.kv_heads; e.rope = m->rope; e.rope_ld = m->rope_len; e.d_pos = nullptr;
+  e.q = w.q; e.q_rows = Sp;
   e.k = kv.k; e.k_bstride = kv.k_bstride; e.k_hstride = kv.k_hstride; e.v = nullptr;
   e.vt = w.vt; e.vt_ld = Sp; e.tap = qkv_tap;
   HIP_TRY(gemm_qkv(m->layers[layer].wqkv, (const f16*)xnorm, c.q_dim + 2 * c.kv_dim, T, c.dim, e, st));
@@ -1026,7 +1030,8 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     HIP_TRY(prep_norm(kv->x, L.g1, n1));
     EpiQKV e{};
     e.q_dim = c.q_dim; e.kv_dim = c.kv_dim; e.hd = c.hd; e.S = 1; e.heads = c.heads;
-    e.kv_heads = c.kv_heads; e.rope = m->rope; e.d_pos = kv->d_pos; e.q = kv->qd; e.q_rows = 1;
+    e.kv_heads = c.kv_heads; e.rope = m->rope; e.rope_ld = m->rope_len; e.d_pos = kv->d_pos;
+    e.q = kv->qd; e.q_rows = 1;
     e.k = t.k; e.k_bstride = t.k_bstride; e.k_hstride = t.k_hstride;
     e.v = t.v; e.v_bstride = t.v_bstride; e.v_hstride = t.v_hstride; e.vt = nullptr; e.vt_ld = 0;
     e.tap = nullptr;

@@ -38,8 +38,8 @@ struct EpiResidual {
   int ld;
   float alpha;
   using Aux = f32x4;
-  HB_DEV f32x4 load(int t, int f0) const { return *(const f32x4*)(res + (size_t)t * ld + f0); }
-  HB_DEV void operator()(int t, int f0, f32x4 v, const f32x4& r) const {
+  HB_DEV f32x4 load(int t, int f0, int = 0) const { return *(const f32x4*)(res + (size_t)t * ld + f0); }
+  HB_DEV void operator()(int t, int f0, f32x4 v, const f32x4& r, int = 0) const {
     f32x4 y;
     y.x = v.x * alpha + r.x;
     y.y = v.y * alpha + r.y;
@@ -108,7 +108,8 @@ struct EpiLogits {
 // position *d_pos of sequence b = t (decode, S = 1, pos0 read from d_pos).
 struct EpiQKV {
   int q_dim, kv_dim, hd, S, heads, kv_heads;
-  const float2* rope;  // [pos][hd/2] (cos, sin)
+  const float2* rope;  // [hd/2][rope_ld] (cos, sin), pair-major
+  int rope_ld;         // positions per pair row
   const int* d_pos;    // decode: position of the current token; prefill: NULL
   // Q: q[((b*heads + h)*q_rows + s)*hd + e]
   f16* q;
@@ -138,69 +139,80 @@ struct EpiQKV {
       s = t - b * S;
     }
   }
+  // fb is the start of the 32-feature block that holds f0. The Q/K/V and head
+  // boundaries are multiples of 32, so the region and the head follow from fb;
+  // the prefill GEMM passes it as a wave-uniform value, which turns every
+  // branch below into a scalar one.
+  HB_DEV int region_start(int fb) const {
+    return fb < q_dim ? 0 : fb < q_dim + kv_dim ? q_dim : q_dim + kv_dim;
+  }
   // RoPE (cos, sin) of the feature pairs (f0, f0+1) and (f0+2, f0+3) of token
   // t; unused for V features.
   struct Aux {
     float2 c0, c1;
   };
-  HB_DEV Aux load(int t, int f0) const {
+  HB_DEV Aux load(int t, int f0, int fb) const {
     Aux a{};
-    if (f0 < q_dim + kv_dim) {
+    if (fb < q_dim + kv_dim) {
       int b, s;
       pos_of(t, b, s);
-      const int f = f0 < q_dim ? f0 : f0 - q_dim;
-      const int e = f - div_hd.div(f) * hd;
-      const float2* rp = rope + (size_t)s * (hd >> 1) + (e >> 1);
+      const int fr = fb - region_start(fb);
+      const int e = fr - div_hd.div(fr) * hd + (f0 - fb);
+      const float2* rp = rope + (size_t)(e >> 1) * rope_ld + s;
       a.c0 = rp[0];
-      a.c1 = rp[1];
+      a.c1 = rp[rope_ld];
     }
     return a;
   }
-  HB_DEV void operator()(int t, int f0, f32x4 v4, const Aux& a) const {
+  HB_DEV void operator()(int t, int f0, f32x4 v4, const Aux& a, int fb) const {
     int b, s;
     pos_of(t, b, s);
-    const int qkv = q_dim + 2 * kv_dim;
-    if (f0 < q_dim + kv_dim) {
-      const bool isq = f0 < q_dim;
-      const int f = isq ? f0 : f0 - q_dim;
-      const int h = div_hd.div(f), e = f - h * hd;
-      f32x4 o;
+    const int r0 = region_start(fb), fr = fb - r0;
+    const int h = div_hd.div(fr), e = fr - h * hd + (f0 - fb);
+    f32x4 o = v4;
+    if (r0 < q_dim + kv_dim) {
       o.x = v4.x * a.c0.x - v4.y * a.c0.y;
       o.y = v4.y * a.c0.x + v4.x * a.c0.y;
       o.z = v4.z * a.c1.x - v4.w * a.c1.y;
       o.w = v4.w * a.c1.x + v4.z * a.c1.y;
-      f16x4 oh;
-      oh.x = (f16)o.x;
-      oh.y = (f16)o.y;
-      oh.z = (f16)o.z;
-      oh.w = (f16)o.w;
-      if (isq) {
-        const int qs = d_pos ? 0 : s;  // decode keeps one Q row per sequence
-        *(f16x4*)(q + (((size_t)b * heads + h) * q_rows + qs) * hd + e) = oh;
-      } else {
-        *(f16x4*)(k + b * k_bstride + h * k_hstride + (size_t)s * hd + e) = oh;
-      }
-      if (tap) *(f32x4*)(tap + (size_t)t * qkv + f0) = o;
-    } else {
-      const int f = f0 - q_dim - kv_dim;
-      const int h = div_hd.div(f), e = f - h * hd;
-      f16x4 vh;
-      vh.x = (f16)v4.x;
-      vh.y = (f16)v4.y;
-      vh.z = (f16)v4.z;
-      vh.w = (f16)v4.w;
-      if (v) *(f16x4*)(v + b * v_bstride + h * v_hstride + (size_t)s * hd + e) = vh;
-      if (vt) {
-        f16* p = vt + ((size_t)b * kv_heads + h) * hd * vt_ld + (size_t)e * vt_ld + s;
-        p[0] = vh.x;
-        p[vt_ld] = vh.y;
-        p[2 * vt_ld] = vh.z;
-        p[3 * vt_ld] = vh.w;
-      }
-      if (tap) *(f32x4*)(tap + (size_t)t * qkv + f0) = v4;
     }
+    f16x4 oh;
+    oh.x = (f16)o.x;
+    oh.y = (f16)o.y;
+    oh.z = (f16)o.z;
+    oh.w = (f16)o.w;
+    // Q, K and V rows share one addressing form: base + b*bstride + h*hstride + s*hd + e
+    f16* base;
+    size_t bs, hs;
+    int srow = s;
+    if (r0 == 0) {
+      base = q;
+      hs = (size_t)q_rows * hd;
+      bs = (size_t)heads * hs;
+      if (d_pos) srow = 0;  // decode keeps one Q row per sequence
+    } else if (r0 == q_dim) {
+      base = k;
+      bs = k_bstride;
+      hs = k_hstride;
+    } else {
+      base = v;
+      bs = v_bstride;
+      hs = v_hstride;
+    }
+    if (base) *(f16x4*)(base + b * bs + h * hs + (size_t)srow * hd + e) = oh;
+    if (r0 == q_dim + kv_dim && vt) {
+      f16* p = vt + ((size_t)b * kv_heads + h) * hd * vt_ld + (size_t)e * vt_ld + s;
+      p[0] = oh.x;
+      p[vt_ld] = oh.y;
+      p[2 * vt_ld] = oh.z;
+      p[3 * vt_ld] = oh.w;
+    }
+    if (tap) *(f32x4*)(tap + (size_t)t * (q_dim + 2 * kv_dim) + f0) = o;
   }
-  HB_DEV void operator()(int t, int f0, f32x4 v4) const { (*this)(t, f0, v4, load(t, f0)); }
+  HB_DEV Aux load(int t, int f0) const { return load(t, f0, f0 & ~31); }
+  HB_DEV void operator()(int t, int f0, f32x4 v4) const {
+    (*this)(t, f0, v4, load(t, f0), f0 & ~31);
+  }
 };
 
 }  // namespace hb

@@ -30,19 +30,22 @@ HB_DEV void static_for(F&& f) {
   }
 }
 
-// Epilogues that read memory declare `Aux`, `Aux load(t, f0)` and
-// `operator()(t, f0, v, aux)`; the others only `operator()(t, f0, v)`.
+// Epilogues that read memory declare `Aux`, `Aux load(t, f0, fb)` and
+// `operator()(t, f0, v, aux, fb)`, where fb is the wave-uniform start of the
+// 32-feature block that holds f0; the others only `operator()(t, f0, v)`.
 template <class E, class = void>
 struct EpiAux {
   struct type {};
-  static HB_DEV type load(const E&, int, int) { return {}; }
-  static HB_DEV void apply(const E& e, int t, int f0, f32x4 v, const type&) { e(t, f0, v); }
+  static HB_DEV type load(const E&, int, int, int) { return {}; }
+  static HB_DEV void apply(const E& e, int t, int f0, f32x4 v, const type&, int) { e(t, f0, v); }
 };
 template <class E>
 struct EpiAux<E, std::void_t<typename E::Aux>> {
   using type = typename E::Aux;
-  static HB_DEV type load(const E& e, int t, int f0) { return e.load(t, f0); }
-  static HB_DEV void apply(const E& e, int t, int f0, f32x4 v, const type& a) { e(t, f0, v, a); }
+  static HB_DEV type load(const E& e, int t, int f0, int fb) { return e.load(t, f0, fb); }
+  static HB_DEV void apply(const E& e, int t, int f0, f32x4 v, const type& a, int fb) {
+    e(t, f0, v, a, fb);
+  }
 };
 
 // LDS-only workgroup barrier: orders LDS accesses of the workgroup without
@@ -90,7 +93,8 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   __shared__ f16x8 sW[2][FT * 8];
   __shared__ f16x8 sX[2][TT * 8];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wf = wave / WT, wt = wave - wf * WT;
   const int nft = (N + FT - 1) / FT, ntt = (T + TT - 1) / TT;
   const int tile = xcd_remap(blockIdx.x, nft * ntt);
@@ -195,6 +199,28 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  // Epilogue operands read from memory: all of them before the main loop when
+  // they fit in 96 registers and the tile runs one wave per SIMD anyway
+  // (192x128 and larger; their latency then hides behind the K loop), else one
+  // accumulator row at a time (see the epilogue).
+  using AX = EpiAux<Epi>;
+  using AuxT = typename AX::type;
+  constexpr bool HOIST =
+      !std::is_empty_v<AuxT> && FM * TM * 4 * sizeof(AuxT) <= 96 * 4 && FT * TT >= 192 * 128;
+  AuxT aux[HOIST ? FM : 2][TM * 4];
+  auto tok = [&](int j) { return t_base + wt * WTT + j * 32 + (lane & 31); };
+  auto fblk = [&](int i) { return f_base + wf * WFT + i * 32; };  // wave-uniform
+  auto feat = [&](int i, int g) { return fblk(i) + 8 * g + 4 * khalf; };
+  auto load_row = [&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    static_for<0, TM * 4>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const int t = tok(q / 4), f = feat(i, q % 4);
+      if (t < T && f < N) aux[HOIST ? i : (i & 1)][q] = AX::load(epi, t, f, fblk(i));
+    });
+  };
+  if constexpr (HOIST) static_for<0, FM>([&](auto ic) { load_row(ic); });
+
   // nk >= 1 for every split (the launcher checks (splits - 1) * kq < K / 64)
   gload(R0{}, kslice(0));
   gload(R1{}, kslice(1));
@@ -210,27 +236,15 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   // Epilogue over the FM x TM x 4 accumulator quads as straight-line code: a
   // loop would be left rolled once the epilogue body is large (EpiQKV on
   // 256x256 tiles), and indexing acc with a loop counter moves the whole
-  // accumulator array to scratch memory. Epilogues that read memory (the
-  // residual stream, the RoPE table) load the quads of accumulator row i+1
-  // before the quads of row i are stored: their loads cannot be moved above
-  // stores that might alias them, so a load-store-load chain per quad would
-  // expose the load latency once per quad.
-  using AX = EpiAux<Epi>;
-  typename AX::type aux[2][TM * 4];
-  auto tok = [&](int j) { return t_base + wt * WTT + j * 32 + (lane & 31); };
-  auto feat = [&](int i, int g) { return f_base + wf * WFT + i * 32 + 8 * g + 4 * khalf; };
-  auto load_row = [&](auto ic) {
-    constexpr int i = decltype(ic)::value;
-    static_for<0, TM * 4>([&](auto qc) {
-      constexpr int q = decltype(qc)::value;
-      const int t = tok(q / 4), f = feat(i, q % 4);
-      if (t < T && f < N) aux[i & 1][q] = AX::load(epi, t, f);
-    });
-  };
-  load_row(std::integral_constant<int, 0>{});
+  // accumulator array to scratch memory. The operands that epilogues read from
+  // memory (residual stream, RoPE table) were loaded before the main loop
+  // (HOIST) or are loaded one accumulator row ahead of the stores: the loads
+  // cannot be moved above stores that might alias them, so a load-store-load
+  // chain per quad would expose the load latency once per quad.
+  if constexpr (!HOIST) load_row(std::integral_constant<int, 0>{});
   static_for<0, FM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    if constexpr (i + 1 < FM) load_row(std::integral_constant<int, i + 1>{});
+    if constexpr (!HOIST && i + 1 < FM) load_row(std::integral_constant<int, i + 1>{});
     static_for<0, TM * 4>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       constexpr int j = q / 4, g = q % 4;
@@ -241,7 +255,7 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
         v.y = acc[i][j][4 * g + 1];
         v.z = acc[i][j][4 * g + 2];
         v.w = acc[i][j][4 * g + 3];
-        AX::apply(epi, t, f, v, aux[i & 1][q]);
+        AX::apply(epi, t, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
       }
     });
   });
