@@ -39,6 +39,11 @@ hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int voca
 
 // ---- RMSNorm (cpu/rmsnorm.rs:149-183) -------------------------------------------
 // r = 1/sqrt(sum(x^2) * (1/dim) + eps); y = x * r * gamma. One workgroup per row.
+// NPT > 0: dim = NPT * 1024, each thread owns NPT float4 chunks, all loads are
+// issued before any use and the row stays in registers for the second pass.
+// NPT = 0: any dim (multiple of 4), strided loop. Both add each thread's
+// squares in the same order, so the result does not depend on the variant.
+template <int NPT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, long row_stride,
                                                       const float* __restrict__ gamma, int dim,
                                                       float eps, f16* __restrict__ out,
@@ -46,32 +51,64 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   __shared__ float red[4];
   const int t = blockIdx.x;
   const float* xr = x + (size_t)t * row_stride;
-  float ss = 0.f;
-  for (int c = threadIdx.x * 4; c < dim; c += 1024) {
-    const f32x4 v = *(const f32x4*)(xr + c);
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-  }
-  ss = block_sum<4>(ss, red);
-  const float r = 1.0f / sqrtf(ss * (1.0f / (float)dim) + eps);
-  if (rms_inv && threadIdx.x == 0) rms_inv[t] = r;
   f16* orow = out + (size_t)t * dim;
-  for (int c = threadIdx.x * 4; c < dim; c += 1024) {
-    const f32x4 v = *(const f32x4*)(xr + c);
-    const f32x4 g = *(const f32x4*)(gamma + c);
-    f16x4 o;
-    o.x = (f16)(v.x * r * g.x);
-    o.y = (f16)(v.y * r * g.y);
-    o.z = (f16)(v.z * r * g.z);
-    o.w = (f16)(v.w * r * g.w);
-    *(f16x4*)(orow + c) = o;
+  float ss = 0.f;
+  if constexpr (NPT > 0) {
+    f32x4 v[NPT], g[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) v[i] = *(const f32x4*)(xr + threadIdx.x * 4 + i * 1024);
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) g[i] = *(const f32x4*)(gamma + threadIdx.x * 4 + i * 1024);
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    ss = block_sum<4>(ss, red);
+    const float r = 1.0f / sqrtf(ss * (1.0f / (float)dim) + eps);
+    if (rms_inv && threadIdx.x == 0) rms_inv[t] = r;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      f16x4 o;
+      o.x = (f16)(v[i].x * r * g[i].x);
+      o.y = (f16)(v[i].y * r * g[i].y);
+      o.z = (f16)(v[i].z * r * g[i].z);
+      o.w = (f16)(v[i].w * r * g[i].w);
+      *(f16x4*)(orow + threadIdx.x * 4 + i * 1024) = o;
+    }
+  } else {
+    for (int c = threadIdx.x * 4; c < dim; c += 1024) {
+      const f32x4 v = *(const f32x4*)(xr + c);
+      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    ss = block_sum<4>(ss, red);
+    const float r = 1.0f / sqrtf(ss * (1.0f / (float)dim) + eps);
+    if (rms_inv && threadIdx.x == 0) rms_inv[t] = r;
+    for (int c = threadIdx.x * 4; c < dim; c += 1024) {
+      const f32x4 v = *(const f32x4*)(xr + c);
+      const f32x4 g = *(const f32x4*)(gamma + c);
+      f16x4 o;
+      o.x = (f16)(v.x * r * g.x);
+      o.y = (f16)(v.y * r * g.y);
+      o.z = (f16)(v.z * r * g.z);
+      o.w = (f16)(v.w * r * g.w);
+      *(f16x4*)(orow + c) = o;
+    }
   }
 }
 
 hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
                    f16* out, float* rms_inv, hipStream_t st) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, st, x, row_stride, gamma, dim, eps,
-                     out, rms_inv);
+  switch (dim % 1024 == 0 ? dim / 1024 : 0) {
+#define HB_NORM(n)                                                                              \
+  case n:                                                                                       \
+    hipLaunchKernelGGL(rmsnorm_kernel<n>, dim3(T), dim3(256), 0, st, x, row_stride, gamma, dim, \
+                       eps, out, rms_inv);                                                      \
+    break;
+    HB_NORM(1) HB_NORM(2) HB_NORM(3) HB_NORM(4) HB_NORM(5) HB_NORM(6) HB_NORM(7) HB_NORM(8)
+#undef HB_NORM
+    default:
+      hipLaunchKernelGGL(rmsnorm_kernel<0>, dim3(T), dim3(256), 0, st, x, row_stride, gamma, dim,
+                         eps, out, rms_inv);
+  }
   return hipGetLastError();
 }
 

@@ -42,6 +42,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // splits in order, applies the residual epilogue (out = res + alpha * v), and
 // normalises the row into xn. The element-to-thread mapping and the block sum
 // are those of rmsnorm_kernel, so xn is bit-identical to reduce + rmsnorm.
+template <int NPT>  // as rmsnorm_kernel: N = NPT * 1024 held in registers, or 0 = any N
 __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __restrict__ P, int S,
                                                                  int N, size_t stride,
                                                                  EpiResidual e, NormOut no) {
@@ -49,37 +50,78 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
   __shared__ float red[4];
   const int t = blockIdx.x;
   const size_t row = (size_t)t * N;
-  float ss = 0.f;
-  for (int c = threadIdx.x * 4; c < N; c += 1024) {
-    f32x4 part[MAXS];
-#pragma unroll
-    for (int s = 0; s < MAXS; ++s)
-      if (s < S) part[s] = *(const f32x4*)(P + s * stride + row + c);
-    f32x4 v = part[0];
-#pragma unroll
-    for (int s = 1; s < MAXS; ++s)
-      if (s < S) v += part[s];
-    const f32x4 r = *(const f32x4*)(e.res + row + c);
-    f32x4 y;
-    y.x = v.x * e.alpha + r.x;
-    y.y = v.y * e.alpha + r.y;
-    y.z = v.z * e.alpha + r.z;
-    y.w = v.w * e.alpha + r.w;
-    *(f32x4*)(e.out + row + c) = y;
-    ss += y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
-  }
-  ss = block_sum<4>(ss, red);
-  const float rinv = 1.0f / sqrtf(ss * (1.0f / (float)N) + no.eps);
   f16* orow = no.xn + row;
-  for (int c = threadIdx.x * 4; c < N; c += 1024) {
-    const f32x4 y = *(const f32x4*)(e.out + row + c);  // this thread's own stores
-    const f32x4 g = *(const f32x4*)(no.gamma + c);
-    f16x4 o;
-    o.x = (f16)(y.x * rinv * g.x);
-    o.y = (f16)(y.y * rinv * g.y);
-    o.z = (f16)(y.z * rinv * g.z);
-    o.w = (f16)(y.w * rinv * g.w);
-    *(f16x4*)(orow + c) = o;
+  float ss = 0.f;
+  if constexpr (NPT > 0) {
+    f32x4 y[NPT], g[NPT];
+    {
+      f32x4 part[NPT][MAXS], r[NPT];
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        const size_t c = row + threadIdx.x * 4 + i * 1024;
+#pragma unroll
+        for (int s = 0; s < MAXS; ++s)
+          if (s < S) part[i][s] = *(const f32x4*)(P + s * stride + c);
+        r[i] = *(const f32x4*)(e.res + c);
+      }
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) g[i] = *(const f32x4*)(no.gamma + threadIdx.x * 4 + i * 1024);
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        f32x4 v = part[i][0];
+#pragma unroll
+        for (int s = 1; s < MAXS; ++s)
+          if (s < S) v += part[i][s];
+        y[i].x = v.x * e.alpha + r[i].x;
+        y[i].y = v.y * e.alpha + r[i].y;
+        y[i].z = v.z * e.alpha + r[i].z;
+        y[i].w = v.w * e.alpha + r[i].w;
+        *(f32x4*)(e.out + row + threadIdx.x * 4 + i * 1024) = y[i];
+        ss += y[i].x * y[i].x + y[i].y * y[i].y + y[i].z * y[i].z + y[i].w * y[i].w;
+      }
+    }
+    ss = block_sum<4>(ss, red);
+    const float rinv = 1.0f / sqrtf(ss * (1.0f / (float)N) + no.eps);
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      f16x4 o;
+      o.x = (f16)(y[i].x * rinv * g[i].x);
+      o.y = (f16)(y[i].y * rinv * g[i].y);
+      o.z = (f16)(y[i].z * rinv * g[i].z);
+      o.w = (f16)(y[i].w * rinv * g[i].w);
+      *(f16x4*)(orow + threadIdx.x * 4 + i * 1024) = o;
+    }
+  } else {
+    for (int c = threadIdx.x * 4; c < N; c += 1024) {
+      f32x4 part[MAXS];
+#pragma unroll
+      for (int s = 0; s < MAXS; ++s)
+        if (s < S) part[s] = *(const f32x4*)(P + s * stride + row + c);
+      f32x4 v = part[0];
+#pragma unroll
+      for (int s = 1; s < MAXS; ++s)
+        if (s < S) v += part[s];
+      const f32x4 r = *(const f32x4*)(e.res + row + c);
+      f32x4 y;
+      y.x = v.x * e.alpha + r.x;
+      y.y = v.y * e.alpha + r.y;
+      y.z = v.z * e.alpha + r.z;
+      y.w = v.w * e.alpha + r.w;
+      *(f32x4*)(e.out + row + c) = y;
+      ss += y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
+    }
+    ss = block_sum<4>(ss, red);
+    const float rinv = 1.0f / sqrtf(ss * (1.0f / (float)N) + no.eps);
+    for (int c = threadIdx.x * 4; c < N; c += 1024) {
+      const f32x4 y = *(const f32x4*)(e.out + row + c);  // this thread's own stores
+      const f32x4 g = *(const f32x4*)(no.gamma + c);
+      f16x4 o;
+      o.x = (f16)(y.x * rinv * g.x);
+      o.y = (f16)(y.y * rinv * g.y);
+      o.z = (f16)(y.z * rinv * g.z);
+      o.w = (f16)(y.w * rinv * g.w);
+      *(f16x4*)(orow + c) = o;
+    }
   }
 }
 
@@ -175,7 +217,18 @@ hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, c
     if (!scr->p || (size_t)S * stride > scr->floats || (long)N * K >= (1L << 31)) return hipErrorInvalidValue;
     const hipError_t err = launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(splitk_reduce_norm_kernel, dim3(T), dim3(256), 0, st, scr->p, S, N, stride, e, no);
+    switch (N % 1024 == 0 ? N / 1024 : 0) {
+#define HB_RN(n)                                                                                \
+  case n:                                                                                       \
+    hipLaunchKernelGGL(splitk_reduce_norm_kernel<n>, dim3(T), dim3(256), 0, st, scr->p, S, N,   \
+                       stride, e, no);                                                          \
+    break;
+      HB_RN(1) HB_RN(2) HB_RN(3) HB_RN(4) HB_RN(5) HB_RN(6) HB_RN(7) HB_RN(8)
+#undef HB_RN
+      default:
+        hipLaunchKernelGGL(splitk_reduce_norm_kernel<0>, dim3(T), dim3(256), 0, st, scr->p, S, N,
+                           stride, e, no);
+    }
     return hipGetLastError();
   }
   const hipError_t err = launch_gemm(W, X, N, T, K, e, nullptr, st);
