@@ -7,7 +7,7 @@
 
 namespace hb {
 
-// ---- prefill: one workgroup of PW waves per (32 queries, head, sequence) --------
+// ---- prefill: one workgroup of 4 waves per (64 queries, head, sequence) ---------
 // S^T = K · Q^T on v_mfma_f32_32x32x16_f16 (rows = key slots, cols = queries):
 // lane l owns query l%32 and the key slots 8*(r/4) + 4*(l/32) + r%4 of the
 // 32-key block, so the online-softmax statistics of a query live in one lane
@@ -17,85 +17,93 @@ namespace hb {
 // registers as the B operand, and the A operand (V^T row, the same 8 keys) is
 // one 16-byte read.
 //
-// The causal key range of a query block is split over the PW waves of the
-// workgroup (wave w takes key blocks w, w+PW, ...), so the longest chain of
-// dependent key blocks is 1/PW of the row and the launch has PW x more waves
-// in flight; each wave keeps its own online-softmax state and waves 1..PW-1
-// hand theirs to wave 0 through LDS for one weighted merge (the same
-// rescaling an online softmax applies between blocks).
-//
-// Each wave stages its key block (K [32][hd] and V^T [hd][32]) in its own LDS
-// region: the global loads are 16 bytes per lane and 1 KB contiguous per wave
-// instruction for K (64 B per V^T row), issued one block ahead into registers,
-// and the MFMA fragments are read from XOR-swizzled LDS without bank
-// conflicts. (Fragment loads straight from global memory touch 32 cache lines
-// per wave instruction, and the L1's tag rate then bounds the kernel.) Only
-// the owning wave touches its region, so no workgroup barrier is needed
-// inside the loop; a wave's LDS operations execute in order.
-constexpr int PW = 4;
+// Wave w = qs + PQ*kh owns query block qs (of PQ = 2) of the workgroup and the
+// key blocks kb with kb % PK == kh (PK = 2): iteration n loads key blocks
+// PK*n .. PK*n+PK-1 (K [32][hd] and V^T [hd][32] each) into LDS once, with
+// 16-byte, wave-contiguous loads issued one iteration ahead, and every block
+// is used by the PQ waves of its key half. Sharing a block between query
+// blocks halves the bytes loaded per MFMA — a wave loading its own K/V needs
+// ~128 B/clk per CU, four times what the L1-L2 path sustains — while splitting
+// the key range over PK waves keeps the chain of dependent key blocks at half
+// the row; the key halves merge through LDS at the end (the same rescaling an
+// online softmax applies between blocks). Fragments are read from
+// XOR-swizzled LDS without bank conflicts.
+constexpr int PQ = 2;  // 32-query blocks per workgroup
+constexpr int PK = 2;  // key blocks per iteration (key halves)
+constexpr int PW = PQ * PK;
 
 HB_DEV int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
-// Orders this wave's LDS accesses around a cross-lane LDS hand-off: waits for
-// its outstanding LDS operations and keeps the compiler from moving memory
-// accesses across.
-HB_DEV void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
 template <int HD>
 __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p) {
-  constexpr int KS = HD / 16;   // k-steps over head dim
-  constexpr int MB = HD / 32;   // 32-row blocks of O^T
-  constexpr int NCH = HD / 8;   // 16-byte chunks per K row
-  constexpr int KT8 = 4 * HD;   // 16-byte chunks per K tile (= per V^T tile)
-  constexpr int NLD = HD / 16;  // 16-byte loads per lane per tile
-  // per wave: K tile (row r, chunk c at r*NCH + (c ^ (swap23(r) % NCH))), then
-  // the V^T tile (row e, chunk c at KT8 + e*4 + (c ^ ((e >> 2) & 3))); after the
-  // loop the same region holds the wave's unnormalised O for the merge
-  __shared__ f16x8 s_kv[PW][2 * KT8];
-  __shared__ float s_ml[PW - 1][2][64];
-  static_assert(2 * KT8 * 16 >= MB * 16 * 64 * 4, "merge buffer fits in a wave's tiles");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, li = lane & 31;
+  constexpr int KS = HD / 16;          // k-steps over head dim
+  constexpr int MB = HD / 32;          // 32-row blocks of O^T
+  constexpr int NCH = HD / 8;          // 16-byte chunks per K row
+  constexpr int KT8 = 4 * HD;          // 16-byte chunks per K tile (= per V^T tile)
+  constexpr int NLD = 2 * PK * KT8 / (PW * 64);  // 16-byte loads per thread per iteration
+  static_assert(NLD * PW * 64 == 2 * PK * KT8, "loader coverage");
+  // K tiles (block kh: row r, chunk c at kh*KT8 + r*NCH + (c ^ (swap23(r) % NCH))), then
+  // V^T tiles (block kh: row e, chunk c at (PK+kh)*KT8 + e*4 + (c ^ ((e >> 2) & 3)));
+  // after the loop the region holds the key-half-1 waves' O for the merge
+  __shared__ f16x8 s_kv[2 * PK * KT8];
+  __shared__ float s_ml[PQ][2][64];
+  static_assert(2 * PK * KT8 * 16 >= PQ * MB * 16 * 64 * 4, "merge buffer fits in the tiles");
+  const int tid = threadIdx.x, lane = tid & 63, h2 = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int qs = wave % PQ, kh = wave / PQ;
   const int nqb = (p.S + 31) / 32;
-  const int qb = nqb - 1 - blockIdx.x;  // heaviest blocks first
+  const int ngr = (nqb + PQ - 1) / PQ;
+  const int gr = ngr - 1 - blockIdx.x;  // heaviest groups first
+  const int qb = gr * PQ + qs;          // >= nqb: this wave has no queries
+  const bool active = qb < nqb;
+  const int nkb = min(gr * PQ + PQ, nqb);  // key blocks the group needs
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (p.H / p.KVH);
   const int q0 = qb * 32;
   const int qi = q0 + li;
 
-  const f16* qp = p.q + (((size_t)b * p.H + h) * p.q_rows + q0 + li) * HD + 8 * h2;
   f16x8 qf[KS];
+  if (active) {
+    const f16* qp = p.q + (((size_t)b * p.H + h) * p.q_rows + q0 + li) * HD + 8 * h2;
 #pragma unroll
-  for (int j = 0; j < KS; ++j) qf[j] = *(const f16x8*)(qp + 16 * j);
+    for (int j = 0; j < KS; ++j) qf[j] = *(const f16x8*)(qp + 16 * j);
+  }
 
   const f16* kbase = p.k + b * p.k_bstride + kvh * p.k_hstride;
   const f16* vbase = p.vt + ((size_t)b * p.KVH + kvh) * HD * p.vt_ld;
   const float sl2 = p.scale * HB_LOG2E;
-  f16x8* sk = s_kv[wave];
-  f16x8* sv = s_kv[wave] + KT8;
 
-  f16x8 kreg[NLD], vreg[NLD];
-  auto gload = [&](int kb) {
-    const f16* kt = kbase + (size_t)kb * 32 * HD;
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) kreg[i] = *(const f16x8*)(kt + (i * 64 + lane) * 8);
+  // thread tid, load i covers 16-byte chunk x = i*256 + tid of the iteration's
+  // 2*PK tiles (K blocks, then V^T blocks)
+  f16x8 kvreg[NLD];
+  auto gload = [&](int n) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int e = (i * 64 + lane) >> 2, c = lane & 3;
-      vreg[i] = *(const f16x8*)(vbase + (size_t)e * p.vt_ld + kb * 32 + c * 8);
+      const int x = i * PW * 64 + tid, tile = x / KT8, y = x % KT8;
+      const int kb = min(n * PK + (tile % PK), nkb - 1);
+      if (tile < PK) {
+        kvreg[i] = *(const f16x8*)(kbase + ((size_t)kb * 32 + y / NCH) * HD + (y % NCH) * 8);
+      } else {
+        const int e = y >> 2, c = y & 3;
+        kvreg[i] = *(const f16x8*)(vbase + (size_t)e * p.vt_ld + kb * 32 + c * 8);
+      }
     }
   };
   auto lstore = [&]() {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int x = i * 64 + lane, r = x / NCH, c = x % NCH;
-      sk[r * NCH + (c ^ (swap23(r) % NCH))] = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int x = i * 64 + lane, e = x >> 2, c = x & 3;
-      sv[e * 4 + (c ^ ((e >> 2) & 3))] = vreg[i];
+      const int x = i * PW * 64 + tid, tile = x / KT8, y = x % KT8;
+      if (tile < PK) {
+        const int r = y / NCH, c = y % NCH;
+        s_kv[tile * KT8 + r * NCH + (c ^ (swap23(r) % NCH))] = kvreg[i];
+      } else {
+        const int e = y >> 2, c = y & 3;
+        s_kv[tile * KT8 + e * 4 + (c ^ ((e >> 2) & 3))] = kvreg[i];
+      }
     }
   };
+  const f16x8* sk = s_kv + kh * KT8;
+  const f16x8* sv = s_kv + (PK + kh) * KT8;
 
   f32x16 o[MB];
 #pragma unroll
@@ -103,12 +111,15 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
   float mrun = -INFINITY, lrun = 0.f;
 
   const int krow = swap23(li);  // key held in this lane's slot
-  if (wave <= qb) gload(wave);
-  for (int kb = wave; kb <= qb; kb += PW) {
-    wave_lds_sync();  // the previous block's fragment reads are done
+  const int niter = (nkb + PK - 1) / PK;
+  gload(0);
+  for (int n = 0; n < niter; ++n) {
+    lds_barrier();  // every wave is done with the previous iteration's tiles
     lstore();
-    wave_lds_sync();  // the tiles are in LDS
-    if (kb + PW <= qb) gload(kb + PW);
+    lds_barrier();  // the tiles are in LDS
+    if (n + 1 < niter) gload(n + 1);
+    const int kb = n * PK + kh;
+    if (!active || kb > qb) continue;  // wave-uniform
 
     f32x16 s = {};
 #pragma unroll
@@ -118,30 +129,35 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
     }
     float mloc = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kb * 32 + swap23(8 * (r >> 2) + 4 * h2 + (r & 3));
-      float v = s[r] * sl2;
-      if (kb == qb && key > qi) v = -INFINITY;
-      s[r] = v;
-      mloc = fmaxf(mloc, v);
+    for (int r = 0; r < 16; ++r) s[r] *= sl2;
+    if (kb == qb) {  // diagonal block: keys after the query are masked
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (kb * 32 + swap23(8 * (r >> 2) + 4 * h2 + (r & 3)) > qi) s[r] = -INFINITY;
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mnew = fmaxf(mrun, mloc);
-    const float corr = exp2f(mrun - mnew);
-    float lsum = 0.f;
+    // The reference max mrun is only raised when a score exceeds it by more
+    // than 2^8 (log2 units): probabilities stay <= 256 (exact in fp16 to the
+    // same relative precision) and the final 1/l cancels the common scale,
+    // so O and l are only rescaled on such jumps (always on the first block).
+    if (__builtin_amdgcn_ballot_w64(mloc > mrun + 8.f)) {
+      const float mnew = fmaxf(mrun, mloc);
+      const float corr = exp2f(mrun - mnew);
+      lrun *= corr;
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[m][r] *= corr;
+      mrun = mnew;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float e = exp2f(s[r] - mnew);
+      const float e = exp2f(s[r] - mrun);
       s[r] = e;
-      lsum += e;
+      lrun += e;  // this lane's keys; the lane pair is summed after the loop
     }
-    lsum += __shfl_xor(lsum, 32, 64);
-    lrun = lrun * corr + lsum;
-    mrun = mnew;
-#pragma unroll
-    for (int m = 0; m < MB; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[m][r] *= corr;
 
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -156,43 +172,33 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
       }
     }
   }
+  lrun += __shfl_xor(lrun, 32, 64);  // both lanes of a query pair share mrun
 
-  // Waves 1..PW-1 hand (o, m, l) to wave 0 (a wave with no key block has
-  // m = -inf and weight 0). Lane l of every wave holds the same (query, row)
-  // slots, so the exchange is one float per lane per register; each wave
-  // writes its O into its own (now idle) tile region.
-  float* s_o = (float*)s_kv[wave];  // [MB*16][64]
-  if (wave > 0) {
-    wave_lds_sync();
+  // The key-half-1 waves hand (o, m, l) to the key-half-0 wave of the same
+  // query block (a wave with no key block has m = -inf and weight 0). Lane l
+  // of both waves holds the same (query, row) slots, so the exchange is one
+  // float per lane per register.
+  float* s_o = (float*)s_kv + qs * (MB * 16 * 64);  // [MB*16][64] per query block
+  lds_barrier();  // every wave is done with the tiles
+  if (kh == 1) {
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s_o[(m * 16 + r) * 64 + lane] = o[m][r];
-    s_ml[wave - 1][0][lane] = mrun;
-    s_ml[wave - 1][1][lane] = lrun;
+    s_ml[qs][0][lane] = mrun;
+    s_ml[qs][1][lane] = lrun;
   }
-  __syncthreads();
-  if (wave > 0) return;
-  float M = mrun;
-#pragma unroll
-  for (int w = 0; w < PW - 1; ++w) M = fmaxf(M, s_ml[w][0][lane]);
-  const float c0 = exp2f(mrun - M);  // wave 0 always holds block 0, so mrun is finite
-  float L = lrun * c0;
+  lds_barrier();
+  if (kh == 1 || !active) return;
+  const float mw = s_ml[qs][0][lane];
+  const float M = fmaxf(mrun, mw);
+  const float c0 = exp2f(mrun - M);  // key half 0 always holds block 0, so mrun is finite
+  const float cw = mw == -INFINITY ? 0.f : exp2f(mw - M);
+  const float L = lrun * c0 + cw * s_ml[qs][1][lane];
 #pragma unroll
   for (int m = 0; m < MB; ++m)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[m][r] *= c0;
-#pragma unroll
-  for (int w = 0; w < PW - 1; ++w) {
-    const float mw = s_ml[w][0][lane];
-    const float cw = mw == -INFINITY ? 0.f : exp2f(mw - M);
-    const float* ow = (const float*)s_kv[w + 1];
-    L += cw * s_ml[w][1][lane];
-#pragma unroll
-    for (int m = 0; m < MB; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[m][r] += cw * ow[(m * 16 + r) * 64 + lane];
-  }
+    for (int r = 0; r < 16; ++r) o[m][r] = o[m][r] * c0 + cw * s_o[(m * 16 + r) * 64 + lane];
 
   if (qi < p.S) {
     const float inv = 1.0f / L;
@@ -212,7 +218,8 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
 }
 
 hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
-  dim3 grid((p.S + 31) / 32, p.H, p.B);
+  const int nqb = (p.S + 31) / 32;
+  dim3 grid((nqb + PQ - 1) / PQ, p.H, p.B);
   if (p.hd == 128)
     hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(PW * 64), 0, st, p);
   else if (p.hd == 64)

@@ -30,6 +30,15 @@ struct FastDiv {
   HB_DEV int div(int n) const { return (int)((__umulhi((uint32_t)n, m) + (uint32_t)n) >> s); }
 };
 
+// LDS-only workgroup barrier: orders LDS accesses of the workgroup without
+// draining outstanding global loads (a full __syncthreads would wait for the
+// prefetches that are meant to stay in flight across it).
+HB_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Wave-wide reductions (64 lanes). __shfl_xor lowers to DPP / ds_swizzle.
 HB_DEV float wave_sum(float v) {
 #pragma unroll

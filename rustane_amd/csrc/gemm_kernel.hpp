@@ -48,15 +48,6 @@ struct EpiAux<E, std::void_t<typename E::Aux>> {
   }
 };
 
-// LDS-only workgroup barrier: orders LDS accesses of the workgroup without
-// draining outstanding global loads (a full __syncthreads would wait for the
-// prefetches that are meant to stay in flight across it).
-HB_DEV void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Pipeline: two 64-wide K slices are in flight in registers while the MFMAs
 // consume a third from LDS. Iteration k computes slice k from LDS buffer k&1,
 // issues the global loads of slice k+2 into register set k&1 and writes slice
