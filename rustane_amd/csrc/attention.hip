@@ -238,24 +238,20 @@ hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
 // (max, sum, unnormalised output) per chunk. Chunks past the current position
 // exit at once, so the launch shape does not depend on the position (one HIP
 // graph replays every step). Measured on MI355X, 512-key chunks on 16 waves
-// stream the cache as fast as 128-key chunks on 4 waves while leaving 4x fewer
-// partials to combine.
+// stream the cache as fast as 128- or 256-key chunks on 4 or 8 waves while
+// leaving fewer partials to combine.
 //
-// The partials are combined either by the consumer -- the Wo GEMV prologue
-// (gemv.hip), when B * chunks is small -- or here (MERGE): the last workgroup
-// of a head to finish (atomic ticket) merges the chunk partials into the
-// output. The in-kernel merge puts three memory round trips on the critical
-// path (agent-scope stores, ticket, agent-scope loads: partials travel through
-// device-coherent accesses instead of a device-scope fence, which on gfx950 is
-// an L2 write-back costing more than the whole pass), about 5 us on the 7B
-// shape, which is why the consumer combine is preferred.
+// The chunk partials are combined by the consumer -- the Wo GEMV prologue
+// (gemv.hip) when B * chunks is small -- or by attn_combine_kernel below,
+// which folds them in the same order with the same arithmetic, so both give
+// the same attention output.
 constexpr int DCHUNK = 512;
 constexpr int DWAVES = 16;
 
 int attn_decode_chunks(int ctx_max) { return (ctx_max + DCHUNK - 1) / DCHUNK; }
 int attn_decode_chunk_keys() { return DCHUNK; }
 
-template <int HD, bool MERGE>
+template <int HD>
 __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) {
   constexpr int NT = DWAVES * 64;
   constexpr int LPK = HD / 8;             // lanes per key row
@@ -264,7 +260,6 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
   constexpr int NIT = WKEYS / KPW;
   __shared__ float s_m[DWAVES], s_l[DWAVES];
   __shared__ float s_o[DWAVES][HD];
-  __shared__ int s_ticket;
 
   const int pos = *p.d_pos;
   const int c0 = blockIdx.x * DCHUNK;
@@ -349,88 +344,73 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
     float o = 0.f;
 #pragma unroll
     for (int v = 0; v < DWAVES; ++v) o += wt(v) * s_o[v][e];
-    if (MERGE)
-      __hip_atomic_store(p.part_o + slot * HD + e, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      p.part_o[slot * HD + e] = o;
+    p.part_o[slot * HD + e] = o;
   }
   if (tid == 0) {
     float L = 0.f;
 #pragma unroll
     for (int v = 0; v < DWAVES; ++v) L += wt(v) * s_l[v];
-    if (MERGE) {
-      __hip_atomic_store(p.part_ml + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.part_ml + slot * 2 + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      p.part_ml[slot * 2] = M;
-      p.part_ml[slot * 2 + 1] = L;
-    }
+    p.part_ml[slot * 2] = M;
+    p.part_ml[slot * 2 + 1] = L;
   }
-  if constexpr (MERGE) {
-    // The last chunk of this head to finish merges all chunks (its reads are
-    // agent-scope loads of the coherent partials). atomicInc wraps the
-    // counter back to 0 after the last arrival, ready for the next launch.
-    const int nvalid = pos / DCHUNK + 1;
-    __builtin_amdgcn_s_waitcnt(0);  // this workgroup's partial stores have completed
-    __syncthreads();
-    if (tid == 0)
-      s_ticket = (int)__builtin_amdgcn_atomic_inc32(p.counters + head, (unsigned)(nvalid - 1),
-                                                    __ATOMIC_RELAXED, "agent");
-    __syncthreads();
-    if (s_ticket != nvalid - 1) return;
-    // Merge in groups of MCH chunks: all threads load a group's partials into
-    // LDS at once (independent loads, one memory latency per group), then each
-    // output dimension folds the group into a running (max, sum, out) state.
-    constexpr int MCH = 32;
-    __shared__ float s_cml[MCH][2];
-    __shared__ float s_co[MCH][HD];
-    auto ld = [](const float* a) {
-      return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-    const float* pml = p.part_ml + head * nch * 2;
-    const float* pso = p.part_o + head * nch * HD;
-    float Mx = -INFINITY, L = 0.f, O = 0.f;
-    for (int g0 = 0; g0 < nvalid; g0 += MCH) {
-      const int cnt = min(MCH, nvalid - g0);
-      for (int i = tid; i < cnt * HD; i += NT)
-        s_co[i / HD][i % HD] = ld(pso + (size_t)(g0 + i / HD) * HD + i % HD);
-      if (tid < 2 * cnt) s_cml[tid >> 1][tid & 1] = ld(pml + (size_t)g0 * 2 + tid);
-      __syncthreads();
-      if (tid < HD) {
-        float gm = Mx;
-        for (int c = 0; c < cnt; ++c) gm = fmaxf(gm, s_cml[c][0]);
-        const float r = exp2f(Mx - gm);  // Mx = -inf on the first group: r = 0
-        L *= r;
-        O *= r;
-        for (int c = 0; c < cnt; ++c) {
-          const float wc = exp2f(s_cml[c][0] - gm);
-          L += wc * s_cml[c][1];
-          O += wc * s_co[c][tid];
-        }
-        Mx = gm;
-      }
-      __syncthreads();
-    }
-    if (tid < HD) p.out[head * HD + tid] = (f16)(O / L);
+}
+
+// out[b][h*hd + e] from the chunk partials of (b, h): one thread per 8
+// consecutive elements; max over the valid chunks, then weights exp2(m_c - M)
+// in chunk order (the Wo GEMV prologue's combine, stage_attn in gemv.hip).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecode p, int nch) {
+  constexpr int GPH = HD / 8;
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  if (gid >= p.B * p.H * GPH) return;
+  const int nvalid = min(*p.d_pos / DCHUNK + 1, nch);
+  const int bh = gid / GPH, e0 = (gid % GPH) * 8;
+  const float* pml = p.part_ml + (size_t)bh * nch * 2;
+  const float* po = p.part_o + (size_t)bh * nch * HD + e0;
+  float M = -INFINITY;
+  for (int c = 0; c < nvalid; ++c) M = fmaxf(M, pml[2 * c]);
+  float L = 0.f;
+  f32x4 O0 = {}, O1 = {};
+  for (int c = 0; c < nvalid; ++c) {
+    const float w = exp2f(pml[2 * c] - M);
+    L += w * pml[2 * c + 1];
+    O0 += w * *(const f32x4*)(po + (size_t)c * HD);
+    O1 += w * *(const f32x4*)(po + (size_t)c * HD + 4);
   }
+  const float iL = 1.0f / L;
+  f16x8 o;
+  o[0] = (f16)(O0.x * iL);
+  o[1] = (f16)(O0.y * iL);
+  o[2] = (f16)(O0.z * iL);
+  o[3] = (f16)(O0.w * iL);
+  o[4] = (f16)(O1.x * iL);
+  o[5] = (f16)(O1.y * iL);
+  o[6] = (f16)(O1.z * iL);
+  o[7] = (f16)(O1.w * iL);
+  *(f16x8*)(p.out + (size_t)bh * HD + e0) = o;
 }
 
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
   const int nch = attn_decode_chunks(p.ctx_max);
   dim3 grid(nch, p.H, p.B), block(DWAVES * 64);
-  if (p.hd == 128) {
-    if (p.merge)
-      hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, block, 0, st, p);
-    else
-      hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, block, 0, st, p);
-  } else if (p.hd == 64) {
-    if (p.merge)
-      hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, block, 0, st, p);
-    else
-      hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, block, 0, st, p);
-  } else {
+  if (p.hd == 128)
+    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, block, 0, st, p);
+  else if (p.hd == 64)
+    hipLaunchKernelGGL(attn_decode_kernel<64>, grid, block, 0, st, p);
+  else
     return hipErrorInvalidValue;
-  }
+  return hipGetLastError();
+}
+
+hipError_t attention_combine(const AttnDecode& p, hipStream_t st) {
+  const int nch = attn_decode_chunks(p.ctx_max);
+  const int n = p.B * p.H * (p.hd / 8);
+  if (p.hd == 128)
+    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((n + 255) / 256), dim3(256), 0, st, p, nch);
+  else if (p.hd == 64)
+    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3((n + 255) / 256), dim3(256), 0, st, p, nch);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

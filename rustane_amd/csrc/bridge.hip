@@ -130,7 +130,6 @@ struct hb_kv {
   int *d_pos = nullptr, *d_pos0 = nullptr;
   uint32_t *d_tok = nullptr, *d_next = nullptr, *d_hist = nullptr;
   float *x = nullptr, *x2 = nullptr, *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
-  unsigned* counters = nullptr;  // decode attention arrival tickets [B][H]
   bool attn_in_wo = false;       // chunk partials combined by the Wo GEMV
   float* amax_val = nullptr;  // greedy argmax partials [B][vocab/16]
   int* amax_idx = nullptr;
@@ -1040,8 +1039,9 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
     a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
     a.ctx_max = kv->ctx_cap; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
-    a.part_ml = kv->part_ml; a.merge = !kv->attn_in_wo; a.counters = kv->counters; a.out = kv->attn;
+    a.part_ml = kv->part_ml; a.out = kv->attn;
     HIP_TRY(attention_decode(a, st));
+    if (!kv->attn_in_wo) HIP_TRY(attention_combine(a, st));
     const AttnIn ain{kv->part_o, kv->part_ml, kv->d_pos, c.heads, c.hd, kv->nch, attn_decode_chunk_keys()};
     HIP_TRY(gemv_residual(L.t_wo, kv->attn, kv->attn_in_wo ? &ain : nullptr, c.dim, B, c.q_dim,
                           EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
@@ -1137,7 +1137,6 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   const size_t o_x = take(B * c.dim * 4), o_x2 = take(B * c.dim * 4);
   const size_t o_logits = take(B * c.vocab * 4);
   const size_t o_po = take(B * c.heads * kv->nch * c.hd * 4), o_pml = take(B * c.heads * kv->nch * 8);
-  const size_t o_cnt = take(B * c.heads * 4);
   const size_t o_aval = take(B * (c.vocab / 16) * 4), o_aidx = take(B * (c.vocab / 16) * 4);
   const size_t o_xn = take(B * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(B * c.q_dim * 2);
   const size_t o_gate = take(B * c.hidden * 2);
@@ -1159,7 +1158,6 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   kv->logits = (float*)(sb + o_logits);
   kv->part_o = (float*)(sb + o_po);
   kv->part_ml = (float*)(sb + o_pml);
-  kv->counters = (unsigned*)(sb + o_cnt);
   kv->amax_val = (float*)(sb + o_aval);
   kv->amax_idx = (int*)(sb + o_aidx);
   kv->xn = (f16*)(sb + o_xn);

@@ -35,8 +35,8 @@
 // way. With B * chunks <= GEMV_ATTN_MAXCH that is at most 8 x 130 floats per
 // (sequence, head) -- 133 KB per workgroup on the 7B shape at 4096 context --
 // fetched in one round trip while the first weight loads are in flight,
-// instead of the three dependent round trips of a merge inside the attention
-// launch.
+// instead of a separate combine launch (attention_combine, used when B *
+// chunks is larger).
 #include <type_traits>
 
 #include "internal.hpp"
@@ -118,7 +118,7 @@ HB_DEV void stage_norm(const NormIn& nin, int B, int K, f16* s_x) {
 
 // attn[b][h*hd + e] = fp16(sum_c w_c o_c[e] / sum_c w_c l_c), w_c = exp2(m_c - M),
 // M = max_c m_c over the chunks c <= *d_pos / chunk of attention_decode -- the
-// arithmetic and chunk order of its in-kernel merge. One 8-dim group of one
+// arithmetic and chunk order of attention_combine. One 8-dim group of one
 // (sequence, head) per thread and pass, every chunk load of a group issued
 // before any is used (one memory round trip).
 template <int NT>

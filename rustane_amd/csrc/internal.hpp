@@ -49,7 +49,7 @@ constexpr int GEMV_NORM_MAXB = 8;
 constexpr size_t GEMV_NORM_LDS = 32768;  // bytes of staged fp16 rows
 bool gemv_norm_fits(int B, int K);
 // Decode-attention chunk combine done inside the Wo GEMV (ain != NULL): the
-// B x H heads' chunk partials of attention_decode (merge = false) are merged
+// B x H heads' chunk partials of attention_decode are combined
 // into the fp16 attention rows [B, H*hd], staged in LDS; X is then unused.
 struct AttnIn {
   const float* part_o;   // [B][H][nch][hd]
@@ -99,16 +99,14 @@ struct AttnDecode {
   float scale;
   float* part_o;   // [B][H][nchunks][hd] unnormalised chunk outputs
   float* part_ml;  // [B][H][nchunks][2] chunk (max, sum) in log2 units
-  // merge: combine the chunks in this launch into out (counters: [B][H]
-  // arrival tickets, zero between launches); otherwise only the partials of
-  // chunks 0..*d_pos/chunk_keys are written and the Wo GEMV combines them.
-  bool merge;
-  unsigned* counters;
-  f16* out;        // [B][H*hd]
+  f16* out;        // [B][H*hd], written by attention_combine
 };
 int attn_decode_chunks(int ctx_max);
 int attn_decode_chunk_keys();
+// Partials of chunks 0..*d_pos/chunk_keys; the Wo GEMV prologue or
+// attention_combine turns them into the attention output.
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st);
+hipError_t attention_combine(const AttnDecode& p, hipStream_t st);
 
 // ---- elementwise / reductions (elementwise.hip) ----
 hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
