@@ -125,14 +125,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
   }
 }
 
-// Tile choice: maximise (relative per-tile throughput) x (fraction of the 256
-// CUs kept busy over the launch's rounds). Relative throughputs are measured
-// on MI355X with many rounds of tiles (7B shapes at 4096 tokens): 256x256
-// (8 waves of 64x128) 1.00, 192x256 (8 waves of 96x64) 0.90, 192x128
-// (4 waves of 96x64) 0.85, 256x128 (8 waves of 64x64) 0.79, 128x128
-// (4 waves of 64x64) 0.77, 64x128 (4 waves of 32x64) 0.55. At 512 tokens
-// this picks 192x256 for W1|W3 (230 tiles instead of 172) and 192x128 for
-// QKV (256 tiles instead of 192).
+// Tile choice: maximise (relative per-tile throughput) x (tiles per CU-round
+// of the 256 CUs). All tiles run 4 waves (2x2); relative throughputs are
+// measured on MI355X with whole rounds of tiles (7B shapes at 4096 tokens):
+// 256x256 1.00, 192x256 0.93, 128x256 0.92, 192x128 0.88, 256x128 0.87,
+// 128x128 0.77, 64x128 0.48. At 512 tokens this picks 192x256 for W1|W3
+// (230 tiles), 192x128 for QKV (256 tiles) and 256x256 for the logits; at
+// 4096 tokens 256x256 throughout.
 //
 // Long-K problems with few output tiles (Wo and W2 at 512 tokens: 128 tiles of
 // 128x128) instead split K over up to GEMM_MAX_SPLITS ranges of >= 8 slices so
@@ -171,7 +170,9 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
   }
   // rel: throughput per CU of each tile shape with every CU busy (7B shapes at
   // 4096 tokens, time per full round of workgroups per tile area, 256x256 = 1);
-  // the score weighs it by the fraction of CU-rounds that hold a tile.
+  // the score weighs it by tiles per CU-round, where a partly filled last round
+  // counts 0.4 + 0.6 x its fill (its tiles run faster with fewer neighbours:
+  // fitted to the measured 7B launches at 512 and 4096 tokens).
   struct Cand {
     int ft, tt;
     float rel;
@@ -183,8 +184,9 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
   float best_score = -1.f;
   for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
     const long n = ntiles(N, T, cands[i].ft, cands[i].tt);
-    const long rounds = (n + GEMM_CUS - 1) / GEMM_CUS;
-    const float score = cands[i].rel * (float)n / (float)(rounds * GEMM_CUS);
+    const float fill = (float)(n % GEMM_CUS) / GEMM_CUS;
+    const float rounds = (float)(n / GEMM_CUS) + (fill > 0.f ? 0.4f + 0.6f * fill : 0.f);
+    const float score = cands[i].rel * (float)n / (rounds * GEMM_CUS);
     if (score > best_score + 1e-6f) {
       best_score = score;
       best = i;
