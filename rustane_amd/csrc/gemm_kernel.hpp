@@ -88,8 +88,16 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wf = wave / WT, wt = wave - wf * WT;
   const int nft = (N + FT - 1) / FT, ntt = (T + TT - 1) / TT;
+  // Tile order: groups of GM weight-row panels, token tiles iterated inside a
+  // group (tile = group*GM*ntt + tt*rows + row), and each XCD takes a
+  // contiguous range of that order. The 32 tiles an XCD runs at a time then
+  // share 8 weight panels and 4 token panels in its L2 instead of 2 and 16:
+  // 7B at 4096 tokens, W1|W3 749 -> 663 us, QKV 372 -> 338 us.
+  constexpr int GM = 8;
   const int tile = xcd_remap(blockIdx.x, nft * ntt);
-  const int ft = tile / ntt, tt = tile - ft * ntt;
+  const int grp = tile / (GM * ntt), rem = tile - grp * (GM * ntt);
+  const int rows = min(GM, nft - grp * GM);
+  const int tt = rem / rows, ft = grp * GM + (rem - tt * rows);
   const int f_base = ft * FT, t_base = tt * TT;
 
   const int r0 = tid >> 3, c0 = tid & 7;
