@@ -25,14 +25,25 @@ def _kernel_metadata():
     objcopy = shutil.which("objcopy") or os.path.join(LLVM, "llvm-objcopy")
     if not (os.path.exists(LIB) and os.path.exists(bundler) and os.path.exists(readelf)):
         pytest.skip("built library or ROCm LLVM tools not present")
+    notes = ""
     with tempfile.TemporaryDirectory() as d:
-        fat, co = os.path.join(d, "fat.bin"), os.path.join(d, "gfx950.co")
+        fat = os.path.join(d, "fat.bin")
         subprocess.run([objcopy, "--dump-section", f".hip_fatbin={fat}", LIB], check=True,
                        capture_output=True)
-        subprocess.run([bundler, "--type=o", "--unbundle", f"--input={fat}", f"--output={co}",
-                        "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True, capture_output=True)
-        notes = subprocess.run([readelf, "--notes", co], check=True, capture_output=True,
-                               text=True).stdout
+        # one offload bundle per translation unit, concatenated; the bundler
+        # reads only the first bundle of a file, so split them
+        data = open(fat, "rb").read()
+        magic = b"__CLANG_OFFLOAD_BUNDLE__"
+        starts = [i for i in range(len(data)) if data.startswith(magic, i)]
+        for n, (a, b) in enumerate(zip(starts, starts[1:] + [len(data)])):
+            part, co = os.path.join(d, f"part{n}.bin"), os.path.join(d, f"part{n}.co")
+            with open(part, "wb") as f:
+                f.write(data[a:b])
+            subprocess.run([bundler, "--type=o", "--unbundle", f"--input={part}", f"--output={co}",
+                            "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True,
+                           capture_output=True)
+            notes += subprocess.run([readelf, "--notes", co], check=True, capture_output=True,
+                                    text=True).stdout
     kernels, cur = [], None
     for line in notes.splitlines():
         if line.startswith("  - "):  # a new entry of amdhsa.kernels
