@@ -315,11 +315,12 @@ def layer_forward(cfg: Config, lw: LayerW, x_cf: np.ndarray, seq: int, rope=None
 
 
 def model_forward(cfg: Config, w: ModelW, tokens, targets=None, softcap: float = 0.0,
-                  want_logits: bool = True, keep_taps: bool = False):
+                  want_logits: bool = True, keep_taps=False):
     """full_model.rs:345-410 / 717-767 for one sequence: embedding + mtrans (201-202) ->
     layers (207-215) -> final RMSNorm (223) -> logits = XF^T E^T into zeroed buffer
     (228-230) -> softcap (234-239) -> CE (242-246). Returns dict(loss, losses, logits,
-    x_final_cf, taps)."""
+    x_final_cf, taps). keep_taps: False, True (every tap of every layer) or a
+    collection of tap names to keep."""
     d, V = cfg.dim, cfg.vocab
     seq = len(tokens)
     x_row = embedding_forward(w.embed, d, tokens)
@@ -328,8 +329,10 @@ def model_forward(cfg: Config, w: ModelW, tokens, targets=None, softcap: float =
     taps = []
     for l in range(cfg.nlayers):
         x, t = layer_forward(cfg, w.layers[l], x, seq, rope)
-        if keep_taps:
+        if keep_taps is True:
             taps.append(t)
+        elif keep_taps:
+            taps.append({k: t[k] for k in keep_taps})
     x_final, _ = rmsnorm_channel_first(x, w.gamma_final, d, seq, cfg.norm_eps)
     x_final_row = mtrans(x_final, d, seq)
     logits = sgemm_at(x_final_row, seq, d, w.embed, V, np.zeros(seq * V, F32))
@@ -374,16 +377,20 @@ class DecodeOracle:
         self.v = np.zeros((L, KVH, ctx_max, hd), F32)
         self.pos = 0
 
-    def prefill(self, tokens) -> np.ndarray:
+    def prefill(self, tokens, targets=None) -> np.ndarray:
         """Full forward over the prompt (model_forward), keeping each layer's K'/V for
-        positions [0, S); returns the last position's logits."""
+        positions [0, S); returns the last position's logits. The whole forward result
+        (logits [S*vocab], and losses/loss when targets are given) stays in
+        self.prefill_out."""
         cfg = self.cfg
         S = len(tokens)
-        out = model_forward(cfg, self.w, tokens, None, cfg.softcap, True, keep_taps=True)
-        for l, t in enumerate(out["taps"]):
+        out = model_forward(cfg, self.w, tokens, targets, cfg.softcap, True,
+                            keep_taps=("k_rope", "v"))
+        for l, t in enumerate(out.pop("taps")):
             self.k[l, :, :S] = t["k_rope"].reshape(cfg.kv_heads, cfg.hd, S).transpose(0, 2, 1)
             self.v[l, :, :S] = t["v"].reshape(cfg.kv_heads, cfg.hd, S).transpose(0, 2, 1)
         self.pos = S
+        self.prefill_out = out
         return out["logits"].reshape(S, cfg.vocab)[-1].copy()
 
     def step(self, token: int) -> np.ndarray:
@@ -404,11 +411,14 @@ class DecodeOracle:
             self.k[l, :, p] = Kr
             self.v[l, :, p] = Vf.reshape(KVH, hd)
             rep = H // KVH
-            K = np.repeat(self.k[l, :, :p + 1], rep, axis=0)  # [H, p+1, hd]
-            Vc = np.repeat(self.v[l, :, :p + 1], rep, axis=0)
-            sc = np.einsum("he,hte->ht", Qr, K).astype(F32) * scale
+            K = self.k[l, :, :p + 1]  # [KVH, p+1, hd]
+            Vc = self.v[l, :, :p + 1]
+            if rep > 1:  # query head h reads kv head h // rep
+                K = np.repeat(K, rep, axis=0)
+                Vc = np.repeat(Vc, rep, axis=0)
+            sc = np.matmul(K, Qr[:, :, None])[:, :, 0].astype(F32) * scale  # [H, p+1]
             pr = _softmax_last(sc)
-            attn = np.einsum("ht,hte->he", pr, Vc).astype(F32).reshape(cfg.q_dim, 1)
+            attn = np.matmul(pr[:, None, :], Vc)[:, 0, :].astype(F32).reshape(cfg.q_dim, 1)
             o = dyn_matmul(attn, lw.wo, cfg.q_dim, d, 1)
             x2 = vsma(o.reshape(-1), alpha, x.reshape(-1)).reshape(d, 1)
             x2n, _ = rmsnorm_channel_first(x2, lw.gamma2, d, 1, cfg.norm_eps)

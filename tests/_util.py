@@ -39,3 +39,46 @@ def f16_round(a):
 def tokens_for(cfg, n, seed=42, stream=0):
     from rustane_amd import hip_bridge as hb
     return hb.synth_tokens(seed, stream, cfg.vocab, n)
+
+
+class SyntheticLayers:
+    """Oracle LayerW for every layer, generated on first access from the seeded
+    stream that hb_model_init_synthetic writes on the device (tensor ids
+    16*layer + 0..6, gammas 1), so a full-size oracle never needs a device
+    copy. cache=True keeps each generated layer (7B: 26.4 GB of fp32 in all)."""
+
+    def __init__(self, cfg, seed, std=0.02, cache=True, round16=False):
+        self.cfg, self.seed, self.std, self.cache, self.round16 = cfg, seed, std, cache, round16
+        self._layers = {}
+
+    def __len__(self):
+        return self.cfg.nlayers
+
+    def __getitem__(self, l):
+        import oracle as O
+        from rustane_amd.engine import LayerWeights
+        if not 0 <= l < self.cfg.nlayers:
+            raise IndexError(l)
+        if l in self._layers:
+            return self._layers[l]
+        lw = LayerWeights.synthetic(self.cfg, l, self.seed, self.std)
+        ow = O.LayerW(**{k: f16_round(getattr(lw, k)) if self.round16 else getattr(lw, k)
+                         for k in O.LayerW.__dataclass_fields__})
+        if self.cache:
+            self._layers[l] = ow
+        return ow
+
+    def __iter__(self):
+        return (self[l] for l in range(len(self)))
+
+
+def synthetic_oracle_weights(cfg, seed, std=0.02, cache=True, round16=False):
+    """O.ModelW equal to ModelWeights.synthetic(cfg, seed, std), layers generated lazily.
+    round16=True rounds every weight to fp16 (the values the device holds) and
+    keeps them as fp32 for the oracle's arithmetic."""
+    import oracle as O
+    from rustane_amd import hip_bridge as hb
+    e = hb.synth_normal(seed, hb.HB_SYNTH_EMBED_ID, cfg.vocab * cfg.dim, std)
+    return O.ModelW(embed=f16_round(e) if round16 else e,
+                    layers=SyntheticLayers(cfg, seed, std, cache, round16),
+                    gamma_final=np.ones(cfg.dim, F32))
