@@ -69,6 +69,7 @@ def main():
     ap.add_argument("--decode-b16", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-optimizer", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (timed) and a 1 GiB device copy, for counter runs")
     args = ap.parse_args()
@@ -202,6 +203,10 @@ def main():
             dec.kv.close()
         extra["decode"] = dec_res
 
+    # ---- optimizer step over the whole model ----
+    if not args.no_optimizer:
+        extra["optimizer"] = bench_optimizer(k, stream, cpu=not args.no_cpu_baseline)
+
     # ---- CPU baseline (oracle, bounded sample) ----
     if not args.no_cpu_baseline:
         extra["cpu_baseline"] = cpu_baseline(cfg, S)
@@ -280,6 +285,87 @@ def time_dominant_kernel(k, cfg, T, launches, stream):
                 "kernel": "gemm_nt_kernel<192,256,2,2,EpiSwiGLU> (FFN up, W1|W3 + SwiGLU)",
                 "flop_per_launch": up_flops, "us_per_launch": round(up_ms * 1e3, 2)}
     return roofline, up_ms
+
+
+class _DeviceArray:
+    """A raw device pointer as a CUDA-array-interface object (for torch.as_tensor)."""
+
+    def __init__(self, ptr, n):
+        self.__cuda_array_interface__ = {"shape": (n,), "typestr": "<f4", "data": (ptr, False),
+                                         "version": 2}
+
+
+def bench_optimizer(k, stream, cpu=True, steps=3):
+    """train_step's optimizer half on the whole 7B-shape model (hb_opt_step:
+    gradient norm + clip decision + fused AdamW over every weight, refreshing
+    the fp16 copy), and the AdamW pass alone (hb_opt_update_weights, the
+    dominant kernel: 30 bytes per parameter -- read param/grad/m/v, write
+    param/m/v and the fp16 weight). Gradients are N(0, 1e-3) noise written
+    into the device arena."""
+    import torch
+    from rustane_amd import hip_bridge as hb
+    from rustane_amd.engine import TrainConfig
+    opt = hb.Optimizer(k.model, TrainConfig())
+    try:
+        ptr, n = opt.grad_arena()
+        try:
+            torch.as_tensor(_DeviceArray(ptr, n), device="cuda").normal_(0.0, 1e-3)
+            grads = "N(0, 1e-3)"
+        except Exception as e:  # pragma: no cover - interface not available
+            log(f"[bench] optimizer: gradients left at zero ({e})")
+            grads = "zero"
+        opt.step(0, want_norm=False)
+        opt.update_weights(2, 1e-4, 1.0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for s in range(1, steps + 1):
+            opt.step(s, want_norm=False)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        step_ms = e0.elapsed_time(e1) / steps
+        e0.record(stream)
+        for t in range(1, steps + 1):
+            opt.update_weights(t + 3, 1e-4, 1.0)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        upd_ms = e0.elapsed_time(e1) / steps
+        norm = opt.grad_norm()
+    finally:
+        opt.close()
+    upd_bytes, step_bytes = 30 * n, 34 * n
+    gbs = upd_bytes / (upd_ms / 1e3) / 1e9
+    res = {"params": n, "grads": grads, "grad_norm": round(norm, 4),
+           "ms_per_optimizer_step": round(step_ms, 3),
+           "step_GB_per_s": round(step_bytes / (step_ms / 1e3) / 1e9, 1),
+           "adamw_ms": round(upd_ms, 3), "adamw_GB_per_s": round(gbs, 1),
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK / 1e9,
+                        "unit": "GB/s", "frac": round(gbs * 1e9 / HBM_PEAK, 4),
+                        "traffic": None, "kernel": "adamw_kernel<true> (fused AdamW, fp16 refresh)",
+                        "bytes_per_launch_set": upd_bytes}}
+    if cpu:
+        res["cpu_baseline"] = cpu_baseline_adam(n)
+    log(f"[bench] optimizer: {res}")
+    return res
+
+
+def cpu_baseline_adam(n_params, sample=1 << 26):
+    """The oracle's fused AdamW (cpu/adam.rs:95-132 in numpy fp32) on a
+    64M-parameter sample; the whole-model time is scaled from it."""
+    import oracle.optimizer as OP
+    rng = np.random.default_rng(0)
+    p = rng.standard_normal(sample, dtype=np.float32)
+    g = (rng.standard_normal(sample, dtype=np.float32) * np.float32(1e-3)).astype(np.float32)
+    m = np.zeros(sample, np.float32)
+    v = np.zeros(sample, np.float32)
+    best = 1e9
+    for t in (1, 2):
+        t0 = time.perf_counter()
+        OP.step_fused(p, g, m, v, t, 1e-4, 0.9, 0.95, 1e-8, 0.1, 1.0)
+        best = min(best, time.perf_counter() - t0)
+    return {"value": round(sample / best / 1e6, 1), "unit": "M params/s", "cores": 1, "kind": "port",
+            "sample": f"numpy fp32 step_fused on {sample} parameters (best of 2): {best*1e3:.0f} ms; "
+                      f"whole model {n_params * best / sample:.1f} s"}
 
 
 def cpu_baseline(cfg, S):

@@ -54,6 +54,7 @@ enum { HB_DTYPE_F16 = 1 };
 typedef struct hb_ctx hb_ctx;
 typedef struct hb_model hb_model;
 typedef struct hb_kv hb_kv;
+typedef struct hb_opt hb_opt;
 
 /*
  * Model shape. Field names and meaning follow rustane's ModelConfig
@@ -258,6 +259,85 @@ int hb_decode_step(hb_model* model, hb_kv* kv, const uint32_t* h_tokens, float* 
  */
 int hb_decode_greedy(hb_model* model, hb_kv* kv, const uint32_t* h_first, int nsteps,
                      uint32_t* h_out);
+
+/* ---- optimizer: fused AdamW, gradient norm and clipping -------------------- */
+
+/* TrainConfig (full_model.rs:33-70): the fields the optimizer step reads. */
+typedef struct hb_train_config {
+  float max_lr;          /* 3e-4   */
+  float min_lr_frac;     /* 0.1    */
+  uint32_t warmup_steps; /* 100    */
+  uint32_t total_steps;  /* 10000  */
+  float beta1;           /* 0.9    */
+  float beta2;           /* 0.95   */
+  float eps;             /* 1e-8   */
+  float weight_decay;    /* 0.1    */
+  float matrix_lr_scale; /* 0.05   */
+  float embed_lr_scale;  /* 5.0    */
+  float loss_scale;      /* 256    */
+  uint32_t accum_steps;  /* 10     */
+  float grad_clip;       /* 1.0    */
+} hb_train_config;
+
+/* learning_rate (full_model.rs:334-342): linear warmup, then cosine decay to
+ * max_lr * min_lr_frac, in fp32 as the reference computes it. */
+int hb_learning_rate(const hb_train_config* tc, uint32_t step, float* out_lr);
+
+/*
+ * Optimizer state of a model: ModelOptState (full_model.rs:26-31) plus the
+ * ModelGrads arena (full_model.rs:20-24) and an fp32 master copy of every
+ * weight, all on the device in the packed order of the fp16 weights (one
+ * fused pass updates master, m, v and the fp16 copy; 4 fp32 arenas, 16 bytes
+ * per parameter). m, v and the gradients start at 0; the master copy starts
+ * from the model's current fp16 weights, or from fp32 values given by
+ * hb_opt_upload_layer / hb_opt_upload_embed / hb_opt_init_synthetic.
+ */
+int hb_opt_create(hb_model* model, const hb_train_config* tc, hb_opt** out);
+int hb_opt_destroy(hb_opt* opt);
+/* fp32 weights in the reference layouts of hb_model_upload_layer/_embed
+ * (layer.rs:16-26, full_model.rs:13-17): written to the master copy and, as
+ * fp16, to the model. */
+int hb_opt_upload_layer(hb_opt* opt, int layer, const float* wq, const float* wk, const float* wv,
+                        const float* wo, const float* w1, const float* w3, const float* w2,
+                        const float* gamma1, const float* gamma2);
+int hb_opt_upload_embed(hb_opt* opt, const float* embed, const float* gamma_final);
+/* hb_model_init_synthetic into the master copy and the model. */
+int hb_opt_init_synthetic(hb_opt* opt, uint64_t seed, float std);
+/* Gradients in the reference layouts (LayerGrads, layer.rs:29-39: dwq [dim*q],
+ * ..., dw2 [dim*hidden], dgamma1, dgamma2; dembed, dgamma_final), replacing
+ * the arena's contents for that layer / the embedding. */
+int hb_opt_upload_grads_layer(hb_opt* opt, int layer, const float* dwq, const float* dwk,
+                              const float* dwv, const float* dwo, const float* dw1,
+                              const float* dw3, const float* dw2, const float* dgamma1,
+                              const float* dgamma2);
+int hb_opt_upload_grads_embed(hb_opt* opt, const float* dembed, const float* dgamma_final);
+/* ModelGrads::zero_out (train_step, full_model.rs:670). */
+int hb_opt_zero_grads(hb_opt* opt);
+/* The device gradient arena (fp32, packed order) for producers on the device:
+ * pointer and length in floats. */
+int hb_opt_grad_arena(hb_opt* opt, float** d_grads, uint64_t* n_floats);
+/* grad_norm (full_model.rs:600-622): global L2 norm of all gradients. */
+int hb_opt_grad_norm(hb_opt* opt, float* out_norm);
+/* clip_grads (full_model.rs:625-641): scale all gradients by max_norm/norm
+ * when norm > max_norm. The norm (nullable) is returned. */
+int hb_opt_clip_grads(hb_opt* opt, float max_norm, float* out_norm);
+/* update_weights (full_model.rs:487-592) with step count t (1-based) and base
+ * learning rate lr: matrices at lr*matrix_lr_scale with weight decay, the
+ * embedding at lr*embed_lr_scale and the gammas at lr without; gradients
+ * multiplied by grad_scale inline. Asynchronous on the context stream. */
+int hb_opt_update_weights(hb_opt* opt, uint32_t t, float lr, float grad_scale);
+/* The optimizer half of train_step (full_model.rs:697-711) after `step`
+ * completed microbatches of accumulation: grad norm, the combined
+ * descale/clip factor (decided on the device: no host round trip),
+ * learning_rate(step), update_weights(t = step + 1). out_norm (nullable)
+ * receives the raw norm, which waits for the step to finish. */
+int hb_opt_step(hb_opt* opt, uint32_t step, float* out_norm);
+/* Read state back in the reference layouts: which = 0 master weights, 1 m,
+ * 2 v, 3 gradients. */
+int hb_opt_download_layer(hb_opt* opt, int layer, int which, float* wq, float* wk, float* wv,
+                          float* wo, float* w1, float* w3, float* w2, float* gamma1,
+                          float* gamma2);
+int hb_opt_download_embed(hb_opt* opt, int which, float* embed, float* gamma_final);
 
 /* ---- failure injection (host-side test hook) ------------------------------ */
 /* While `code` != 0, every entry point above except hb_last_error,

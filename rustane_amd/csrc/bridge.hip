@@ -746,6 +746,477 @@ extern "C" int hb_model_init_synthetic(hb_model* m, uint64_t seed, float std) {
 }
 
 // ---------------------------------------------------------------------------
+// optimizer
+// ---------------------------------------------------------------------------
+namespace {
+enum { OPT_MATRIX = 0, OPT_EMBED = 1, OPT_GAMMA = 2 };
+// A run of elements that one AdamW launch updates: arena offset, length,
+// learning-rate group and the model tensor (fp16 weights or fp32 gammas)
+// rewritten from the new master values.
+struct OptSeg {
+  size_t off, n;
+  int group;
+  f16* d16;
+  float* d32;
+};
+struct OptLayerOff {
+  size_t wqkv, wo, w13, w2, g1, g2;
+};
+
+// f32::powi as the reference's bias corrections evaluate it (cpu/adam.rs:113-114):
+// exponentiation by squaring in fp32 (the compiler-rt __powisf2 algorithm
+// that llvm.powi.f32 lowers to).
+float powi_f32(float a, int b) {
+  const bool recip = b < 0;
+  float r = 1.0f;
+  for (;;) {
+    if (b & 1) r *= a;
+    b /= 2;
+    if (b == 0) break;
+    a *= a;
+  }
+  return recip ? 1.0f / r : r;
+}
+
+float learning_rate_f32(const hb_train_config& tc, uint32_t step) {
+  if (step < tc.warmup_steps) return tc.max_lr * (float)(step + 1) / (float)tc.warmup_steps;
+  const float decay = (float)(step - tc.warmup_steps) / (float)(tc.total_steps - tc.warmup_steps);
+  const float min_lr = tc.max_lr * tc.min_lr_frac;
+  const float pi = 3.14159265358979323846f;
+  return min_lr + 0.5f * (1.0f + cosf(pi * decay)) * (tc.max_lr - min_lr);
+}
+
+// out[i*C + j] = packed element that repack(mode, row0, ld) wrote for src[i][j].
+void unpack_host(const float* packed, int R, int C, int ld, int row0, int mode, float* out) {
+  for (int i = 0; i < R; ++i)
+    for (int j = 0; j < C; ++j) {
+      const int row = mode == 0 ? row0 + j : mode == 1 ? ((j >> 1) << 2) + (j & 1) + row0 : row0 + i;
+      out[(size_t)i * C + j] = packed[(size_t)row * ld + (mode == 2 ? j : i)];
+    }
+}
+
+int validate_train_config(const hb_train_config& tc) {
+  if (!(tc.beta1 >= 0.f && tc.beta1 < 1.f && tc.beta2 >= 0.f && tc.beta2 < 1.f))
+    return fail(HB_E_INVALID, "betas must be in [0, 1)");
+  if (!(tc.eps > 0.f) || !(tc.loss_scale > 0.f) || tc.accum_steps == 0 || !(tc.grad_clip > 0.f))
+    return fail(HB_E_INVALID, "eps, loss_scale, accum_steps and grad_clip must be positive");
+  if (tc.warmup_steps == 0 || tc.total_steps <= tc.warmup_steps)
+    return fail(HB_E_INVALID, "need 0 < warmup_steps < total_steps");
+  return HB_OK;
+}
+}  // namespace
+
+struct hb_opt {
+  hb_model* model = nullptr;
+  int device = 0;
+  hb_train_config tc{};
+  void* base = nullptr;
+  size_t n = 0;  // floats per arena
+  float *p = nullptr, *g = nullptr, *m = nullptr, *v = nullptr;
+  std::vector<OptSeg> segs;
+  std::vector<OptLayerOff> lo;
+  size_t embed_off = 0, gf_off = 0;
+  double* partials = nullptr;
+  float* scal = nullptr;  // [0] norm, [1] train_step scale, [2] clip_grads factor
+};
+
+extern "C" int hb_learning_rate(const hb_train_config* tc, uint32_t step, float* out) {
+  HB_INJECT_CHECK();
+  if (!tc || !out) return fail(HB_E_INVALID, "null argument");
+  TRY(validate_train_config(*tc));
+  *out = learning_rate_f32(*tc, step);
+  return HB_OK;
+}
+
+extern "C" int hb_opt_create(hb_model* mo, const hb_train_config* tc, hb_opt** out) {
+  HB_INJECT_CHECK();
+  if (!mo || !tc || !out) return fail(HB_E_INVALID, "null argument");
+  *out = nullptr;
+  TRY(validate_train_config(*tc));
+  DeviceGuard gd(mo->ctx->device);
+  const hb_model_config& c = mo->cfg;
+  const size_t d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden, V = c.vocab;
+  hb_opt* o = new hb_opt();
+  o->model = mo;
+  o->device = mo->device;
+  o->tc = *tc;
+  size_t off = 0;
+  std::vector<OptSeg> raw;
+  for (int l = 0; l < c.nlayers; ++l) {
+    LayerW& L = mo->layers[l];
+    OptLayerOff lo{};
+    auto add = [&](size_t n, int group, f16* d16, float* d32) {
+      raw.push_back(OptSeg{off, n, group, d16, d32});
+      const size_t at = off;
+      off += n;
+      return at;
+    };
+    lo.wqkv = add((q + 2 * kv) * d, OPT_MATRIX, L.wqkv, nullptr);
+    lo.wo = add(d * q, OPT_MATRIX, L.wo, nullptr);
+    lo.w13 = add(2 * h * d, OPT_MATRIX, L.w13, nullptr);
+    lo.w2 = add(d * h, OPT_MATRIX, L.w2, nullptr);
+    lo.g1 = add(d, OPT_GAMMA, nullptr, L.g1);
+    lo.g2 = add(d, OPT_GAMMA, nullptr, L.g2);
+    o->lo.push_back(lo);
+  }
+  o->embed_off = off;
+  raw.push_back(OptSeg{off, V * d, OPT_EMBED, mo->embed, nullptr});
+  off += V * d;
+  o->gf_off = off;
+  raw.push_back(OptSeg{off, d, OPT_GAMMA, nullptr, mo->gamma_f});
+  off += d;
+  o->n = off;
+  // one launch per run of same-group tensors that are contiguous in both the
+  // arenas and the model's weights (a layer's four matrices are)
+  for (const OptSeg& sg : raw) {
+    if (!o->segs.empty()) {
+      OptSeg& b = o->segs.back();
+      const bool same = b.group == sg.group && b.off + b.n == sg.off &&
+                        ((b.d16 && sg.d16 && b.d16 + b.n == sg.d16) ||
+                         (b.d32 && sg.d32 && b.d32 + b.n == sg.d32));
+      if (same) {
+        b.n += sg.n;
+        continue;
+      }
+    }
+    o->segs.push_back(sg);
+  }
+  const size_t arena = align256(o->n * 4);
+  const size_t total = 4 * arena + align256(SUMSQ_BLOCKS * 8) + 256;
+  char* b = nullptr;
+  hipError_t e = hipMalloc(&b, total);
+  if (e != hipSuccess) {
+    delete o;
+    return fail(e == hipErrorOutOfMemory ? HB_E_OOM : HB_E_DEVICE,
+                "optimizer state of %zu bytes: %s", total, hipGetErrorString(e));
+  }
+  o->base = b;
+  o->p = (float*)b;
+  o->g = (float*)(b + arena);
+  o->m = (float*)(b + 2 * arena);
+  o->v = (float*)(b + 3 * arena);
+  o->partials = (double*)(b + 4 * arena);
+  o->scal = (float*)(b + 4 * arena + align256(SUMSQ_BLOCKS * 8));
+  hipStream_t st = mo->ctx->stream();
+  auto init = [&]() -> int {
+    HIP_TRY(hipMemsetAsync(b + arena, 0, 3 * arena, st));  // g, m, v
+    for (const OptSeg& sg : raw) {
+      if (sg.d16)
+        HIP_TRY(widen_f16(sg.d16, o->p + sg.off, sg.n, st));
+      else
+        HIP_TRY(hipMemcpyAsync(o->p + sg.off, sg.d32, sg.n * 4, hipMemcpyDeviceToDevice, st));
+    }
+    HIP_TRY(hipStreamSynchronize(st));
+    return HB_OK;
+  };
+  int r = init();
+  if (r != HB_OK) {
+    (void)hipFree(b);
+    delete o;
+    return r;
+  }
+  *out = o;
+  return HB_OK;
+}
+
+extern "C" int hb_opt_destroy(hb_opt* o) {
+  if (!o) return HB_OK;
+  DeviceGuard g(o->device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(o->base);
+  delete o;
+  return HB_OK;
+}
+
+namespace {
+// Host fp32 [R][C] (reference layout) -> staging -> packed fp32 at dst32 and,
+// when dst16 is set, packed fp16 at dst16.
+int opt_put(hb_model* m, const float* src, int R, int C, float* dst32, f16* dst16, int ld, int row0,
+            int mode) {
+  TRY(ensure_staging(m, (size_t)R * C));
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(m->staging, src, (size_t)R * C * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(repack_f32(m->staging, R, C, dst32, ld, row0, mode, st));
+  if (dst16) HIP_TRY(repack(m->staging, R, C, dst16, ld, row0, mode, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+
+// Reference-layout layer tensors into arena `a` (and the model when `model`).
+int opt_put_layer(hb_opt* o, float* a, bool model, int layer, const float* const w[9]) {
+  hb_model* m = o->model;
+  const hb_model_config& c = m->cfg;
+  LayerW& L = m->layers[layer];
+  const OptLayerOff& lo = o->lo[layer];
+  const int d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden;
+  TRY(opt_put(m, w[0], d, q, a + lo.wqkv, model ? L.wqkv : nullptr, d, 0, 0));
+  TRY(opt_put(m, w[1], d, kv, a + lo.wqkv, model ? L.wqkv : nullptr, d, q, 0));
+  TRY(opt_put(m, w[2], d, kv, a + lo.wqkv, model ? L.wqkv : nullptr, d, q + kv, 0));
+  TRY(opt_put(m, w[3], q, d, a + lo.wo, model ? L.wo : nullptr, q, 0, 0));
+  TRY(opt_put(m, w[4], d, h, a + lo.w13, model ? L.w13 : nullptr, d, 0, 1));
+  TRY(opt_put(m, w[5], d, h, a + lo.w13, model ? L.w13 : nullptr, d, 2, 1));
+  TRY(opt_put(m, w[6], d, h, a + lo.w2, model ? L.w2 : nullptr, h, 0, 2));
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(a + lo.g1, w[7], d * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(a + lo.g2, w[8], d * 4, hipMemcpyHostToDevice, st));
+  if (model) {
+    HIP_TRY(hipMemcpyAsync(L.g1, w[7], d * 4, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(L.g2, w[8], d * 4, hipMemcpyHostToDevice, st));
+    L.uploaded = true;
+    m->dec_stale = true;
+  }
+  HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+
+int opt_put_embed(hb_opt* o, float* a, bool model, const float* embed, const float* gf) {
+  hb_model* m = o->model;
+  const hb_model_config& c = m->cfg;
+  const int rows_per = std::max(1, (int)std::min<size_t>(c.vocab, (64u << 20) / c.dim));
+  for (int r0 = 0; r0 < c.vocab; r0 += rows_per) {
+    const int rows = std::min(rows_per, c.vocab - r0);
+    TRY(opt_put(m, embed + (size_t)r0 * c.dim, rows, c.dim, a + o->embed_off,
+                model ? m->embed : nullptr, c.dim, r0, 2));
+  }
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(a + o->gf_off, gf, c.dim * 4, hipMemcpyHostToDevice, st));
+  if (model) {
+    HIP_TRY(hipMemcpyAsync(m->gamma_f, gf, c.dim * 4, hipMemcpyHostToDevice, st));
+    m->embed_uploaded = true;
+    m->dec_stale = true;
+  }
+  HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+
+float* opt_arena(hb_opt* o, int which) {
+  return which == 0 ? o->p : which == 1 ? o->m : which == 2 ? o->v : which == 3 ? o->g : nullptr;
+}
+
+// Device part of update_weights: one fused AdamW launch per segment.
+int opt_update(hb_opt* o, uint32_t t, float lr, float grad_scale, const float* d_gscale) {
+  const hb_train_config& tc = o->tc;
+  hipStream_t st = o->model->ctx->stream();
+  AdamW h{};
+  h.b1 = tc.beta1;
+  h.b2 = tc.beta2;
+  h.omb1 = 1.0f - tc.beta1;
+  h.omb2 = 1.0f - tc.beta2;
+  h.eps = tc.eps;
+  h.bc1 = 1.0f / (1.0f - powi_f32(tc.beta1, (int)t));
+  h.bc2 = 1.0f / (1.0f - powi_f32(tc.beta2, (int)t));
+  h.gscale = grad_scale;
+  const float matrix_lr = lr * tc.matrix_lr_scale, embed_lr = lr * tc.embed_lr_scale;
+  for (const OptSeg& sg : o->segs) {
+    AdamW hs = h;
+    hs.lr = sg.group == OPT_MATRIX ? matrix_lr : sg.group == OPT_EMBED ? embed_lr : lr;
+    hs.wd = sg.group == OPT_MATRIX ? tc.weight_decay : 0.0f;
+    HIP_TRY(adamw(o->p + sg.off, o->g + sg.off, o->m + sg.off, o->v + sg.off, sg.d16, sg.d32, sg.n,
+                  hs, d_gscale, st));
+  }
+  o->model->dec_stale = true;
+  return HB_OK;
+}
+
+int opt_norm(hb_opt* o, ClipCfg cc) {
+  hipStream_t st = o->model->ctx->stream();
+  HIP_TRY(grad_sumsq(o->g, o->n, o->partials, st));
+  HIP_TRY(grad_clip_scale(o->partials, cc, o->scal, st));
+  return HB_OK;
+}
+
+int opt_read_norm(hb_opt* o, float* out) {
+  hipStream_t st = o->model->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(out, o->scal, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+}  // namespace
+
+#define HB_OPT_CHECK(o)                                        \
+  do {                                                         \
+    HB_INJECT_CHECK();                                         \
+    if (!(o)) return fail(HB_E_INVALID, "null optimizer");     \
+  } while (0)
+
+extern "C" int hb_opt_upload_layer(hb_opt* o, int layer, const float* wq, const float* wk,
+                                   const float* wv, const float* wo, const float* w1,
+                                   const float* w3, const float* w2, const float* g1,
+                                   const float* g2) {
+  HB_OPT_CHECK(o);
+  if (layer < 0 || layer >= o->model->cfg.nlayers) return fail(HB_E_INVALID, "layer %d out of range", layer);
+  const float* w[9] = {wq, wk, wv, wo, w1, w3, w2, g1, g2};
+  for (const float* x : w)
+    if (!x) return fail(HB_E_INVALID, "null weight pointer");
+  DeviceGuard g(o->device);
+  return opt_put_layer(o, o->p, true, layer, w);
+}
+
+extern "C" int hb_opt_upload_embed(hb_opt* o, const float* embed, const float* gamma_final) {
+  HB_OPT_CHECK(o);
+  if (!embed || !gamma_final) return fail(HB_E_INVALID, "null argument");
+  DeviceGuard g(o->device);
+  return opt_put_embed(o, o->p, true, embed, gamma_final);
+}
+
+extern "C" int hb_opt_init_synthetic(hb_opt* o, uint64_t seed, float std) {
+  HB_OPT_CHECK(o);
+  if (!(std > 0.f)) return fail(HB_E_INVALID, "std must be positive");
+  DeviceGuard gd(o->device);
+  hb_model* m = o->model;
+  TRY(hb_model_init_synthetic(m, seed, std));
+  const hb_model_config& c = m->cfg;
+  hipStream_t st = m->ctx->stream();
+  const float sc = hb_normal_scale(std);
+  const int d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden;
+  // the same seeded fp32 arrays hb_model_init_synthetic generated, packed in fp32
+  auto put = [&](uint64_t id, int R, int C, float* dst, int ld, int row0, int mode) -> int {
+    TRY(ensure_staging(m, (size_t)R * C));
+    HIP_TRY(synth_f32(seed, id, sc, 0, (size_t)R * C, m->staging, st));
+    HIP_TRY(repack_f32(m->staging, R, C, dst, ld, row0, mode, st));
+    return HB_OK;
+  };
+  for (int l = 0; l < c.nlayers; ++l) {
+    const OptLayerOff& lo = o->lo[l];
+    const uint64_t id = 16ull * l;
+    TRY(put(id + 0, d, q, o->p + lo.wqkv, d, 0, 0));
+    TRY(put(id + 1, d, kv, o->p + lo.wqkv, d, q, 0));
+    TRY(put(id + 2, d, kv, o->p + lo.wqkv, d, q + kv, 0));
+    TRY(put(id + 3, q, d, o->p + lo.wo, q, 0, 0));
+    TRY(put(id + 4, d, h, o->p + lo.w13, d, 0, 1));
+    TRY(put(id + 5, d, h, o->p + lo.w13, d, 2, 1));
+    TRY(put(id + 6, d, h, o->p + lo.w2, h, 0, 2));
+    HIP_TRY(fill_f32(o->p + lo.g1, 1.0f, d, st));
+    HIP_TRY(fill_f32(o->p + lo.g2, 1.0f, d, st));
+  }
+  const int rows_per = std::max(1, (int)std::min<size_t>(c.vocab, (64u << 20) / c.dim));
+  for (int r0 = 0; r0 < c.vocab; r0 += rows_per) {
+    const int rows = std::min(rows_per, c.vocab - r0);
+    TRY(ensure_staging(m, (size_t)rows * d));
+    HIP_TRY(synth_f32(seed, HB_SYNTH_EMBED_ID, sc, (uint64_t)r0 * d, (size_t)rows * d, m->staging, st));
+    HIP_TRY(repack_f32(m->staging, rows, d, o->p + o->embed_off, d, r0, 2, st));
+  }
+  HIP_TRY(fill_f32(o->p + o->gf_off, 1.0f, d, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+
+extern "C" int hb_opt_upload_grads_layer(hb_opt* o, int layer, const float* dwq, const float* dwk,
+                                         const float* dwv, const float* dwo, const float* dw1,
+                                         const float* dw3, const float* dw2, const float* dg1,
+                                         const float* dg2) {
+  HB_OPT_CHECK(o);
+  if (layer < 0 || layer >= o->model->cfg.nlayers) return fail(HB_E_INVALID, "layer %d out of range", layer);
+  const float* w[9] = {dwq, dwk, dwv, dwo, dw1, dw3, dw2, dg1, dg2};
+  for (const float* x : w)
+    if (!x) return fail(HB_E_INVALID, "null gradient pointer");
+  DeviceGuard g(o->device);
+  return opt_put_layer(o, o->g, false, layer, w);
+}
+
+extern "C" int hb_opt_upload_grads_embed(hb_opt* o, const float* dembed, const float* dgamma_final) {
+  HB_OPT_CHECK(o);
+  if (!dembed || !dgamma_final) return fail(HB_E_INVALID, "null argument");
+  DeviceGuard g(o->device);
+  return opt_put_embed(o, o->g, false, dembed, dgamma_final);
+}
+
+extern "C" int hb_opt_zero_grads(hb_opt* o) {
+  HB_OPT_CHECK(o);
+  DeviceGuard g(o->device);
+  HIP_TRY(fill_f32(o->g, 0.0f, o->n, o->model->ctx->stream()));
+  return HB_OK;
+}
+
+extern "C" int hb_opt_grad_arena(hb_opt* o, float** d_grads, uint64_t* n_floats) {
+  HB_OPT_CHECK(o);
+  if (!d_grads || !n_floats) return fail(HB_E_INVALID, "null argument");
+  *d_grads = o->g;
+  *n_floats = o->n;
+  return HB_OK;
+}
+
+extern "C" int hb_opt_grad_norm(hb_opt* o, float* out_norm) {
+  HB_OPT_CHECK(o);
+  if (!out_norm) return fail(HB_E_INVALID, "null argument");
+  DeviceGuard g(o->device);
+  TRY(opt_norm(o, ClipCfg{1.0f, o->tc.grad_clip}));
+  return opt_read_norm(o, out_norm);
+}
+
+extern "C" int hb_opt_clip_grads(hb_opt* o, float max_norm, float* out_norm) {
+  HB_OPT_CHECK(o);
+  if (!(max_norm > 0.f)) return fail(HB_E_INVALID, "max_norm must be positive");
+  DeviceGuard g(o->device);
+  TRY(opt_norm(o, ClipCfg{1.0f, max_norm}));
+  HIP_TRY(scale_inplace(o->g, o->n, o->scal + 2, o->model->ctx->stream()));
+  return out_norm ? opt_read_norm(o, out_norm) : HB_OK;
+}
+
+extern "C" int hb_opt_update_weights(hb_opt* o, uint32_t t, float lr, float grad_scale) {
+  HB_OPT_CHECK(o);
+  if (t == 0) return fail(HB_E_INVALID, "t is 1-based");
+  DeviceGuard g(o->device);
+  return opt_update(o, t, lr, grad_scale, nullptr);
+}
+
+extern "C" int hb_opt_step(hb_opt* o, uint32_t step, float* out_norm) {
+  HB_OPT_CHECK(o);
+  DeviceGuard g(o->device);
+  const hb_train_config& tc = o->tc;
+  const float gsc = 1.0f / ((float)tc.accum_steps * tc.loss_scale);
+  TRY(opt_norm(o, ClipCfg{gsc, tc.grad_clip}));
+  TRY(opt_update(o, step + 1, learning_rate_f32(tc, step), 0.0f, o->scal + 1));
+  return out_norm ? opt_read_norm(o, out_norm) : HB_OK;
+}
+
+extern "C" int hb_opt_download_layer(hb_opt* o, int layer, int which, float* wq, float* wk,
+                                     float* wv, float* wo, float* w1, float* w3, float* w2,
+                                     float* g1, float* g2) {
+  HB_OPT_CHECK(o);
+  const hb_model_config& c = o->model->cfg;
+  if (layer < 0 || layer >= c.nlayers) return fail(HB_E_INVALID, "layer %d out of range", layer);
+  float* a = opt_arena(o, which);
+  if (!a) return fail(HB_E_INVALID, "which must be 0 (weights), 1 (m), 2 (v) or 3 (gradients)");
+  float* w[9] = {wq, wk, wv, wo, w1, w3, w2, g1, g2};
+  for (float* x : w)
+    if (!x) return fail(HB_E_INVALID, "null output pointer");
+  DeviceGuard g(o->device);
+  const OptLayerOff& lo = o->lo[layer];
+  const int d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden;
+  const size_t n = lo.g2 + d - lo.wqkv;
+  std::vector<float> host(n);
+  hipStream_t st = o->model->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(host.data(), a + lo.wqkv, n * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  const float* b = host.data();
+  unpack_host(b, d, q, d, 0, 0, wq);
+  unpack_host(b, d, kv, d, q, 0, wk);
+  unpack_host(b, d, kv, d, q + kv, 0, wv);
+  unpack_host(b + (lo.wo - lo.wqkv), q, d, q, 0, 0, wo);
+  unpack_host(b + (lo.w13 - lo.wqkv), d, h, d, 0, 1, w1);
+  unpack_host(b + (lo.w13 - lo.wqkv), d, h, d, 2, 1, w3);
+  unpack_host(b + (lo.w2 - lo.wqkv), d, h, h, 0, 2, w2);
+  std::memcpy(g1, b + (lo.g1 - lo.wqkv), d * 4);
+  std::memcpy(g2, b + (lo.g2 - lo.wqkv), d * 4);
+  return HB_OK;
+}
+
+extern "C" int hb_opt_download_embed(hb_opt* o, int which, float* embed, float* gamma_final) {
+  HB_OPT_CHECK(o);
+  float* a = opt_arena(o, which);
+  if (!a) return fail(HB_E_INVALID, "which must be 0 (weights), 1 (m), 2 (v) or 3 (gradients)");
+  if (!embed || !gamma_final) return fail(HB_E_INVALID, "null output pointer");
+  DeviceGuard g(o->device);
+  const hb_model_config& c = o->model->cfg;
+  hipStream_t st = o->model->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(embed, a + o->embed_off, (size_t)c.vocab * c.dim * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(gamma_final, a + o->gf_off, c.dim * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+
+// ---------------------------------------------------------------------------
 // synthetic host inputs
 // ---------------------------------------------------------------------------
 template <class F>

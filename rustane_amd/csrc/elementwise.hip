@@ -222,9 +222,12 @@ HB_DEV int repack_row(int mode, int i, int j, int row0) {
   return row0 + i;
 }
 
-// 64x64 tiles through LDS so both the fp32 reads and fp16 writes are coalesced.
+// 64x64 tiles through LDS so both the fp32 reads and the writes are coalesced.
+// D is f16 (the weights the GEMMs read) or float (the optimizer's fp32 master
+// copy, stored in the same packed order).
+template <class D>
 __global__ __launch_bounds__(256) void repack_kernel(const float* __restrict__ src, int R, int C,
-                                                     f16* __restrict__ dst, int ld, int row0,
+                                                     D* __restrict__ dst, int ld, int row0,
                                                      int mode) {
   __shared__ float tile[64][65];
   const int i0 = blockIdx.y * 64, j0 = blockIdx.x * 64;
@@ -237,13 +240,13 @@ __global__ __launch_bounds__(256) void repack_kernel(const float* __restrict__ s
   if (mode == 2) {
     for (int r = ty; r < 64; r += 4) {
       const int i = i0 + r, j = j0 + tx;
-      if (i < R && j < C) dst[(size_t)repack_row(mode, i, j, row0) * ld + j] = (f16)tile[r][tx];
+      if (i < R && j < C) dst[(size_t)repack_row(mode, i, j, row0) * ld + j] = (D)tile[r][tx];
     }
   } else {
     // dst row indexed by source column j, dst column = source row i.
     for (int r = ty; r < 64; r += 4) {
       const int j = j0 + r, i = i0 + tx;
-      if (i < R && j < C) dst[(size_t)repack_row(mode, i, j, row0) * ld + i] = (f16)tile[tx][r];
+      if (i < R && j < C) dst[(size_t)repack_row(mode, i, j, row0) * ld + i] = (D)tile[tx][r];
     }
   }
 }
@@ -251,7 +254,14 @@ __global__ __launch_bounds__(256) void repack_kernel(const float* __restrict__ s
 hipError_t repack(const float* src, int R, int C, f16* dst, int ld, int row0, int mode,
                   hipStream_t st) {
   dim3 grid((C + 63) / 64, (R + 63) / 64);
-  hipLaunchKernelGGL(repack_kernel, grid, dim3(256), 0, st, src, R, C, dst, ld, row0, mode);
+  hipLaunchKernelGGL(repack_kernel<f16>, grid, dim3(256), 0, st, src, R, C, dst, ld, row0, mode);
+  return hipGetLastError();
+}
+
+hipError_t repack_f32(const float* src, int R, int C, float* dst, int ld, int row0, int mode,
+                      hipStream_t st) {
+  dim3 grid((C + 63) / 64, (R + 63) / 64);
+  hipLaunchKernelGGL(repack_kernel<float>, grid, dim3(256), 0, st, src, R, C, dst, ld, row0, mode);
   return hipGetLastError();
 }
 

@@ -126,10 +126,36 @@ hipError_t set_int(int* d, int value, hipStream_t st);
 //   mode 2: dst[(row0 + i) * ld + j] = src[i][j]              (copy)
 hipError_t repack(const float* src, int R, int C, f16* dst, int ld, int row0, int mode,
                   hipStream_t st);
+// The same permutation into fp32 (the optimizer's master copy).
+hipError_t repack_f32(const float* src, int R, int C, float* dst, int ld, int row0, int mode,
+                      hipStream_t st);
 // Elements [first, first+n) of hb_synth_normal(seed, tensor_id) as fp32.
 hipError_t synth_f32(uint64_t seed, uint64_t tensor_id, float scale, uint64_t first, size_t n,
                      float* dst, hipStream_t st);
 hipError_t fill_f32(float* d, float v, size_t n, hipStream_t st);
 hipError_t fill_f16_zero(f16* d, size_t n, hipStream_t st);
+
+// ---- optimizer (optimizer.hip) ----
+// AdamW hyperparameters of one launch (cpu/adam.rs:95-132): omb1 = 1 - b1,
+// omb2 = 1 - b2, bc1 = 1/(1 - b1^t), bc2 = 1/(1 - b2^t), all computed in fp32
+// on the host; gscale is used when no device scale pointer is given.
+struct AdamW {
+  float lr, wd, b1, b2, omb1, omb2, eps, bc1, bc2, gscale;
+};
+// One fused step over n (multiple of 4) elements of param/grad/m/v; the new
+// param is also written to dst16 (fp16 weights) or dst32 (fp32 gammas).
+hipError_t adamw(float* p, const float* g, float* m, float* v, f16* dst16, float* dst32, size_t n,
+                 const AdamW& h, const float* d_gscale, hipStream_t st);
+constexpr int SUMSQ_BLOCKS = 1024;
+// partials[SUMSQ_BLOCKS] = fp64 sums of squares of fixed shares of g[0, n).
+hipError_t grad_sumsq(const float* g, size_t n, double* partials, hipStream_t st);
+struct ClipCfg {
+  float gsc;        // 1 / (accum_steps * loss_scale)
+  float grad_clip;  // max norm
+};
+// out[0] = norm, out[1] = train_step's gradient scale, out[2] = clip_grads' factor.
+hipError_t grad_clip_scale(const double* partials, ClipCfg c, float* out, hipStream_t st);
+hipError_t scale_inplace(float* g, size_t n, const float* d_scale, hipStream_t st);
+hipError_t widen_f16(const f16* src, float* dst, size_t n, hipStream_t st);
 
 }  // namespace hb

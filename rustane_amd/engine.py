@@ -321,3 +321,105 @@ class Decoder:
 
     def length(self) -> int:
         return self.kv.length()
+
+
+# ---------------------------------------------------------------------------
+# optimizer (full_model.rs:33-70, 334-342, 487-641, 697-711)
+# ---------------------------------------------------------------------------
+@dataclass
+class TrainConfig:
+    """full_model.rs:33-70 with its defaults (53-70)."""
+    max_lr: float = 3e-4
+    min_lr_frac: float = 0.1
+    warmup_steps: int = 100
+    total_steps: int = 10000
+    beta1: float = 0.9
+    beta2: float = 0.95
+    eps: float = 1e-8
+    weight_decay: float = 0.1
+    matrix_lr_scale: float = 0.05
+    embed_lr_scale: float = 5.0
+    loss_scale: float = 256.0
+    accum_steps: int = 10
+    grad_clip: float = 1.0
+    softcap: float = 0.0
+
+
+def learning_rate(step: int, tc: TrainConfig) -> float:
+    """full_model.rs:334-342."""
+    return hb.learning_rate(tc, step)
+
+
+@dataclass
+class LayerGrads:
+    """layer.rs:29-39 (reference layouts, fp32)."""
+    dwq: np.ndarray
+    dwk: np.ndarray
+    dwv: np.ndarray
+    dwo: np.ndarray
+    dw1: np.ndarray
+    dw3: np.ndarray
+    dw2: np.ndarray
+    dgamma1: np.ndarray
+    dgamma2: np.ndarray
+
+    def as_dict(self) -> dict:
+        return dict(wq=self.dwq, wk=self.dwk, wv=self.dwv, wo=self.dwo, w1=self.dw1, w3=self.dw3,
+                    w2=self.dw2, gamma1=self.dgamma1, gamma2=self.dgamma2)
+
+
+@dataclass
+class ModelGrads:
+    """full_model.rs:20-24."""
+    dembed: np.ndarray
+    layers: List[LayerGrads]
+    dgamma_final: np.ndarray
+
+
+class ModelOptState:
+    """ModelOptState (full_model.rs:26-31) on the device, together with the
+    gradient arena and an fp32 master copy of the weights the kernels' fp16
+    copy is refreshed from (hb_opt). Built from the model's current weights,
+    or from fp32 ModelWeights when given."""
+
+    def __init__(self, kernels: CompiledKernels, tc: TrainConfig,
+                 weights: Optional[ModelWeights] = None):
+        self.kernels, self.tc = kernels, tc
+        self.opt = hb.Optimizer(kernels.model, tc)
+        if weights is not None:
+            for l, lw in enumerate(weights.layers):
+                self.opt.upload_layer(l, lw)
+            self.opt.upload_embed(weights.embed, weights.gamma_final)
+            kernels._uploaded = (id(weights), weights.version)
+
+    def set_grads(self, grads: ModelGrads) -> None:
+        for l, lg in enumerate(grads.layers):
+            self.opt.upload_grads_layer(l, lg.as_dict())
+        self.opt.upload_grads_embed(grads.dembed, grads.dgamma_final)
+
+    def zero_grads(self) -> None:
+        self.opt.zero_grads()
+
+    def close(self) -> None:
+        self.opt.close()
+
+
+def grad_norm(opt: ModelOptState) -> float:
+    """full_model.rs:600-622."""
+    return opt.opt.grad_norm()
+
+
+def clip_grads(opt: ModelOptState, max_norm: float) -> float:
+    """full_model.rs:625-641; returns the norm before clipping."""
+    return opt.opt.clip_grads(max_norm)
+
+
+def update_weights(opt: ModelOptState, t: int, lr: float, grad_scale: float) -> None:
+    """full_model.rs:487-592 (weights, grads and moments live on the device)."""
+    opt.opt.update_weights(t, lr, grad_scale)
+
+
+def optimizer_step(opt: ModelOptState, step: int) -> float:
+    """The optimizer half of train_step (full_model.rs:697-711); returns the raw
+    gradient norm."""
+    return opt.opt.step(step)

@@ -17,6 +17,8 @@ import os
 import threading
 from dataclasses import dataclass, fields
 
+import numpy as np
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libhip_bridge.so")
 
@@ -63,6 +65,25 @@ class hb_model_config(C.Structure):
         ("norm_eps", C.c_float),
         ("residual_alpha", C.c_float),
         ("softcap", C.c_float),
+    ]
+
+
+class hb_train_config(C.Structure):
+    """TrainConfig (full_model.rs:33-70), the optimizer's fields."""
+    _fields_ = [
+        ("max_lr", C.c_float),
+        ("min_lr_frac", C.c_float),
+        ("warmup_steps", C.c_uint32),
+        ("total_steps", C.c_uint32),
+        ("beta1", C.c_float),
+        ("beta2", C.c_float),
+        ("eps", C.c_float),
+        ("weight_decay", C.c_float),
+        ("matrix_lr_scale", C.c_float),
+        ("embed_lr_scale", C.c_float),
+        ("loss_scale", C.c_float),
+        ("accum_steps", C.c_uint32),
+        ("grad_clip", C.c_float),
     ]
 
 
@@ -114,6 +135,22 @@ SIGNATURES = {
     "hb_prefill": [_P, _P, _P, _I, _P, _P],
     "hb_decode_step": [_P, _P, _P, _P, _P],
     "hb_decode_greedy": [_P, _P, _P, _I, _P],
+    "hb_learning_rate": [C.POINTER(hb_train_config), _U32, C.POINTER(C.c_float)],
+    "hb_opt_create": [_P, C.POINTER(hb_train_config), C.POINTER(_P)],
+    "hb_opt_destroy": [_P],
+    "hb_opt_upload_layer": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "hb_opt_upload_embed": [_P, _P, _P],
+    "hb_opt_init_synthetic": [_P, _U64, _F],
+    "hb_opt_upload_grads_layer": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "hb_opt_upload_grads_embed": [_P, _P, _P],
+    "hb_opt_zero_grads": [_P],
+    "hb_opt_grad_arena": [_P, C.POINTER(_P), C.POINTER(C.c_uint64)],
+    "hb_opt_grad_norm": [_P, C.POINTER(C.c_float)],
+    "hb_opt_clip_grads": [_P, _F, C.POINTER(C.c_float)],
+    "hb_opt_update_weights": [_P, _U32, _F, _F],
+    "hb_opt_step": [_P, _U32, C.POINTER(C.c_float)],
+    "hb_opt_download_layer": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "hb_opt_download_embed": [_P, _I, _P, _P],
     "hb_debug_inject_error": [_I],
 }
 _RESTYPE = {"hb_backend_name": C.c_char_p, "hb_last_error": C.c_char_p}
@@ -339,3 +376,121 @@ def synth_tokens(seed: int, stream: int, vocab: int, n: int):
     out = np.empty(n, dtype=np.uint32)
     call("hb_synth_tokens", seed, stream, vocab, n, out.ctypes.data)
     return out
+
+
+def train_config_struct(tc) -> hb_train_config:
+    s = hb_train_config()
+    for name, _ in hb_train_config._fields_:
+        setattr(s, name, getattr(tc, name))
+    return s
+
+
+LAYER_TENSORS = ("wq", "wk", "wv", "wo", "w1", "w3", "w2", "gamma1", "gamma2")
+
+
+class Optimizer:
+    """hb_opt: fp32 master weights, gradients and AdamW moments of a Model on
+    its device (ModelOptState + ModelGrads, full_model.rs:20-31)."""
+
+    WEIGHTS, M, V, GRADS = 0, 1, 2, 3
+
+    def __init__(self, model: Model, tc):
+        self.model = model
+        self.cfg = model.config
+        self.tc = train_config_struct(tc)
+        h = _P()
+        call("hb_opt_create", model.handle, C.byref(self.tc), C.byref(h))
+        self.handle = h
+
+    def _layer_shapes(self):
+        c = self.cfg
+        d, q, kv, h = c.dim, c.q_dim, c.kv_dim, c.hidden
+        return dict(wq=d * q, wk=d * kv, wv=d * kv, wo=q * d, w1=d * h, w3=d * h, w2=d * h,
+                    gamma1=d, gamma2=d)
+
+    @staticmethod
+    def _arrays(obj, names):
+        out = []
+        for n in names:
+            a = np.ascontiguousarray(getattr(obj, n), dtype=np.float32)
+            out.append(a)
+        return out
+
+    def upload_layer(self, layer: int, lw) -> None:
+        arrs = self._arrays(lw, LAYER_TENSORS)
+        call("hb_opt_upload_layer", self.handle, layer, *[a.ctypes.data for a in arrs])
+
+    def upload_embed(self, embed, gamma_final) -> None:
+        e = np.ascontiguousarray(embed, dtype=np.float32)
+        g = np.ascontiguousarray(gamma_final, dtype=np.float32)
+        call("hb_opt_upload_embed", self.handle, e.ctypes.data, g.ctypes.data)
+
+    def init_synthetic(self, seed: int, std: float = 0.02) -> None:
+        call("hb_opt_init_synthetic", self.handle, seed, std)
+
+    def upload_grads_layer(self, layer: int, grads: dict) -> None:
+        arrs = [np.ascontiguousarray(grads[k], dtype=np.float32) for k in LAYER_TENSORS]
+        call("hb_opt_upload_grads_layer", self.handle, layer, *[a.ctypes.data for a in arrs])
+
+    def upload_grads_embed(self, dembed, dgamma_final) -> None:
+        e = np.ascontiguousarray(dembed, dtype=np.float32)
+        g = np.ascontiguousarray(dgamma_final, dtype=np.float32)
+        call("hb_opt_upload_grads_embed", self.handle, e.ctypes.data, g.ctypes.data)
+
+    def zero_grads(self) -> None:
+        call("hb_opt_zero_grads", self.handle)
+
+    def grad_arena(self):
+        p, n = _P(), C.c_uint64()
+        call("hb_opt_grad_arena", self.handle, C.byref(p), C.byref(n))
+        return p.value, n.value
+
+    def grad_norm(self) -> float:
+        out = C.c_float()
+        call("hb_opt_grad_norm", self.handle, C.byref(out))
+        return out.value
+
+    def clip_grads(self, max_norm: float) -> float:
+        out = C.c_float()
+        call("hb_opt_clip_grads", self.handle, max_norm, C.byref(out))
+        return out.value
+
+    def update_weights(self, t: int, lr: float, grad_scale: float) -> None:
+        call("hb_opt_update_weights", self.handle, t, lr, grad_scale)
+
+    def step(self, step: int, want_norm: bool = True):
+        out = C.c_float()
+        call("hb_opt_step", self.handle, step, C.byref(out) if want_norm else None)
+        return out.value if want_norm else None
+
+    def download_layer(self, layer: int, which: int = 0) -> dict:
+        sh = self._layer_shapes()
+        out = {k: np.empty(sh[k], np.float32) for k in LAYER_TENSORS}
+        call("hb_opt_download_layer", self.handle, layer, which,
+             *[out[k].ctypes.data for k in LAYER_TENSORS])
+        return out
+
+    def download_embed(self, which: int = 0):
+        c = self.cfg
+        e = np.empty(c.vocab * c.dim, np.float32)
+        g = np.empty(c.dim, np.float32)
+        call("hb_opt_download_embed", self.handle, which, e.ctypes.data, g.ctypes.data)
+        return e, g
+
+    def close(self) -> None:
+        if self.handle and not _exiting:
+            lib().hb_opt_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def learning_rate(tc, step: int) -> float:
+    out = C.c_float()
+    s = train_config_struct(tc)
+    call("hb_learning_rate", C.byref(s), step, C.byref(out))
+    return out.value

@@ -163,3 +163,20 @@ def test_error_message_is_thread_local():
     [t.join() for t in ts]
     for i in range(4):
         assert f"got {96 + i}" in msgs[i]
+
+
+def test_learning_rate_matches_oracle():
+    """hb_learning_rate (host fp32, full_model.rs:334-342) against the oracle:
+    bit-identical through the warmup; within 2 ulp on the cosine part, where
+    the C library's cosf and numpy's float32 cos may round differently."""
+    import oracle.optimizer as OP
+    from rustane_amd import engine as E
+    tc, otc = E.TrainConfig(), OP.TrainConfig()
+    for s in range(0, tc.warmup_steps):
+        assert np.float32(hb.learning_rate(tc, s)) == OP.learning_rate(s, otc), s
+    for s in range(tc.warmup_steps, tc.total_steps + 1, 37):
+        a = np.float32(hb.learning_rate(tc, s)).view(np.int32)
+        b = OP.learning_rate(s, otc).view(np.int32)
+        assert abs(int(a) - int(b)) <= 2, s
+    with pytest.raises(hb.HipBridgeError):
+        hb.learning_rate(E.TrainConfig(warmup_steps=0), 1)
