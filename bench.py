@@ -70,6 +70,7 @@ def main():
     ap.add_argument("--no-b8", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-optimizer", action="store_true")
+    ap.add_argument("--no-validate", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (timed) and a 1 GiB device copy, for counter runs")
     args = ap.parse_args()
@@ -203,6 +204,10 @@ def main():
             dec.kv.close()
         extra["decode"] = dec_res
 
+    # ---- validation loop (windows of a resident token stream) ----
+    if not args.no_validate:
+        extra["validate"] = bench_validate(k, cfg, stream)
+
     # ---- optimizer step over the whole model ----
     if not args.no_optimizer:
         extra["optimizer"] = bench_optimizer(k, stream, cpu=not args.no_cpu_baseline)
@@ -285,6 +290,31 @@ def time_dominant_kernel(k, cfg, T, launches, stream):
                 "kernel": "gemm_nt_kernel<192,256,2,2,EpiSwiGLU> (FFN up, W1|W3 + SwiGLU)",
                 "flop_per_launch": up_flops, "us_per_launch": round(up_ms * 1e3, 2)}
     return roofline, up_ms
+
+
+def bench_validate(k, cfg, stream, steps=32):
+    """hb_validate (bin/train.rs:123-163 on the device) over a resident stream of
+    2M uniform token ids with a synthetic byte table: windows of seq 512, 8 per
+    forward, and one per forward as the reference runs them."""
+    import torch
+    from rustane_amd import hip_bridge as hb
+    toks = hb.synth_tokens(7, 0, cfg.vocab, 2_000_000).astype("<u2")
+    tb = (hb.synth_tokens(8, 0, 5, cfg.vocab)).astype("<i4")
+    dt = hb.DeviceTokens(k.ctx, tokens=toks)
+    res = {"seq": cfg.seq, "windows": steps}
+    try:
+        for B in (8, 1):
+            hb.validate(k.model, dt, tb, B, B)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            avg, bpb, _, _ = hb.validate(k.model, dt, tb, steps, B)
+            sec = time.perf_counter() - t0
+            res[f"batch{B}"] = {"tok_per_s": round(steps * cfg.seq / sec, 1), "ms": round(sec * 1e3, 2),
+                                "avg_loss": round(avg, 5), "bpb": round(bpb, 5)}
+    finally:
+        dt.close()
+    log(f"[bench] validate: {res}")
+    return res
 
 
 class _DeviceArray:

@@ -55,6 +55,7 @@ typedef struct hb_ctx hb_ctx;
 typedef struct hb_model hb_model;
 typedef struct hb_kv hb_kv;
 typedef struct hb_opt hb_opt;
+typedef struct hb_tokens hb_tokens;
 
 /*
  * Model shape. Field names and meaning follow rustane's ModelConfig
@@ -338,6 +339,58 @@ int hb_opt_download_layer(hb_opt* opt, int layer, int which, float* wq, float* w
                           float* wo, float* w1, float* w3, float* w2, float* gamma1,
                           float* gamma2);
 int hb_opt_download_embed(hb_opt* opt, int which, float* embed, float* gamma_final);
+
+/* ---- RSTK checkpoints (bin/train.rs:165-202) ------------------------------ */
+
+/* Header of the reference's checkpoint file: "RSTK", then little-endian u32
+ * version (1), step, dim, nlayers, vocab, seq (28 bytes), followed by fp32
+ * weights in the order embed, gamma_final, then per layer wq, wk, wv, wo, w1,
+ * w3, w2, gamma1, gamma2 in the reference layouts. */
+typedef struct hb_rstk_header {
+  uint32_t version, step, dim, nlayers, vocab, seq;
+} hb_rstk_header;
+
+/* Read and check a checkpoint's header (host only, no device): HB_E_INVALID
+ * for a missing file, a bad magic or version. */
+int hb_rstk_read_header(const char* path, hb_rstk_header* out);
+/* Load a checkpoint into the model -- as hb_model_upload_layer/_embed, and
+ * into the optimizer's fp32 master copy when opt != NULL. The header's dim,
+ * nlayers and vocab must match the model (HB_E_CONFIG) and the file size must
+ * be exactly what the model's shapes give (HB_E_INVALID); the checkpoint's seq
+ * is informational. out_step (nullable) receives the header's step.
+ * The reference writes these files but has no loader. */
+int hb_model_load_rstk(hb_model* model, hb_opt* opt, const char* path, uint32_t* out_step);
+/* Write a checkpoint with save_checkpoint's byte layout (bin/train.rs:165-202):
+ * from the optimizer's fp32 master weights when opt != NULL, else from the
+ * model's fp16 weights widened to fp32. */
+int hb_model_save_rstk(hb_model* model, hb_opt* opt, uint32_t step, const char* path);
+
+/* ---- data path and validation (data.rs, bin/train.rs:123-163) ------------- */
+
+/* A token stream -- TokenData (data.rs:11-40): flat little-endian uint16 ids,
+ * as the train/val .bin files hold them -- copied to the device once. */
+int hb_tokens_create(hb_ctx* ctx, const uint16_t* h_tokens, uint64_t n, hb_tokens** out);
+/* TokenData::open: map the file and copy it to the device (HB_E_INVALID for a
+ * missing file or an odd byte count). */
+int hb_tokens_open(hb_ctx* ctx, const char* path, hb_tokens** out);
+int hb_tokens_destroy(hb_tokens* t);
+int hb_tokens_length(const hb_tokens* t, uint64_t* out_n);
+/*
+ * validate (bin/train.rs:123-163) on the device: window vs (0 <= vs < steps)
+ * starts at pos = (vs * seq) % (n - seq - 1) with seq = the model's seq;
+ * each window's per-position losses (forward_losses, full_model.rs:717-767)
+ * are summed on the device, and with token_bytes [tb_len] (TokenBytes,
+ * data.rs:43-58; nullable) so are the losses and byte lengths of targets with
+ * a positive byte count (compute_bpb, data.rs:61-83). `batch` windows run per
+ * forward (1 = the reference's one window per call; larger batches give the
+ * same windows through the batched GEMMs, so the sums agree to rounding).
+ * Outputs (each nullable): mean loss per token, val_bpb = nats / (ln 2 *
+ * bytes), and the totals. Synchronous; HB_E_INVALID if the stream holds an id
+ * outside the vocabulary or fewer than seq + 2 tokens.
+ */
+int hb_validate(hb_model* model, const hb_tokens* val, const int32_t* token_bytes, int tb_len,
+                int steps, int batch, float* out_avg_loss, float* out_bpb, double* out_nats,
+                uint64_t* out_bytes);
 
 /* ---- failure injection (host-side test hook) ------------------------------ */
 /* While `code` != 0, every entry point above except hb_last_error,

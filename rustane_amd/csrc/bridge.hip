@@ -13,6 +13,11 @@
 #include <thread>
 #include <vector>
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include "../../include/hip_bridge.h"
 #include "internal.hpp"
 #include "synth.hpp"
@@ -1213,6 +1218,316 @@ extern "C" int hb_opt_download_embed(hb_opt* o, int which, float* embed, float* 
   HIP_TRY(hipMemcpyAsync(embed, a + o->embed_off, (size_t)c.vocab * c.dim * 4, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipMemcpyAsync(gamma_final, a + o->gf_off, c.dim * 4, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// RSTK checkpoints (bin/train.rs:165-202)
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t RSTK_HDR = 28;
+
+uint32_t le32(const unsigned char* p) {
+  return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+}
+
+int rstk_parse(const unsigned char* b, size_t n, hb_rstk_header* h) {
+  if (n < RSTK_HDR || std::memcmp(b, "RSTK", 4) != 0)
+    return fail(HB_E_INVALID, "not an RSTK checkpoint (bad magic or shorter than its header)");
+  h->version = le32(b + 4);
+  h->step = le32(b + 8);
+  h->dim = le32(b + 12);
+  h->nlayers = le32(b + 16);
+  h->vocab = le32(b + 20);
+  h->seq = le32(b + 24);
+  if (h->version != 1) return fail(HB_E_INVALID, "RSTK version %u (only 1 is defined)", h->version);
+  return HB_OK;
+}
+
+// fp32 values after the header for this config: embed, gamma_final, then per
+// layer wq, wk, wv, wo, w1, w3, w2, gamma1, gamma2.
+size_t rstk_floats(const hb_model_config& c) {
+  const size_t d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden;
+  const size_t per_layer = d * q + 2 * d * kv + q * d + 3 * d * h + 2 * d;
+  return (size_t)c.vocab * d + d + (size_t)c.nlayers * per_layer;
+}
+
+struct MappedFile {
+  const unsigned char* p = nullptr;
+  size_t n = 0;
+  ~MappedFile() {
+    if (p) munmap((void*)p, n);
+  }
+};
+
+int map_file(const char* path, MappedFile& mf) {
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) return fail(HB_E_INVALID, "cannot open %s", path);
+  struct stat st {};
+  if (fstat(fd, &st) != 0 || st.st_size <= 0) {
+    close(fd);
+    return fail(HB_E_INVALID, "cannot stat %s (or it is empty)", path);
+  }
+  void* p = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  if (p == MAP_FAILED) return fail(HB_E_INVALID, "cannot map %s", path);
+  mf.p = (const unsigned char*)p;
+  mf.n = (size_t)st.st_size;
+  return HB_OK;
+}
+
+// The model's fp16 weights of one layer, widened and returned in the
+// reference layouts (the inverse of hb_model_upload_layer's packing).
+int model_download_layer(hb_model* m, int layer, std::vector<float> out[9]) {
+  const hb_model_config& c = m->cfg;
+  const LayerW& L = m->layers[layer];
+  const int d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden;
+  hipStream_t st = m->ctx->stream();
+  auto fetch = [&](const f16* src, size_t n, std::vector<float>& dst) -> int {
+    std::vector<f16> tmp(n);
+    HIP_TRY(hipMemcpyAsync(tmp.data(), src, n * 2, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    dst.resize(n);
+    for (size_t i = 0; i < n; ++i) dst[i] = (float)tmp[i];
+    return HB_OK;
+  };
+  std::vector<float> wqkv, wo, w13, w2;
+  TRY(fetch(L.wqkv, (size_t)(q + 2 * kv) * d, wqkv));
+  TRY(fetch(L.wo, (size_t)d * q, wo));
+  TRY(fetch(L.w13, (size_t)2 * h * d, w13));
+  TRY(fetch(L.w2, (size_t)d * h, w2));
+  const size_t sz[9] = {(size_t)d * q, (size_t)d * kv, (size_t)d * kv, (size_t)q * d, (size_t)d * h,
+                        (size_t)d * h, (size_t)d * h, (size_t)d, (size_t)d};
+  for (int i = 0; i < 9; ++i) out[i].resize(sz[i]);
+  unpack_host(wqkv.data(), d, q, d, 0, 0, out[0].data());
+  unpack_host(wqkv.data(), d, kv, d, q, 0, out[1].data());
+  unpack_host(wqkv.data(), d, kv, d, q + kv, 0, out[2].data());
+  unpack_host(wo.data(), q, d, q, 0, 0, out[3].data());
+  unpack_host(w13.data(), d, h, d, 0, 1, out[4].data());
+  unpack_host(w13.data(), d, h, d, 2, 1, out[5].data());
+  unpack_host(w2.data(), d, h, h, 0, 2, out[6].data());
+  HIP_TRY(hipMemcpyAsync(out[7].data(), L.g1, d * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(out[8].data(), L.g2, d * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return HB_OK;
+}
+
+struct FileCloser {
+  FILE* f;
+  ~FileCloser() {
+    if (f) fclose(f);
+  }
+};
+}  // namespace
+
+extern "C" int hb_rstk_read_header(const char* path, hb_rstk_header* out) {
+  HB_INJECT_CHECK();
+  if (!path || !out) return fail(HB_E_INVALID, "null argument");
+  FileCloser fc{fopen(path, "rb")};
+  if (!fc.f) return fail(HB_E_INVALID, "cannot open %s", path);
+  unsigned char b[RSTK_HDR];
+  const size_t n = fread(b, 1, RSTK_HDR, fc.f);
+  return rstk_parse(b, n, out);
+}
+
+extern "C" int hb_model_load_rstk(hb_model* m, hb_opt* opt, const char* path, uint32_t* out_step) {
+  HB_INJECT_CHECK();
+  if (!m || !path) return fail(HB_E_INVALID, "null argument");
+  if (opt && opt->model != m) return fail(HB_E_INVALID, "optimizer belongs to another model");
+  MappedFile mf;
+  TRY(map_file(path, mf));
+  hb_rstk_header h{};
+  TRY(rstk_parse(mf.p, mf.n, &h));
+  const hb_model_config& c = m->cfg;
+  if ((int)h.dim != c.dim || (int)h.nlayers != c.nlayers || (int)h.vocab != c.vocab)
+    return fail(HB_E_CONFIG, "checkpoint is dim %u / %u layers / vocab %u, the model %d / %d / %d",
+                h.dim, h.nlayers, h.vocab, c.dim, c.nlayers, c.vocab);
+  const size_t want = RSTK_HDR + 4 * rstk_floats(c);
+  if (mf.n != want)
+    return fail(HB_E_INVALID, "checkpoint has %zu bytes; this model's shapes give %zu", mf.n, want);
+  const float* f = (const float*)(mf.p + RSTK_HDR);  // little-endian fp32, 4-byte aligned
+  const size_t d = c.dim, q = c.q_dim, kv = c.kv_dim, hd = c.hidden;
+  const float* embed = f;
+  const float* gf = embed + (size_t)c.vocab * d;
+  const float* p = gf + d;
+  if (opt)
+    TRY(hb_opt_upload_embed(opt, embed, gf));
+  else
+    TRY(hb_model_upload_embed(m, embed, gf));
+  for (int l = 0; l < c.nlayers; ++l) {
+    const float* w[9];
+    const size_t sz[9] = {d * q, d * kv, d * kv, q * d, d * hd, d * hd, d * hd, d, d};
+    for (int i = 0; i < 9; ++i) {
+      w[i] = p;
+      p += sz[i];
+    }
+    if (opt)
+      TRY(hb_opt_upload_layer(opt, l, w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7], w[8]));
+    else
+      TRY(hb_model_upload_layer(m, l, w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7], w[8]));
+  }
+  if (out_step) *out_step = h.step;
+  return HB_OK;
+}
+
+extern "C" int hb_model_save_rstk(hb_model* m, hb_opt* opt, uint32_t step, const char* path) {
+  HB_INJECT_CHECK();
+  if (!m || !path) return fail(HB_E_INVALID, "null argument");
+  if (opt && opt->model != m) return fail(HB_E_INVALID, "optimizer belongs to another model");
+  const hb_model_config& c = m->cfg;
+  if (!opt) {
+    if (!m->embed_uploaded) return fail(HB_E_STATE, "embedding not uploaded");
+    for (const LayerW& L : m->layers)
+      if (!L.uploaded) return fail(HB_E_STATE, "layer weights not uploaded");
+  }
+  DeviceGuard g(m->ctx->device);
+  FileCloser fc{fopen(path, "wb")};
+  if (!fc.f) return fail(HB_E_INVALID, "cannot create %s", path);
+  unsigned char hdr[RSTK_HDR];
+  std::memcpy(hdr, "RSTK", 4);
+  const uint32_t vals[6] = {1u, step, (uint32_t)c.dim, (uint32_t)c.nlayers, (uint32_t)c.vocab,
+                            (uint32_t)c.seq};
+  for (int i = 0; i < 6; ++i)
+    for (int b = 0; b < 4; ++b) hdr[4 + 4 * i + b] = (unsigned char)(vals[i] >> (8 * b));
+  auto put = [&](const void* src, size_t bytes) -> int {
+    if (fwrite(src, 1, bytes, fc.f) != bytes) return fail(HB_E_INVALID, "write to %s failed", path);
+    return HB_OK;
+  };
+  TRY(put(hdr, RSTK_HDR));
+  const size_t d = c.dim;
+  std::vector<float> embed((size_t)c.vocab * d), gf(d);
+  if (opt) {
+    TRY(hb_opt_download_embed(opt, 0, embed.data(), gf.data()));
+  } else {
+    std::vector<f16> tmp(embed.size());
+    hipStream_t st = m->ctx->stream();
+    HIP_TRY(hipMemcpyAsync(tmp.data(), m->embed, tmp.size() * 2, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(gf.data(), m->gamma_f, d * 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    for (size_t i = 0; i < tmp.size(); ++i) embed[i] = (float)tmp[i];
+  }
+  TRY(put(embed.data(), embed.size() * 4));
+  TRY(put(gf.data(), d * 4));
+  for (int l = 0; l < c.nlayers; ++l) {
+    std::vector<float> w[9];
+    if (opt) {
+      const size_t q = c.q_dim, kv = c.kv_dim, h = c.hidden;
+      const size_t sz[9] = {d * q, d * kv, d * kv, q * d, d * h, d * h, d * h, d, d};
+      for (int i = 0; i < 9; ++i) w[i].resize(sz[i]);
+      TRY(hb_opt_download_layer(opt, l, 0, w[0].data(), w[1].data(), w[2].data(), w[3].data(),
+                                w[4].data(), w[5].data(), w[6].data(), w[7].data(), w[8].data()));
+    } else {
+      TRY(model_download_layer(m, l, w));
+    }
+    for (int i = 0; i < 9; ++i) TRY(put(w[i].data(), w[i].size() * 4));
+  }
+  if (fflush(fc.f) != 0) return fail(HB_E_INVALID, "write to %s failed", path);
+  return HB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// data path and validation (data.rs, bin/train.rs:123-163)
+// ---------------------------------------------------------------------------
+static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets,
+                               int B, int S, float* d_loss, float* d_logits, float* d_mean);
+
+struct hb_tokens {
+  int device = 0;
+  uint16_t* d = nullptr;
+  uint64_t n = 0;
+};
+
+extern "C" int hb_tokens_create(hb_ctx* ctx, const uint16_t* h, uint64_t n, hb_tokens** out) {
+  HB_INJECT_CHECK();
+  if (!ctx || !out || (!h && n)) return fail(HB_E_INVALID, "null argument");
+  *out = nullptr;
+  DeviceGuard g(ctx->device);
+  hb_tokens* t = new hb_tokens();
+  t->device = ctx->device;
+  t->n = n;
+  if (n) {
+    hipError_t e = hipMalloc(&t->d, n * 2);
+    if (e == hipSuccess) e = hipMemcpy(t->d, h, n * 2, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      if (t->d) (void)hipFree(t->d);
+      delete t;
+      return fail(e == hipErrorOutOfMemory ? HB_E_OOM : HB_E_DEVICE, "token stream of %llu ids: %s",
+                  (unsigned long long)n, hipGetErrorString(e));
+    }
+  }
+  *out = t;
+  return HB_OK;
+}
+
+extern "C" int hb_tokens_open(hb_ctx* ctx, const char* path, hb_tokens** out) {
+  HB_INJECT_CHECK();
+  if (!ctx || !path || !out) return fail(HB_E_INVALID, "null argument");
+  MappedFile mf;
+  TRY(map_file(path, mf));
+  if (mf.n % 2) return fail(HB_E_INVALID, "%s has an odd byte count (%zu)", path, mf.n);
+  return hb_tokens_create(ctx, (const uint16_t*)mf.p, mf.n / 2, out);
+}
+
+extern "C" int hb_tokens_destroy(hb_tokens* t) {
+  if (!t) return HB_OK;
+  DeviceGuard g(t->device);
+  if (t->d) (void)hipFree(t->d);
+  delete t;
+  return HB_OK;
+}
+
+extern "C" int hb_tokens_length(const hb_tokens* t, uint64_t* out) {
+  HB_INJECT_CHECK();
+  if (!t || !out) return fail(HB_E_INVALID, "null argument");
+  *out = t->n;
+  return HB_OK;
+}
+
+extern "C" int hb_validate(hb_model* m, const hb_tokens* val, const int32_t* token_bytes, int tb_len,
+                           int steps, int batch, float* out_avg_loss, float* out_bpb,
+                           double* out_nats, uint64_t* out_bytes) {
+  HB_INJECT_CHECK();
+  if (!m || !val) return fail(HB_E_INVALID, "null argument");
+  if (steps < 1 || batch < 1) return fail(HB_E_INVALID, "steps and batch must be positive");
+  if (token_bytes && tb_len < 1) return fail(HB_E_INVALID, "token_bytes needs tb_len >= 1");
+  if (val->device != m->device) return fail(HB_E_INVALID, "token stream is on another device");
+  const hb_model_config& c = m->cfg;
+  const int S = c.seq;
+  if (val->n < (uint64_t)S + 2)
+    return fail(HB_E_INVALID, "%llu tokens: need at least seq + 2 = %d", (unsigned long long)val->n, S + 2);
+  if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
+  DeviceGuard g(m->ctx->device);
+  const int B = std::min(batch, steps);
+  TRY(ensure_workspace(m, (long)B * S, (long)B * S_pad_of(S)));
+  Workspace& w = m->ws;
+  hipStream_t st = m->ctx->stream();
+  // totals (3 doubles) and the byte table in one scratch allocation
+  const size_t tb_bytes = token_bytes ? (size_t)tb_len * 4 : 0;
+  char* scratch = nullptr;
+  HIP_TRY(hipMalloc(&scratch, 32 + tb_bytes));
+  struct Free {
+    char* p;
+    ~Free() { (void)hipFree(p); }
+  } fr{scratch};
+  double* acc = (double*)scratch;
+  int* tb = token_bytes ? (int*)(scratch + 32) : nullptr;
+  HIP_TRY(hipMemsetAsync(acc, 0, 32, st));
+  if (tb) HIP_TRY(hipMemcpyAsync(tb, token_bytes, tb_bytes, hipMemcpyHostToDevice, st));
+  for (int vs = 0; vs < steps; vs += B) {
+    const int nb = std::min(B, steps - vs);
+    HIP_TRY(window_gather(val->d, val->n, (uint32_t)vs, nb, S, w.tok, w.tgt, st));
+    TRY(forward_device_impl(m, w.tok, w.tgt, nb, S, w.loss, nullptr, nullptr));
+    HIP_TRY(bpb_accum(w.loss, w.tgt, nb * S, tb, tb_len, acc, st));
+  }
+  double host[3];
+  HIP_TRY(hipMemcpyAsync(host, acc, sizeof host, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  TRY(check_err_word(m->ctx));
+  const double tokens = (double)steps * S;
+  if (out_avg_loss) *out_avg_loss = (float)(host[0] / tokens);
+  if (out_bpb) *out_bpb = host[2] > 0 ? (float)(host[1] / (0.69314718055994530942 * host[2])) : 0.0f;
+  if (out_nats) *out_nats = host[1];
+  if (out_bytes) *out_bytes = (uint64_t)host[2];
   return HB_OK;
 }
 

@@ -304,4 +304,70 @@ hipError_t fill_f16_zero(f16* d, size_t n, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ---- validation windows (bin/train.rs:123-163, data.rs) --------------------------
+// Window w = vs0 + b starts at pos = (w * S) % max_pos of the uint16 token
+// stream (train.rs:135-137): inputs tokens[pos, pos+S), targets shifted by
+// one. pos + S < max_pos + S = n - 1, so every read is inside the stream.
+__global__ __launch_bounds__(256) void window_gather_kernel(const uint16_t* __restrict__ toks,
+                                                            uint32_t vs0, int S, uint64_t max_pos,
+                                                            uint32_t* __restrict__ tok,
+                                                            uint32_t* __restrict__ tgt) {
+  const int b = blockIdx.x;
+  const uint64_t pos = ((uint64_t)(vs0 + (uint32_t)b) * (uint64_t)S) % max_pos;
+  for (int s = threadIdx.x; s < S; s += 256) {
+    tok[(size_t)b * S + s] = toks[pos + s];
+    tgt[(size_t)b * S + s] = toks[pos + 1 + s];
+  }
+}
+
+hipError_t window_gather(const uint16_t* toks, uint64_t n, uint32_t vs0, int B, int S,
+                         uint32_t* tok, uint32_t* tgt, hipStream_t st) {
+  if (B < 1 || S < 1 || n < (uint64_t)S + 2) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(window_gather_kernel, dim3(B), dim3(256), 0, st, toks, vs0, S,
+                     n - (uint64_t)S - 1, tok, tgt);
+  return hipGetLastError();
+}
+
+// acc[0] += sum of loss[0, T); with a byte-length table (data.rs:61-83):
+// acc[1] += sum of loss[i] over targets with tb[target] > 0 and acc[2] += the
+// sum of those byte lengths. One workgroup, fixed summation order (fp64), so
+// the totals do not depend on scheduling.
+__global__ __launch_bounds__(256) void bpb_accum_kernel(const float* __restrict__ loss,
+                                                        const uint32_t* __restrict__ tgt, int T,
+                                                        const int* __restrict__ tb, int tb_len,
+                                                        double* __restrict__ acc) {
+  __shared__ double red[3][256];
+  double l = 0.0, nats = 0.0, bytes = 0.0;
+  for (int i = threadIdx.x; i < T; i += 256) {
+    const float x = loss[i];
+    l += x;
+    if (tb) {
+      const uint32_t t = tgt[i];
+      const int bl = t < (uint32_t)tb_len ? tb[t] : 0;
+      if (bl > 0) {
+        nats += x;
+        bytes += bl;
+      }
+    }
+  }
+  red[0][threadIdx.x] = l;
+  red[1][threadIdx.x] = nats;
+  red[2][threadIdx.x] = bytes;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w)
+      for (int k = 0; k < 3; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0)
+    for (int k = 0; k < 3; ++k) acc[k] += red[k][0];
+}
+
+hipError_t bpb_accum(const float* loss, const uint32_t* tgt, int T, const int* tb, int tb_len,
+                     double* acc, hipStream_t st) {
+  if (T < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(bpb_accum_kernel, dim3(1), dim3(256), 0, st, loss, tgt, T, tb, tb_len, acc);
+  return hipGetLastError();
+}
+
 }  // namespace hb

@@ -135,6 +135,15 @@ hipError_t synth_f32(uint64_t seed, uint64_t tensor_id, float scale, uint64_t fi
 hipError_t fill_f32(float* d, float v, size_t n, hipStream_t st);
 hipError_t fill_f16_zero(f16* d, size_t n, hipStream_t st);
 
+// ---- validation windows (elementwise.hip) ----
+// tok/tgt [B][S] of windows vs0 .. vs0+B-1 of a uint16 stream of n tokens
+// (window w starts at (w*S) % (n - S - 1)).
+hipError_t window_gather(const uint16_t* toks, uint64_t n, uint32_t vs0, int B, int S,
+                         uint32_t* tok, uint32_t* tgt, hipStream_t st);
+// acc[3] (fp64) += {sum loss, sum loss over byte-bearing targets, sum bytes}.
+hipError_t bpb_accum(const float* loss, const uint32_t* tgt, int T, const int* tb, int tb_len,
+                     double* acc, hipStream_t st);
+
 // ---- optimizer (optimizer.hip) ----
 // AdamW hyperparameters of one launch (cpu/adam.rs:95-132): omb1 = 1 - b1,
 // omb2 = 1 - b2, bc1 = 1/(1 - b1^t), bc2 = 1/(1 - b2^t), all computed in fp32

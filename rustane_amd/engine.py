@@ -423,3 +423,132 @@ def optimizer_step(opt: ModelOptState, step: int) -> float:
     """The optimizer half of train_step (full_model.rs:697-711); returns the raw
     gradient norm."""
     return opt.opt.step(step)
+
+
+# ---------------------------------------------------------------------------
+# checkpoints (bin/train.rs:165-202)
+# ---------------------------------------------------------------------------
+def save_checkpoint(cfg: ModelConfig, kernels: CompiledKernels, opt: Optional[ModelOptState],
+                    step: int, directory) -> str:
+    """bin/train.rs:165-202: writes <dir>/ckpt_<step:06>.bin (RSTK v1) from the
+    optimizer's fp32 master weights, or from the model's fp16 weights when no
+    optimizer is given; returns the path."""
+    import os
+    os.makedirs(directory, exist_ok=True)
+    path = os.path.join(directory, f"ckpt_{step:06d}.bin")
+    hb.rstk_save(kernels.model, path, step, opt.opt if opt is not None else None)
+    return path
+
+
+def load_checkpoint(path, kernels: CompiledKernels, opt: Optional[ModelOptState] = None) -> int:
+    """Load an RSTK checkpoint into the model (and the optimizer's master copy);
+    returns its step. The reference has no loader (train.rs only writes)."""
+    step = hb.rstk_load(kernels.model, path, opt.opt if opt is not None else None)
+    kernels._uploaded = ("rstk", str(path), step)
+    return step
+
+
+# ---------------------------------------------------------------------------
+# data path (data.rs) and validation (bin/train.rs:123-163)
+# ---------------------------------------------------------------------------
+class TokenData:
+    """data.rs:11-40: a flat little-endian uint16 token file, memory-mapped."""
+
+    def __init__(self, tokens):
+        self._t = tokens
+        self._dev = {}
+
+    @staticmethod
+    def open(path) -> "TokenData":
+        return TokenData(np.memmap(path, dtype="<u2", mode="r"))
+
+    def len(self) -> int:
+        return int(self._t.shape[0])
+
+    __len__ = len
+
+    def token(self, pos: int) -> int:
+        return int(self._t[pos])
+
+    def tokens(self, start: int, length: int) -> np.ndarray:
+        return np.asarray(self._t[start:start + length], dtype=np.uint32)
+
+    def device(self, kernels: CompiledKernels) -> "hb.DeviceTokens":
+        """The stream copied once to the kernels' device (cached)."""
+        key = id(kernels.ctx)
+        if key not in self._dev:
+            self._dev[key] = hb.DeviceTokens(kernels.ctx, tokens=np.asarray(self._t))
+        return self._dev[key]
+
+
+class TokenBytes:
+    """data.rs:43-58: byte length per token id (int32 little-endian file)."""
+
+    def __init__(self, bytes_per_token):
+        self.bytes = np.asarray(bytes_per_token, dtype=np.int32)
+
+    @staticmethod
+    def load(path) -> "TokenBytes":
+        return TokenBytes(np.fromfile(path, dtype="<i4"))
+
+    def byte_len(self, token_id: int) -> int:
+        return int(self.bytes[token_id])
+
+
+def compute_bpb(losses, targets, token_bytes: TokenBytes):
+    """data.rs:61-83 in its fp32 arithmetic: (val_bpb, total_nats, total_bytes)."""
+    total_nats = np.float32(0.0)
+    total_bytes = 0
+    for loss, tok in zip(np.asarray(losses, np.float32), np.asarray(targets)):
+        bl = token_bytes.byte_len(int(tok))
+        if bl > 0:
+            total_nats = np.float32(total_nats + loss)
+            total_bytes += bl
+    bpb = (np.float32(total_nats / np.float32(np.float32(math.log(2.0)) * np.float32(total_bytes)))
+           if total_bytes > 0 else np.float32(0.0))
+    return float(bpb), float(total_nats), total_bytes
+
+
+def random_position(step: int, micro: int, max_pos: int) -> int:
+    """data.rs:86-90 (wrapping u64 arithmetic)."""
+    mask = (1 << 64) - 1
+    seed = ((step * 7919) & mask) + ((micro * 104729) & mask)
+    return (seed & mask) % max_pos
+
+
+def validate(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights],
+             val_data: TokenData, token_bytes: Optional[TokenBytes], steps: int,
+             softcap: float = 0.0, batch: int = 1):
+    """bin/train.rs:123-163 -> (avg_loss, val_bpb), run on the device: windows
+    gathered from the resident token stream, losses and byte counts summed
+    there (hb_validate); `batch` windows per forward."""
+    kernels.ensure_weights(weights)
+    kernels.set_softcap(softcap)
+    tb = token_bytes.bytes if token_bytes is not None else None
+    avg, bpb, _, _ = hb.validate(kernels.model, val_data.device(kernels), tb, steps, batch)
+    return avg, bpb
+
+
+def validate_host(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights],
+                  val_data: TokenData, token_bytes: Optional[TokenBytes], steps: int,
+                  softcap: float = 0.0):
+    """The reference's loop as written (train.rs:123-163): one forward_losses call
+    per window with host token slices, fp32 sums on the host, compute_bpb."""
+    seq = cfg.seq
+    total_loss = np.float32(0.0)
+    all_losses, all_targets = [], []
+    max_pos = val_data.len() - seq - 1
+    for vs in range(steps):
+        pos = (vs * seq) % max_pos
+        inp = val_data.tokens(pos, seq)
+        tgt = val_data.tokens(pos + 1, seq)
+        losses = forward_losses(cfg, kernels, weights, inp, tgt, softcap)
+        total_loss = np.float32(total_loss + np.float32(losses.sum(dtype=np.float32)))
+        if token_bytes is not None:
+            all_losses.append(losses)
+            all_targets.append(tgt)
+    avg = float(np.float32(total_loss / np.float32(steps * seq)))
+    bpb = 0.0
+    if token_bytes is not None:
+        bpb = compute_bpb(np.concatenate(all_losses), np.concatenate(all_targets), token_bytes)[0]
+    return avg, bpb

@@ -87,6 +87,11 @@ class hb_train_config(C.Structure):
     ]
 
 
+class hb_rstk_header(C.Structure):
+    """RSTK checkpoint header (bin/train.rs:175-183) after the magic."""
+    _fields_ = [(n, C.c_uint32) for n in ("version", "step", "dim", "nlayers", "vocab", "seq")]
+
+
 _P = C.c_void_p
 _I = C.c_int
 _F = C.c_float
@@ -151,6 +156,15 @@ SIGNATURES = {
     "hb_opt_step": [_P, _U32, C.POINTER(C.c_float)],
     "hb_opt_download_layer": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "hb_opt_download_embed": [_P, _I, _P, _P],
+    "hb_rstk_read_header": [C.c_char_p, C.POINTER(hb_rstk_header)],
+    "hb_model_load_rstk": [_P, _P, C.c_char_p, C.POINTER(C.c_uint32)],
+    "hb_model_save_rstk": [_P, _P, _U32, C.c_char_p],
+    "hb_tokens_create": [_P, _P, _U64, C.POINTER(_P)],
+    "hb_tokens_open": [_P, C.c_char_p, C.POINTER(_P)],
+    "hb_tokens_destroy": [_P],
+    "hb_tokens_length": [_P, C.POINTER(C.c_uint64)],
+    "hb_validate": [_P, _P, _P, _I, _I, _I, C.POINTER(C.c_float), C.POINTER(C.c_float),
+                    C.POINTER(C.c_double), C.POINTER(C.c_uint64)],
     "hb_debug_inject_error": [_I],
 }
 _RESTYPE = {"hb_backend_name": C.c_char_p, "hb_last_error": C.c_char_p}
@@ -494,3 +508,59 @@ def learning_rate(tc, step: int) -> float:
     s = train_config_struct(tc)
     call("hb_learning_rate", C.byref(s), step, C.byref(out))
     return out.value
+
+
+def rstk_read_header(path) -> dict:
+    h = hb_rstk_header()
+    call("hb_rstk_read_header", os.fsencode(path), C.byref(h))
+    return {n: getattr(h, n) for n, _ in hb_rstk_header._fields_}
+
+
+def rstk_load(model: Model, path, opt: "Optimizer | None" = None) -> int:
+    step = C.c_uint32()
+    call("hb_model_load_rstk", model.handle, opt.handle if opt else None, os.fsencode(path),
+         C.byref(step))
+    return step.value
+
+
+def rstk_save(model: Model, path, step: int, opt: "Optimizer | None" = None) -> None:
+    call("hb_model_save_rstk", model.handle, opt.handle if opt else None, step, os.fsencode(path))
+
+
+class DeviceTokens:
+    """hb_tokens: a uint16 token stream resident on the device."""
+
+    def __init__(self, ctx: Context, tokens=None, path=None):
+        h = _P()
+        if path is not None:
+            call("hb_tokens_open", ctx.handle, os.fsencode(path), C.byref(h))
+        else:
+            a = np.ascontiguousarray(tokens, dtype="<u2")
+            call("hb_tokens_create", ctx.handle, a.ctypes.data if a.size else None, a.size, C.byref(h))
+        self.handle = h
+
+    def __len__(self) -> int:
+        n = C.c_uint64()
+        call("hb_tokens_length", self.handle, C.byref(n))
+        return n.value
+
+    def close(self) -> None:
+        if self.handle and not _exiting:
+            lib().hb_tokens_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def validate(model: Model, val: DeviceTokens, token_bytes, steps: int, batch: int = 1):
+    """hb_validate -> (avg_loss, bpb, total_nats, total_bytes)."""
+    tb = None if token_bytes is None else np.ascontiguousarray(token_bytes, dtype="<i4")
+    avg, bpb, nats, nbytes = C.c_float(), C.c_float(), C.c_double(), C.c_uint64()
+    call("hb_validate", model.handle, val.handle, tb.ctypes.data if tb is not None else None,
+         tb.size if tb is not None else 0, steps, batch, C.byref(avg), C.byref(bpb), C.byref(nats),
+         C.byref(nbytes))
+    return avg.value, bpb.value, nats.value, nbytes.value
