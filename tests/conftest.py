@@ -7,6 +7,14 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# One HIP runtime per process: torch brings its own libamdhip64, and a process
+# that loads libhip_bridge.so (system ROCm) before importing torch can crash in
+# torch's import. Import torch first, before any test can load the library.
+try:
+    import torch  # noqa: F401
+except ImportError:  # pragma: no cover - torch is optional for the CPU tests
+    pass
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (run with -m gpu)")

@@ -28,7 +28,11 @@ def _kernel_metadata():
     notes = ""
     with tempfile.TemporaryDirectory() as d:
         fat = os.path.join(d, "fat.bin")
-        subprocess.run([objcopy, "--dump-section", f".hip_fatbin={fat}", LIB], check=True,
+        # objcopy rewrites its input file when no output file is named, which
+        # would change the library under any process that has it mapped: write
+        # the (unused) copy into the temporary directory instead.
+        subprocess.run([objcopy, "--dump-section", f".hip_fatbin={fat}", LIB,
+                        os.path.join(d, "lib_copy.so")], check=True,
                        capture_output=True)
         # one offload bundle per translation unit, concatenated; the bundler
         # reads only the first bundle of a file, so split them
