@@ -43,6 +43,15 @@ def fwd_flops(cfg, B, S):
     return 2 * B * S * (L * (d * q + 2 * d * kv + q * d + 3 * d * h) + d * V) + B * L * 2 * q * S * (S + 1)
 
 
+def train_flops(cfg, B, S):
+    """Algorithmic flops of one training forward + backward: every weight
+    product three times (forward, dX, dW: 6*T*params) and causal attention
+    3.5 times its forward (scores recomputed, dP, dQ, dK, dV)."""
+    d, q, kv, h, L, V = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden, cfg.nlayers, cfg.vocab
+    mats = L * (d * q + 2 * d * kv + q * d + 3 * d * h) + d * V
+    return 6 * B * S * mats + 3.5 * B * L * 2 * q * S * (S + 1)
+
+
 def decode_bytes(cfg, B, p):
     """fp16 bytes one decode step at position p must move: all weights (tied E
     read once for the logits) + K/V read for p+1 positions + K/V write."""
@@ -71,6 +80,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-optimizer", action="store_true")
     ap.add_argument("--no-validate", action="store_true")
+    ap.add_argument("--no-train", action="store_true")
+    ap.add_argument("--train-only", action="store_true",
+                    help="only the training forward + backward section (for profiling)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (timed) and a 1 GiB device copy, for counter runs")
     args = ap.parse_args()
@@ -109,6 +121,10 @@ def main():
     def step():
         hb.call("hb_forward_device", k.model.handle, d_tok.data_ptr(), d_tgt.data_ptr(), B, S,
                 d_loss.data_ptr(), None, d_mean.data_ptr())
+
+    if args.train_only:
+        print(json.dumps({"train": bench_train(k, cfg, stream, B, S, steps=args.steps)}), flush=True)
+        return
 
     if args.kernel_only:
         # Reference transfer of known size (read 1 GiB + write 1 GiB) for scaling
@@ -211,6 +227,10 @@ def main():
     # ---- optimizer step over the whole model ----
     if not args.no_optimizer:
         extra["optimizer"] = bench_optimizer(k, stream, cpu=not args.no_cpu_baseline)
+
+    # ---- training forward + backward and train_step ----
+    if not args.no_train:
+        extra["train"] = bench_train(k, cfg, stream, B, S)
 
     # ---- CPU baseline (oracle, bounded sample) ----
     if not args.no_cpu_baseline:
@@ -376,6 +396,55 @@ def bench_optimizer(k, stream, cpu=True, steps=3):
     if cpu:
         res["cpu_baseline"] = cpu_baseline_adam(n)
     log(f"[bench] optimizer: {res}")
+    return res
+
+
+def bench_train(k, cfg, stream, B, S, steps=4):
+    """Training on the 7B-shape model: hb_forward_backward_device (forward
+    keeping activations + backward accumulating every gradient) alone, and the
+    whole train_step (zero grads, forward + backward, hb_opt_step)."""
+    import torch
+    from rustane_amd import hip_bridge as hb
+    from rustane_amd.engine import TrainConfig
+    opt = hb.Optimizer(k.model, TrainConfig())
+    try:
+        tok = hb.synth_tokens(42, 300, cfg.vocab, B * (S + 1)).reshape(B, S + 1)
+        d_tok = torch.from_numpy(tok[:, :-1].astype(np.int32).copy()).cuda()
+        d_tgt = torch.from_numpy(tok[:, 1:].astype(np.int32).copy()).cuda()
+        d_mean = torch.empty(1, device="cuda")
+        fb = lambda: opt.forward_backward_device(d_tok.data_ptr(), d_tgt.data_ptr(), B, S, 256.0,
+                                                 d_mean=d_mean.data_ptr())
+        opt.zero_grads()
+        fb()
+        torch.cuda.synchronize()
+        loss0 = float(d_mean.cpu()[0])
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fb()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        fb_ms = e0.elapsed_time(e1) / steps
+        norm = opt.grad_norm()
+        t0 = time.perf_counter()
+        for s in range(steps):
+            opt.zero_grads()
+            fb()
+            opt.step(s, want_norm=False)
+        torch.cuda.synchronize()
+        step_ms = (time.perf_counter() - t0) * 1e3 / steps
+        loss1 = float(d_mean.cpu()[0])
+    finally:
+        opt.close()
+    fl = train_flops(cfg, B, S)
+    res = {"batch": B, "seq": S, "ms_per_fwd_bwd": round(fb_ms, 3),
+           "tok_per_s_fwd_bwd": round(B * S / fb_ms * 1e3, 1),
+           "tflop_per_s": round(fl / fb_ms / 1e9, 1), "mfma_frac": round(fl / (fb_ms / 1e3) / MFMA_PEAK_F16, 4),
+           "tflop_per_fwd_bwd": round(fl / 1e12, 3),
+           "ms_per_train_step": round(step_ms, 3), "tok_per_s_train_step": round(B * S / step_ms * 1e3, 1),
+           "loss_first": round(loss0, 5), "loss_after_steps": round(loss1, 5),
+           "grad_norm_x_loss_scale": round(norm, 3)}
+    log(f"[bench] train: {res}")
     return res
 
 

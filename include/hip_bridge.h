@@ -340,6 +340,29 @@ int hb_opt_download_layer(hb_opt* opt, int layer, int which, float* wq, float* w
                           float* gamma2);
 int hb_opt_download_embed(hb_opt* opt, int which, float* embed, float* gamma_final);
 
+/* ---- training forward + backward ------------------------------------------ */
+
+/* forward_ws + backward_ws (full_model.rs:187-247 and 250-331, the per-layer
+ * backward of layer.rs:1606-1858) on B sequences of S tokens: the forward
+ * keeps every layer's activations, the backward ADDS the gradients of
+ * loss_scale * (mean cross-entropy of each sequence) to opt's fp32 gradient
+ * arena (the reference accumulates into ModelGrads the same way; train_step
+ * divides loss_scale and the accumulation count back out, hb_opt_step).
+ * Softcap comes from the model config. Per-position losses (nullable, [B*S])
+ * and their mean (nullable) are returned. Host ids, synchronous; opt must
+ * belong to m. The first call allocates fp16 transposed weight copies (the
+ * size of the weights) and the activations for (B, S). */
+int hb_forward_backward(hb_model* m, hb_opt* opt, const uint32_t* tokens,
+                        const uint32_t* targets, int B, int S, float loss_scale,
+                        float* per_pos_loss, float* mean_loss);
+/* The same with ids in device memory; asynchronous on the context stream,
+ * losses written to device pointers (nullable). Ids >= vocab are reported
+ * through the context's error word by the forward and skipped by the
+ * embedding backward. */
+int hb_forward_backward_device(hb_model* m, hb_opt* opt, const uint32_t* d_tokens,
+                               const uint32_t* d_targets, int B, int S, float loss_scale,
+                               float* d_loss, float* d_mean);
+
 /* ---- RSTK checkpoints (bin/train.rs:165-202) ------------------------------ */
 
 /* Header of the reference's checkpoint file: "RSTK", then little-endian u32

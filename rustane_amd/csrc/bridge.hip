@@ -97,6 +97,11 @@ struct Workspace {
 
 }  // namespace
 
+namespace hb {
+struct TrainState;
+void train_free(TrainState* t);
+}  // namespace hb
+
 struct hb_model {
   hb_ctx* ctx = nullptr;
   int device = 0;
@@ -122,6 +127,11 @@ struct hb_model {
   // split-K partial sums of the prefill residual GEMMs (gemm_splits)
   float* splitk = nullptr;
   size_t splitk_floats = 0;
+  // Training state (transposed weights, kept activations, backward scratch),
+  // allocated by the first hb_forward_backward; wt_stale marks the transposed
+  // weights out of date after any weight write.
+  TrainState* train = nullptr;
+  bool wt_stale = true;
 };
 
 struct hb_kv {
@@ -279,9 +289,9 @@ int S_pad_of(int S) { return (S + 31) & ~31; }
 
 // Scratch for a residual GEMM of this shape: grown on demand (outside any
 // capture: prefill is never captured), empty when the shape does not split.
-int residual_scratch(hb_model* m, int N, int T, int K, GemmScratch& out) {
-  out = GemmScratch{m->splitk, m->splitk_floats};
-  const int S = gemm_splits(N, T, K);
+int residual_scratch(hb_model* m, int N, int T, int K, GemmScratch& out, int wgs = 256) {
+  out = GemmScratch{m->splitk, m->splitk_floats, wgs};
+  const int S = gemm_splits(N, T, K, wgs);
   if (S <= 1) return HB_OK;
   const size_t need = (size_t)S * T * N;
   if (need > m->splitk_floats) {
@@ -292,7 +302,7 @@ int residual_scratch(hb_model* m, int N, int T, int K, GemmScratch& out) {
     HIP_TRY(hipMalloc(&m->splitk, need * 4));
     m->splitk_floats = need;
   }
-  out = GemmScratch{m->splitk, m->splitk_floats};
+  out = GemmScratch{m->splitk, m->splitk_floats, wgs};
   return HB_OK;
 }
 
@@ -331,6 +341,7 @@ int ensure_decode_weights(hb_model* m) {
     }
     m->t_embed = (f16*)(base + off);
     m->dec_stale = true;
+    m->wt_stale = true;
     m->graph_epoch++;
   }
   if (m->dec_stale) {
@@ -614,6 +625,7 @@ extern "C" int hb_model_destroy(hb_model* m) {
   if (m->rope) (void)hipFree(m->rope);
   if (m->staging) (void)hipFree(m->staging);
   if (m->ws.base) (void)hipFree(m->ws.base);
+  train_free(m->train);
   delete m;
   return HB_OK;
 }
@@ -685,6 +697,7 @@ extern "C" int hb_model_upload_layer(hb_model* m, int layer, const float* wq, co
   TRY(upload_f32(m, g2, d, L.g2));
   L.uploaded = true;
   m->dec_stale = true;
+  m->wt_stale = true;
   return HB_OK;
 }
 
@@ -702,6 +715,7 @@ extern "C" int hb_model_upload_embed(hb_model* m, const float* embed, const floa
   TRY(upload_f32(m, gamma_final, c.dim, m->gamma_f));
   m->embed_uploaded = true;
   m->dec_stale = true;
+  m->wt_stale = true;
   return HB_OK;
 }
 
@@ -747,6 +761,7 @@ extern "C" int hb_model_init_synthetic(hb_model* m, uint64_t seed, float std) {
   HIP_TRY(hipStreamSynchronize(st));
   m->embed_uploaded = true;
   m->dec_stale = true;
+  m->wt_stale = true;
   return HB_OK;
 }
 
@@ -823,6 +838,9 @@ struct hb_opt {
   size_t embed_off = 0, gf_off = 0;
   double* partials = nullptr;
   float* scal = nullptr;  // [0] norm, [1] train_step scale, [2] clip_grads factor
+  // The gradient arena holds zeros (creation, hb_opt_zero_grads) and nothing
+  // has written it since: the next training backward stores instead of adding.
+  bool grads_zero = true;
 };
 
 extern "C" int hb_learning_rate(const hb_train_config* tc, uint32_t step, float* out) {
@@ -969,6 +987,7 @@ int opt_put_layer(hb_opt* o, float* a, bool model, int layer, const float* const
     HIP_TRY(hipMemcpyAsync(L.g2, w[8], d * 4, hipMemcpyHostToDevice, st));
     L.uploaded = true;
     m->dec_stale = true;
+    m->wt_stale = true;
   }
   HIP_TRY(hipStreamSynchronize(st));
   return HB_OK;
@@ -989,6 +1008,7 @@ int opt_put_embed(hb_opt* o, float* a, bool model, const float* embed, const flo
     HIP_TRY(hipMemcpyAsync(m->gamma_f, gf, c.dim * 4, hipMemcpyHostToDevice, st));
     m->embed_uploaded = true;
     m->dec_stale = true;
+    m->wt_stale = true;
   }
   HIP_TRY(hipStreamSynchronize(st));
   return HB_OK;
@@ -1020,6 +1040,7 @@ int opt_update(hb_opt* o, uint32_t t, float lr, float grad_scale, const float* d
                   hs, d_gscale, st));
   }
   o->model->dec_stale = true;
+  o->model->wt_stale = true;
   return HB_OK;
 }
 
@@ -1116,6 +1137,7 @@ extern "C" int hb_opt_upload_grads_layer(hb_opt* o, int layer, const float* dwq,
   for (const float* x : w)
     if (!x) return fail(HB_E_INVALID, "null gradient pointer");
   DeviceGuard g(o->device);
+  o->grads_zero = false;
   return opt_put_layer(o, o->g, false, layer, w);
 }
 
@@ -1123,6 +1145,7 @@ extern "C" int hb_opt_upload_grads_embed(hb_opt* o, const float* dembed, const f
   HB_OPT_CHECK(o);
   if (!dembed || !dgamma_final) return fail(HB_E_INVALID, "null argument");
   DeviceGuard g(o->device);
+  o->grads_zero = false;
   return opt_put_embed(o, o->g, false, dembed, dgamma_final);
 }
 
@@ -1130,6 +1153,7 @@ extern "C" int hb_opt_zero_grads(hb_opt* o) {
   HB_OPT_CHECK(o);
   DeviceGuard g(o->device);
   HIP_TRY(fill_f32(o->g, 0.0f, o->n, o->model->ctx->stream()));
+  o->grads_zero = true;
   return HB_OK;
 }
 
@@ -1138,6 +1162,7 @@ extern "C" int hb_opt_grad_arena(hb_opt* o, float** d_grads, uint64_t* n_floats)
   if (!d_grads || !n_floats) return fail(HB_E_INVALID, "null argument");
   *d_grads = o->g;
   *n_floats = o->n;
+  o->grads_zero = false;  // the caller may write through the pointer
   return HB_OK;
 }
 
@@ -2086,4 +2111,365 @@ extern "C" int hb_decode_greedy(hb_model* m, hb_kv* kv, const uint32_t* first, i
   TRY(check_err_word(m->ctx));
   kv->len += nsteps;
   return HB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// training: forward with kept activations + backward into the gradient arena
+// ---------------------------------------------------------------------------
+namespace hb {
+
+// Activations of one layer that the backward reads (the reference's per-layer
+// forward cache, layer.rs:684-806 with `cache`): token-major [T, features]
+// except Q/K/V, which are head-major [B][heads][Sp][hd] with Sp = S rounded up
+// to 64 (zero padding rows).
+struct LayerAct {
+  float *x, *x2, *h13;  // layer input, attention residual, FFN pre-activations h1|h3
+  f16 *xn, *x2n, *q, *k, *v, *attn, *gate;
+};
+
+struct TrainState {
+  // transposed fp16 weights for the dX products
+  void* wtbase = nullptr;
+  std::vector<f16*> wqkvT, woT, w13T, w2T;  // [dim][qkv], [q][dim], [dim][2h], [h][dim]
+  f16* eT = nullptr;                        // [dim][Vp], columns >= vocab zero
+  // activations and backward scratch for one (B, S)
+  void* abase = nullptr;
+  size_t abytes = 0;
+  int B = 0, S = 0;
+  std::vector<LayerAct> act;
+  float *xL = nullptr, *logits = nullptr, *loss = nullptr, *mean = nullptr;
+  f16* xf = nullptr;
+  uint32_t *tok = nullptr, *tgt = nullptr;
+  float *dy = nullptr, *dx2 = nullptr, *dtmp = nullptr, *rinv = nullptr, *part = nullptr;
+  float *sc = nullptr, *dp = nullptr;
+  f16 *d16 = nullptr, *d16T = nullptr, *dh = nullptr, *dhT = nullptr, *actT = nullptr;
+  f16 *dqkv = nullptr, *dqkvT = nullptr, *dl = nullptr, *dlT = nullptr;
+  f16 *dA = nullptr, *dAT = nullptr, *qT = nullptr, *kT = nullptr, *vt = nullptr;
+  f16 *P = nullptr, *PT = nullptr, *dS = nullptr, *dST = nullptr;
+};
+
+void train_free(TrainState* t) {
+  if (!t) return;
+  if (t->wtbase) (void)hipFree(t->wtbase);
+  if (t->abase) (void)hipFree(t->abase);
+  delete t;
+}
+
+}  // namespace hb
+
+namespace {
+
+long round64(long v) { return (v + 63) & ~63L; }
+
+// Transposed copies of every matrix, rebuilt after any weight write.
+int train_weights(hb_model* m) {
+  const hb_model_config& c = m->cfg;
+  TrainState* ts = m->train;
+  const long d = c.dim, h = c.hidden, q = c.q_dim, qkv = c.q_dim + 2L * c.kv_dim;
+  const long Vp = round64(c.vocab);
+  hipStream_t st = m->ctx->stream();
+  if (!ts->wtbase) {
+    const size_t per = align256(d * qkv * 2) + align256(q * d * 2) + align256(2 * h * d * 2) +
+                       align256(h * d * 2);
+    const size_t bytes = per * c.nlayers + align256(d * Vp * 2);
+    char* base = nullptr;
+    HIP_TRY(hipMalloc(&base, bytes));
+    ts->wtbase = base;
+    size_t off = 0;
+    for (int l = 0; l < c.nlayers; ++l) {
+      ts->wqkvT.push_back((f16*)(base + off)); off += align256(d * qkv * 2);
+      ts->woT.push_back((f16*)(base + off)); off += align256(q * d * 2);
+      ts->w13T.push_back((f16*)(base + off)); off += align256(2 * h * d * 2);
+      ts->w2T.push_back((f16*)(base + off)); off += align256(h * d * 2);
+    }
+    ts->eT = (f16*)(base + off);
+    m->wt_stale = true;
+  }
+  if (!m->wt_stale) return HB_OK;
+  for (int l = 0; l < c.nlayers; ++l) {
+    const LayerW& L = m->layers[l];
+    HIP_TRY(transpose_f16(L.wqkv, (int)qkv, (int)d, (int)d, 0, ts->wqkvT[l], (int)qkv, 0, 1, st));
+    HIP_TRY(transpose_f16(L.wo, (int)d, (int)q, (int)q, 0, ts->woT[l], (int)d, 0, 1, st));
+    HIP_TRY(transpose_f16(L.w13, (int)(2 * h), (int)d, (int)d, 0, ts->w13T[l], (int)(2 * h), 0, 1, st));
+    HIP_TRY(transpose_f16(L.w2, (int)d, (int)h, (int)h, 0, ts->w2T[l], (int)d, 0, 1, st));
+  }
+  HIP_TRY(transpose_f16(m->embed, c.vocab, (int)d, (int)d, 0, ts->eT, (int)Vp, 0, 1, st));
+  m->wt_stale = false;
+  return HB_OK;
+}
+
+// Activation + scratch arena for (B, S), zero-filled whenever the shape
+// changes so that every padding row and column starts at zero.
+int train_buffers(hb_model* m, int B, int S) {
+  const hb_model_config& c = m->cfg;
+  TrainState* ts = m->train;
+  if (ts->abase && ts->B == B && ts->S == S) return HB_OK;
+  const long T = (long)B * S, Sp = round64(S), Tp = round64(T), Vp = round64(c.vocab);
+  const long d = c.dim, h = c.hidden, q = c.q_dim, kv = c.kv_dim, qkv = q + 2 * kv, V = c.vocab;
+  const long qh = (long)B * c.heads * Sp * c.hd, kvh = (long)B * c.kv_heads * Sp * c.hd;
+  const long scores = (long)B * c.heads * Sp * Sp;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  struct ActOff {
+    size_t x, x2, h13, xn, x2n, q, k, v, attn, gate;
+  };
+  std::vector<ActOff> ao(c.nlayers);
+  for (auto& a : ao) {
+    a.x = take(T * d * 4); a.x2 = take(T * d * 4); a.h13 = take(T * 2 * h * 4);
+    a.xn = take(T * d * 2); a.x2n = take(T * d * 2); a.q = take(qh * 2); a.k = take(kvh * 2);
+    a.v = take(kvh * 2); a.attn = take(T * q * 2); a.gate = take(T * h * 2);
+  }
+  const size_t o_xL = take(T * d * 4), o_logits = take(T * V * 4), o_loss = take(T * 4),
+               o_mean = take(4), o_xf = take(T * d * 2), o_tok = take(T * 4), o_tgt = take(T * 4);
+  const size_t o_dy = take(T * d * 4), o_dx2 = take(T * d * 4), o_dtmp = take(T * d * 4),
+               o_rinv = take(T * 4), o_part = take(rmsnorm_backward_part_floats(c.dim) * 4);
+  const size_t o_sc = take(scores * 4), o_dp = take(scores * 4);
+  const long actw = std::max(std::max(h, d), q);
+  const size_t o_d16 = take(T * d * 2), o_d16T = take(d * Tp * 2), o_dh = take(T * 2 * h * 2),
+               o_dhT = take(2 * h * Tp * 2), o_actT = take(actw * Tp * 2), o_dqkv = take(T * qkv * 2),
+               o_dqkvT = take(qkv * Tp * 2), o_dl = take(T * Vp * 2), o_dlT = take(V * Tp * 2);
+  const size_t o_dA = take(qh * 2), o_dAT = take(qh * 2), o_qT = take(qh * 2), o_kT = take(kvh * 2),
+               o_vt = take(kvh * 2);
+  const size_t o_P = take(scores * 2), o_PT = take(scores * 2), o_dS = take(scores * 2),
+               o_dST = take(scores * 2);
+  hipStream_t st = m->ctx->stream();
+  if (off > ts->abytes) {
+    HIP_TRY(hipStreamSynchronize(st));
+    if (ts->abase) HIP_TRY(hipFree(ts->abase));
+    ts->abase = nullptr;
+    ts->abytes = 0;
+    HIP_TRY(hipMalloc(&ts->abase, off));
+    ts->abytes = off;
+  }
+  char* b = (char*)ts->abase;
+  ts->act.resize(c.nlayers);
+  for (int l = 0; l < c.nlayers; ++l) {
+    LayerAct& A = ts->act[l];
+    const ActOff& a = ao[l];
+    A.x = (float*)(b + a.x); A.x2 = (float*)(b + a.x2); A.h13 = (float*)(b + a.h13);
+    A.xn = (f16*)(b + a.xn); A.x2n = (f16*)(b + a.x2n); A.q = (f16*)(b + a.q); A.k = (f16*)(b + a.k);
+    A.v = (f16*)(b + a.v); A.attn = (f16*)(b + a.attn); A.gate = (f16*)(b + a.gate);
+  }
+  ts->xL = (float*)(b + o_xL); ts->logits = (float*)(b + o_logits); ts->loss = (float*)(b + o_loss);
+  ts->mean = (float*)(b + o_mean); ts->xf = (f16*)(b + o_xf); ts->tok = (uint32_t*)(b + o_tok);
+  ts->tgt = (uint32_t*)(b + o_tgt);
+  ts->dy = (float*)(b + o_dy); ts->dx2 = (float*)(b + o_dx2); ts->dtmp = (float*)(b + o_dtmp);
+  ts->rinv = (float*)(b + o_rinv); ts->part = (float*)(b + o_part);
+  ts->sc = (float*)(b + o_sc); ts->dp = (float*)(b + o_dp);
+  ts->d16 = (f16*)(b + o_d16); ts->d16T = (f16*)(b + o_d16T); ts->dh = (f16*)(b + o_dh);
+  ts->dhT = (f16*)(b + o_dhT); ts->actT = (f16*)(b + o_actT); ts->dqkv = (f16*)(b + o_dqkv);
+  ts->dqkvT = (f16*)(b + o_dqkvT); ts->dl = (f16*)(b + o_dl); ts->dlT = (f16*)(b + o_dlT);
+  ts->dA = (f16*)(b + o_dA); ts->dAT = (f16*)(b + o_dAT); ts->qT = (f16*)(b + o_qT);
+  ts->kT = (f16*)(b + o_kT); ts->vt = (f16*)(b + o_vt);
+  ts->P = (f16*)(b + o_P); ts->PT = (f16*)(b + o_PT); ts->dS = (f16*)(b + o_dS);
+  ts->dST = (f16*)(b + o_dST);
+  HIP_TRY(fill_f16_zero((f16*)b, off / 2, st));
+  ts->B = B;
+  ts->S = S;
+  return HB_OK;
+}
+
+// forward_ws (full_model.rs:187-247) keeping every layer's activations.
+int train_forward(hb_model* m, int B, int S) {
+  const hb_model_config& c = m->cfg;
+  TrainState* ts = m->train;
+  hipStream_t st = m->ctx->stream();
+  const int T = B * S, Sp = (int)round64(S);
+  const int qkv = c.q_dim + 2 * c.kv_dim;
+  const float alpha = alpha_of(c);
+  const size_t khs = (size_t)Sp * c.hd, kbs = (size_t)c.kv_heads * khs;
+  HIP_TRY(embedding(m->embed, ts->tok, T, c.dim, c.vocab, ts->act[0].x, m->ctx->d_err, st));
+  for (int l = 0; l < c.nlayers; ++l) {
+    const LayerW& L = m->layers[l];
+    const LayerAct& A = ts->act[l];
+    float* xout = l + 1 < c.nlayers ? ts->act[l + 1].x : ts->xL;
+    HIP_TRY(rmsnorm(A.x, c.dim, L.g1, T, c.dim, c.norm_eps, A.xn, nullptr, st));
+    EpiQKV e{};
+    e.q_dim = c.q_dim; e.kv_dim = c.kv_dim; e.hd = c.hd; e.S = S; e.heads = c.heads;
+    e.kv_heads = c.kv_heads; e.rope = m->rope; e.rope_ld = m->rope_len; e.d_pos = nullptr;
+    e.q = A.q; e.q_rows = Sp;
+    e.k = A.k; e.k_bstride = kbs; e.k_hstride = khs;
+    e.v = A.v; e.v_bstride = kbs; e.v_hstride = khs;
+    e.vt = ts->vt; e.vt_ld = Sp; e.tap = nullptr;
+    HIP_TRY(gemm_qkv(L.wqkv, A.xn, qkv, T, c.dim, e, st));
+    AttnPrefill a{};
+    a.q = A.q; a.q_rows = Sp; a.k = A.k; a.k_bstride = kbs; a.k_hstride = khs;
+    a.vt = ts->vt; a.vt_ld = Sp; a.out = A.attn; a.B = B; a.S = S; a.H = c.heads;
+    a.KVH = c.kv_heads; a.hd = c.hd; a.scale = 1.0f / sqrtf((float)c.hd);
+    HIP_TRY(attention_prefill(a, st));
+    GemmScratch so, s2;
+    TRY(residual_scratch(m, c.dim, T, c.q_dim, so));
+    HIP_TRY(gemm_residual_norm(L.wo, A.attn, c.dim, T, c.q_dim, EpiResidual{A.x, A.x2, c.dim, alpha},
+                               NormOut{L.g2, c.norm_eps, A.x2n}, &so, st));
+    HIP_TRY(gemm_swiglu(L.w13, A.x2n, 2 * c.hidden, T, c.dim, EpiSwiGLU{A.gate, A.h13, c.hidden}, st));
+    TRY(residual_scratch(m, c.dim, T, c.hidden, s2));
+    HIP_TRY(gemm_residual(L.w2, A.gate, c.dim, T, c.hidden, EpiResidual{A.x2, xout, c.dim, alpha}, &s2, st));
+  }
+  HIP_TRY(rmsnorm(ts->xL, c.dim, m->gamma_f, T, c.dim, c.norm_eps, ts->xf, nullptr, st));
+  HIP_TRY(gemm_logits(m->embed, ts->xf, c.vocab, T, c.dim, EpiLogits{ts->logits, c.vocab, c.softcap}, st));
+  HIP_TRY(cross_entropy(ts->logits, ts->tgt, T, c.vocab, ts->loss, nullptr, m->ctx->d_err, st));
+  HIP_TRY(mean_reduce(ts->loss, T, ts->mean, st));
+  return HB_OK;
+}
+
+// Attention backward of one layer (kernels/sdpa_bwd.rs:46-161) on the MFMA
+// GEMM, batched over z = b*kv_heads + g with the rep = heads/kv_heads query
+// heads of a group stacked as rows r*Sp + s:
+//   scores = Q K^T, dP = dO V^T            [rep*Sp, Sp] fp32 per z
+//   P, dS = causal softmax backward          fp16, then transposed
+//   dQ = dS K        (W = K^T)               -> RoPE^-1 -> dQKV columns of Q
+//   dK = dS^T Q      (K-dim rep*Sp)          -> RoPE^-1 -> dQKV columns of K
+//   dV = P^T dO      (K-dim rep*Sp)          -> dQKV columns of V
+// The stacked K-dimension of dK and dV is the sum over the group's heads.
+int attention_backward(hb_model* m, const LayerAct& A, int B, int S) {
+  const hb_model_config& c = m->cfg;
+  TrainState* ts = m->train;
+  hipStream_t st = m->ctx->stream();
+  const int Sp = (int)round64(S), T = B * S, Tp = (int)round64(T);
+  const int Z = B * c.kv_heads, rep = c.heads / c.kv_heads, Rq = rep * Sp, hd = c.hd;
+  const int qkv = c.q_dim + 2 * c.kv_dim;
+  const size_t khs = (size_t)Sp * hd, qzs = (size_t)Rq * hd, szs = (size_t)Rq * Sp;
+  const float scale = 1.0f / sqrtf((float)hd);
+  HIP_TRY(gemm_store_batched(A.k, A.q, Sp, Rq, hd, EpiStoreBatched{ts->sc, Sp, szs},
+                             GemmBatch{Z, khs, qzs}, st));
+  HIP_TRY(gemm_store_batched(A.v, ts->dA, Sp, Rq, hd, EpiStoreBatched{ts->dp, Sp, szs},
+                             GemmBatch{Z, khs, qzs}, st));
+  HIP_TRY(attn_softmax_backward(ts->sc, ts->dp, (long)Z * Rq, Sp, S, scale, ts->P, ts->dS, st));
+  HIP_TRY(transpose_f16(ts->dS, Rq, Sp, Sp, szs, ts->dST, Rq, szs, Z, st));
+  HIP_TRY(transpose_f16(ts->P, Rq, Sp, Sp, szs, ts->PT, Rq, szs, Z, st));
+  HIP_TRY(transpose_f16(A.k, Sp, hd, hd, khs, ts->kT, Sp, khs, Z, st));
+  HIP_TRY(transpose_f16(A.q, Rq, hd, hd, qzs, ts->qT, Rq, qzs, Z, st));
+  HIP_TRY(transpose_f16(ts->dA, Rq, hd, hd, qzs, ts->dAT, Rq, qzs, Z, st));
+  EpiAttnGrad e{};
+  e.d = ts->dqkv; e.dt = ts->dqkvT; e.ld = qkv; e.tld = Tp; e.rows = Sp; e.kv_heads = c.kv_heads;
+  e.S = S; e.hd = hd; e.rope_ld = m->rope_len;
+  e.col0 = 0; e.hpz = rep; e.rope = m->rope;
+  HIP_TRY(gemm_attn_grad(ts->kT, ts->dS, hd, Rq, Sp, e, GemmBatch{Z, khs, szs}, st));
+  e.col0 = c.q_dim; e.hpz = 1;
+  HIP_TRY(gemm_attn_grad(ts->qT, ts->dST, hd, Sp, Rq, e, GemmBatch{Z, qzs, szs}, st));
+  e.col0 = c.q_dim + c.kv_dim; e.rope = nullptr;
+  HIP_TRY(gemm_attn_grad(ts->dAT, ts->PT, hd, Sp, Rq, e, GemmBatch{Z, qzs, szs}, st));
+  return HB_OK;
+}
+
+// backward_ws (full_model.rs:250-331) with layer::backward_into
+// (layer.rs:1606-1858) per layer, accumulating into the optimizer's fp32
+// gradient arena (packed order, element for element like the fp16 weights).
+int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
+  const hb_model_config& c = m->cfg;
+  TrainState* ts = m->train;
+  hipStream_t st = m->ctx->stream();
+  const int T = B * S, Tp = (int)round64(T), Vp = (int)round64(c.vocab), Sp = (int)round64(S);
+  const int d = c.dim, h = c.hidden, q = c.q_dim, qkv = c.q_dim + 2 * c.kv_dim;
+  const float alpha = alpha_of(c);
+  float* g = o->g;
+  // every gradient element is written below: onto zeros, store instead of add
+  const bool acc = !o->grads_zero;
+  // head: dlogits, dX of the tied embedding, dE, final norm
+  HIP_TRY(ce_backward(ts->logits, ts->tgt, T, c.vocab, Vp, loss_scale / (float)S, c.softcap, ts->dl, st));
+  HIP_TRY(transpose_f16(ts->dl, T, c.vocab, Vp, 0, ts->dlT, Tp, 0, 1, st));
+  GemmScratch se;
+  TRY(residual_scratch(m, d, T, Vp, se, 512));
+  HIP_TRY(gemm_store_split(ts->eT, ts->dl, d, T, Vp, ts->dtmp, &se, st));
+  HIP_TRY(transpose_f16(ts->xf, T, d, d, 0, ts->actT, Tp, 0, 1, st));
+  HIP_TRY(gemm_wgrad(ts->actT, ts->dlT, d, c.vocab, Tp, g + o->embed_off, d, acc, st));
+  HIP_TRY(rmsnorm_backward(ts->dtmp, ts->xL, m->gamma_f, nullptr, T, d, c.norm_eps, ts->dy, ts->rinv,
+                           ts->part, g + o->gf_off, acc, st));
+  for (int l = c.nlayers - 1; l >= 0; --l) {
+    const LayerW& L = m->layers[l];
+    const LayerAct& A = ts->act[l];
+    const OptLayerOff& go = o->lo[l];
+    // FFN: x_out = x2 + alpha * W2 (silu(W1 x2n) * W3 x2n)
+    HIP_TRY(cast_transpose(ts->dy, T, d, alpha, ts->d16, ts->d16T, Tp, st));
+    HIP_TRY(gemm_silu_bwd(ts->w2T[l], ts->d16, h, T, d, EpiSiluBwd{A.h13, ts->dh, ts->dhT, h, Tp}, st));
+    GemmScratch s13, sqkv;
+    TRY(residual_scratch(m, d, T, 2 * h, s13, 512));
+    HIP_TRY(gemm_store_split(ts->w13T[l], ts->dh, d, T, 2 * h, ts->dtmp, &s13, st));
+    HIP_TRY(transpose_f16(A.gate, T, h, h, 0, ts->actT, Tp, 0, 1, st));
+    HIP_TRY(gemm_wgrad(ts->actT, ts->d16T, h, d, Tp, g + go.w2, h, acc, st));
+    HIP_TRY(transpose_f16(A.x2n, T, d, d, 0, ts->actT, Tp, 0, 1, st));
+    HIP_TRY(gemm_wgrad(ts->actT, ts->dhT, d, 2 * h, Tp, g + go.w13, d, acc, st));
+    HIP_TRY(rmsnorm_backward(ts->dtmp, A.x2, L.g2, ts->dy, T, d, c.norm_eps, ts->dx2, ts->rinv, ts->part,
+                             g + go.g2, acc, st));
+    // attention: x2 = x + alpha * Wo attn(x n)
+    HIP_TRY(cast_transpose(ts->dx2, T, d, alpha, ts->d16, ts->d16T, Tp, st));
+    HIP_TRY(gemm_heads(ts->woT[l], ts->d16, q, T, d, EpiHeads{ts->dA, S, c.heads, c.hd, Sp}, st));
+    HIP_TRY(transpose_f16(A.attn, T, q, q, 0, ts->actT, Tp, 0, 1, st));
+    HIP_TRY(gemm_wgrad(ts->actT, ts->d16T, q, d, Tp, g + go.wo, q, acc, st));
+    TRY(attention_backward(m, A, B, S));
+    TRY(residual_scratch(m, d, T, qkv, sqkv, 512));
+    HIP_TRY(gemm_store_split(ts->wqkvT[l], ts->dqkv, d, T, qkv, ts->dtmp, &sqkv, st));
+    HIP_TRY(transpose_f16(A.xn, T, d, d, 0, ts->actT, Tp, 0, 1, st));
+    HIP_TRY(gemm_wgrad(ts->actT, ts->dqkvT, d, qkv, Tp, g + go.wqkv, d, acc, st));
+    HIP_TRY(rmsnorm_backward(ts->dtmp, A.x, L.g1, ts->dx2, T, d, c.norm_eps, ts->dy, ts->rinv, ts->part,
+                             g + go.g1, acc, st));
+  }
+  HIP_TRY(embedding_backward(ts->dy, ts->tok, T, d, c.vocab, g + o->embed_off, st));
+  o->grads_zero = false;
+  return HB_OK;
+}
+
+// Checks the call and brings the transposed weights and the (B, S) buffers up to date.
+int train_prepare(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
+  const hb_model_config& c = m->cfg;
+  if (!o || o->model != m) return fail(HB_E_INVALID, "optimizer belongs to another model");
+  if (B <= 0 || S <= 0 || S > c.seq) return fail(HB_E_INVALID, "need B >= 1 and 1 <= S <= seq (%d)", c.seq);
+  if (!(loss_scale > 0.f) || !std::isfinite(loss_scale)) return fail(HB_E_INVALID, "loss_scale must be positive");
+  if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
+  if (c.dim > 8192) return fail(HB_E_CONFIG, "training needs dim <= 8192");
+  const long T = (long)B * S, Sp = round64(S);
+  if (round64(T) * std::max<long>(c.vocab, 2L * c.hidden) >= (1L << 31) ||
+      (long)c.heads / c.kv_heads * Sp * Sp >= (1L << 31) || (long)B * c.kv_heads > 65535)
+    return fail(HB_E_INVALID, "B=%d S=%d too large for one training call", B, S);
+  if (!m->train) m->train = new TrainState();
+  TRY(train_weights(m));
+  TRY(train_buffers(m, B, S));
+  return HB_OK;
+}
+
+}  // namespace
+
+extern "C" int hb_forward_backward_device(hb_model* m, hb_opt* o, const uint32_t* d_tokens,
+                                          const uint32_t* d_targets, int B, int S, float loss_scale,
+                                          float* d_loss, float* d_mean) {
+  HB_INJECT_CHECK();
+  if (!m || !o || !d_tokens || !d_targets) return fail(HB_E_INVALID, "null argument");
+  DeviceGuard g(m->ctx->device);
+  TRY(train_prepare(m, o, B, S, loss_scale));
+  TrainState* ts = m->train;
+  hipStream_t st = m->ctx->stream();
+  const size_t T = (size_t)B * S;
+  HIP_TRY(hipMemcpyAsync(ts->tok, d_tokens, T * 4, hipMemcpyDeviceToDevice, st));
+  HIP_TRY(hipMemcpyAsync(ts->tgt, d_targets, T * 4, hipMemcpyDeviceToDevice, st));
+  TRY(train_forward(m, B, S));
+  TRY(train_backward(m, o, B, S, loss_scale));
+  if (d_loss) HIP_TRY(hipMemcpyAsync(d_loss, ts->loss, T * 4, hipMemcpyDeviceToDevice, st));
+  if (d_mean) HIP_TRY(hipMemcpyAsync(d_mean, ts->mean, 4, hipMemcpyDeviceToDevice, st));
+  return HB_OK;
+}
+
+extern "C" int hb_forward_backward(hb_model* m, hb_opt* o, const uint32_t* tokens,
+                                   const uint32_t* targets, int B, int S, float loss_scale,
+                                   float* per_pos_loss, float* mean_loss) {
+  HB_INJECT_CHECK();
+  if (!m || !o || !tokens || !targets) return fail(HB_E_INVALID, "null argument");
+  DeviceGuard g(m->ctx->device);
+  TRY(train_prepare(m, o, B, S, loss_scale));
+  const size_t T = (size_t)B * S;
+  TRY(check_ids(tokens, T, m->cfg.vocab, "tokens"));
+  TRY(check_ids(targets, T, m->cfg.vocab, "targets"));
+  TrainState* ts = m->train;
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(ts->tok, tokens, T * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(ts->tgt, targets, T * 4, hipMemcpyHostToDevice, st));
+  TRY(train_forward(m, B, S));
+  TRY(train_backward(m, o, B, S, loss_scale));
+  if (per_pos_loss) HIP_TRY(hipMemcpyAsync(per_pos_loss, ts->loss, T * 4, hipMemcpyDeviceToHost, st));
+  if (mean_loss) HIP_TRY(hipMemcpyAsync(mean_loss, ts->mean, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return check_err_word(m->ctx);
 }

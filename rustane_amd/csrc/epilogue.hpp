@@ -215,4 +215,135 @@ struct EpiQKV {
   }
 };
 
+// ---- training (backward) epilogues ----
+
+// c[blockIdx.z * bstride + t * ldc + f0 ..] = v: batched fp32 store (attention
+// scores and their gradient, one batch entry per sequence and KV head).
+struct EpiStoreBatched {
+  float* c;
+  int ldc;
+  size_t bstride;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    float* p = c + blockIdx.z * bstride + (size_t)t * ldc + f0;
+    *(f32x4*)p = v;
+  }
+};
+
+// g[t * ld + f0 ..] += v: weight-gradient accumulation into the fp32 gradient
+// arena (layer.rs:1864-1867 accumulate_dw: dW += A B^T). Each element belongs
+// to exactly one lane of one tile, so the read-modify-write needs no atomics.
+// The old values are Aux operands, so the prefill GEMM loads them one
+// accumulator row ahead of the stores (as for EpiResidual) instead of exposing
+// a load latency per quad.
+struct EpiAccum {
+  float* g;
+  int ld;
+  using Aux = f32x4;
+  HB_DEV f32x4 load(int t, int f0, int = 0) const { return *(const f32x4*)(g + (size_t)t * ld + f0); }
+  HB_DEV void operator()(int t, int f0, f32x4 v, const f32x4& a, int = 0) const {
+    f32x4 o;
+    o.x = a.x + v.x;
+    o.y = a.y + v.y;
+    o.z = a.z + v.z;
+    o.w = a.w + v.w;
+    *(f32x4*)(g + (size_t)t * ld + f0) = o;
+  }
+  HB_DEV void operator()(int t, int f0, f32x4 v) const { (*this)(t, f0, v, load(t, f0)); }
+};
+
+// SwiGLU backward (layer.rs:1657-1666, cpu/silu.rs:20-33): v = dgate of hidden
+// units u..u+3 of token t; with h1, h3 the forward pre-activations (tap [T][2h]
+// = h1 | h3) and sig = 1/(1+exp(-h1)):
+//   dh3 = dgate * h1 sig,   dh1 = dgate * h3 * sig (1 + h1 (1 - sig)).
+// The result is written in the packed W1|W3 row order (see EpiSwiGLU) — eight
+// consecutive halfs dh1[u], dh1[u+1], dh3[u], dh3[u+1], dh1[u+2], dh1[u+3],
+// dh3[u+2], dh3[u+3] — once token-major (dh [T][2h], input of dX = dH W13) and
+// once feature-major (dht [2h][tld], tokens contiguous, operand of dW13 = dH^T X);
+// the feature-major stores are 64-byte runs across the 32 lanes of a row.
+struct EpiSiluBwd {
+  const float* tap;  // [T][2h] = h1 | h3
+  f16* dh;           // [T][2h]
+  f16* dht;          // [2h][tld]
+  int hidden, tld;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    const float* r = tap + (size_t)t * 2 * hidden;
+    const f32x4 h1 = *(const f32x4*)(r + f0), h3 = *(const f32x4*)(r + hidden + f0);
+    const float g[4] = {v.x, v.y, v.z, v.w}, a[4] = {h1.x, h1.y, h1.z, h1.w},
+                b[4] = {h3.x, h3.y, h3.z, h3.w};
+    float d1[4], d3[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float sg = 1.0f / (1.0f + __expf(-a[i]));
+      d3[i] = g[i] * (a[i] * sg);
+      d1[i] = g[i] * b[i] * (sg * (1.0f + a[i] * (1.0f - sg)));
+    }
+    const float o[8] = {d1[0], d1[1], d3[0], d3[1], d1[2], d1[3], d3[2], d3[3]};
+    f16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = (f16)o[i];
+    const int c0 = 2 * f0;
+    *(f16x8*)(dh + (size_t)t * 2 * hidden + c0) = h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dht[(size_t)(c0 + i) * tld + t] = h[i];
+  }
+};
+
+// Token-major [B*S][H*hd] result stored head-major as fp16: out[((b*H + h) *
+// rows + s) * hd + e] for token t = b*S + s (attention-output gradient, read
+// per head by the attention backward products).
+struct EpiHeads {
+  f16* out;
+  int S, H, hd, rows;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    const int b = t / S, s = t - b * S, h = f0 / hd, e = f0 - h * hd;
+    f16x4 o;
+    o.x = (f16)v.x;
+    o.y = (f16)v.y;
+    o.z = (f16)v.z;
+    o.w = (f16)v.w;
+    *(f16x4*)(out + (((size_t)b * H + h) * rows + s) * hd + e) = o;
+  }
+};
+
+// dQ, dK or dV of one batch entry z = b*kv_heads + g of the attention backward
+// (rows r*rows + s: head g*hpz + r, position s) into the packed QKV gradient,
+// token-major d [T][ld] and feature-major dt [ld][tld], at columns
+// col0 + head*hd + e. Q and K gradients go through the inverse of the forward
+// RoPE rotation (layer.rs:1880-1897 rope_backward_inplace):
+//   dx[2i] = d[2i] c + d[2i+1] s,   dx[2i+1] = d[2i+1] c - d[2i] s.
+// Padding positions s >= S are dropped.
+struct EpiAttnGrad {
+  static constexpr int kMaxFT = 128;  // N = hd
+  f16* d;
+  f16* dt;
+  int ld, tld, col0, rows, hpz, kv_heads, S, hd;
+  const float2* rope;  // [hd/2][rope_ld], NULL for V
+  int rope_ld;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    const int z = blockIdx.z, b = z / kv_heads, g = z - b * kv_heads;
+    const int r = t / rows, s = t - r * rows;
+    if (s >= S) return;
+    f32x4 o = v;
+    if (rope) {
+      const float2* rp = rope + (size_t)(f0 >> 1) * rope_ld + s;
+      const float2 c0 = rp[0], c1 = rp[rope_ld];
+      o.x = v.x * c0.x + v.y * c0.y;
+      o.y = v.y * c0.x - v.x * c0.y;
+      o.z = v.z * c1.x + v.w * c1.y;
+      o.w = v.w * c1.x - v.z * c1.y;
+    }
+    f16x4 h;
+    h.x = (f16)o.x;
+    h.y = (f16)o.y;
+    h.z = (f16)o.z;
+    h.w = (f16)o.w;
+    const int tok = b * S + s, col = col0 + (g * hpz + r) * hd + f0;
+    *(f16x4*)(d + (size_t)tok * ld + col) = h;
+    dt[(size_t)col * tld + tok] = h.x;
+    dt[(size_t)(col + 1) * tld + tok] = h.y;
+    dt[(size_t)(col + 2) * tld + tok] = h.z;
+    dt[(size_t)(col + 3) * tld + tok] = h.w;
+  }
+};
+
 }  // namespace hb

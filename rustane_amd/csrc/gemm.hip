@@ -6,12 +6,13 @@ namespace hb {
 
 template <int FT, int TT, int WF, int WT, class Epi>
 static hipError_t launch_tile(const f16* W, const f16* X, int N, int T, int K, const Epi& epi,
-                              hipStream_t st, int splits = 1) {
+                              hipStream_t st, int splits = 1, GemmBatch bt = {}) {
   const int tiles = ((N + FT - 1) / FT) * ((T + TT - 1) / TT);
   const int nk = K / 64, kq = (nk + splits - 1) / splits;
-  if (nk < 1 || splits < 1 || (splits - 1) * kq >= nk) return hipErrorInvalidValue;  // empty split
-  hipLaunchKernelGGL((gemm_nt_kernel<FT, TT, WF, WT, Epi>), dim3(tiles, splits), dim3(WF * WT * 64),
-                     0, st, W, X, N, T, K, kq, epi);
+  if (nk < 1 || K % 64 || splits < 1 || (splits - 1) * kq >= nk) return hipErrorInvalidValue;
+  if (bt.n < 1 || bt.n > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_nt_kernel<FT, TT, WF, WT, Epi>), dim3(tiles, splits, bt.n),
+                     dim3(WF * WT * 64), 0, st, W, X, N, T, K, kq, epi, bt.wbs, bt.xbs);
   return hipGetLastError();
 }
 
@@ -143,20 +144,32 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
 constexpr int GEMM_CUS = 256;  // MI355X compute units
 static long ntiles(int N, int T, int ft, int tt) { return (long)((N + ft - 1) / ft) * ((T + tt - 1) / tt); }
 
-int gemm_splits(int N, int T, int K) {
+int gemm_splits(int N, int T, int K, int wgs) {
   const long t = ntiles(N, T, 128, 128);
   const int nk = K / 64;
-  if (t >= GEMM_CUS || nk < 32) return 1;
-  int S = (int)std::min<long>(GEMM_MAX_SPLITS, GEMM_CUS / t);
+  if (t >= wgs || nk < 32) return 1;
+  int S = (int)std::min<long>(GEMM_MAX_SPLITS, wgs / t);
   S = std::min(S, nk / 8);
   return S >= 2 ? S : 1;
 }
 
+// Widest feature tile an epilogue is instantiated for (Epi::kMaxFT, default
+// 256): the attention-backward products have N = hd <= 128 features.
+template <class E, class = void>
+struct EpiMaxFT {
+  static constexpr int value = 256;
+};
+template <class E>
+struct EpiMaxFT<E, std::void_t<decltype(E::kMaxFT)>> {
+  static constexpr int value = E::kMaxFT;
+};
+
 template <class Epi>
 static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, const Epi& epi,
-                              const GemmScratch* scr, hipStream_t st) {
+                              const GemmScratch* scr, hipStream_t st, GemmBatch bt = {}) {
   if ((long)N * K >= (1L << 31) || (long)T * K >= (1L << 31)) return hipErrorInvalidValue;
-  const int S = scr ? gemm_splits(N, T, K) : 1;
+  if (bt.n != 1 && scr) return hipErrorInvalidValue;
+  const int S = scr ? gemm_splits(N, T, K, scr->wgs) : 1;
   if (S > 1) {
     const size_t stride = (size_t)T * N;
     if (!scr->p || (size_t)S * stride > scr->floats) return hipErrorInvalidValue;
@@ -182,8 +195,12 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
                                    {64, 128, 0.48f}};
   int best = 0;
   float best_score = -1.f;
+  constexpr int max_ft = EpiMaxFT<Epi>::value;
   for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
-    const long n = ntiles(N, T, cands[i].ft, cands[i].tt);
+    if (cands[i].ft > max_ft) continue;
+    // batched (attention) products: no tile wider than the features rounded to 64
+    if (bt.n > 1 && cands[i].ft > std::max(64, (N + 63) / 64 * 64)) continue;
+    const long n = ntiles(N, T, cands[i].ft, cands[i].tt) * bt.n;
     const float fill = (float)(n % GEMM_CUS) / GEMM_CUS;
     const float rounds = (float)(n / GEMM_CUS) + (fill > 0.f ? 0.4f + 0.6f * fill : 0.f);
     const float score = cands[i].rel * (float)n / (rounds * GEMM_CUS);
@@ -192,15 +209,17 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
       best = i;
     }
   }
-  switch (best) {
-    case 0: return launch_tile<256, 256, 2, 2>(W, X, N, T, K, epi, st);
-    case 1: return launch_tile<192, 256, 2, 2>(W, X, N, T, K, epi, st);
-    case 2: return launch_tile<128, 256, 2, 2>(W, X, N, T, K, epi, st);
-    case 3: return launch_tile<192, 128, 2, 2>(W, X, N, T, K, epi, st);
-    case 4: return launch_tile<256, 128, 2, 2>(W, X, N, T, K, epi, st);
-    case 5: return launch_tile<128, 128, 2, 2>(W, X, N, T, K, epi, st);
-    default: return launch_tile<64, 128, 2, 2>(W, X, N, T, K, epi, st);
+  if constexpr (max_ft >= 256) {
+    if (best == 0) return launch_tile<256, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
+    if (best == 4) return launch_tile<256, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
   }
+  if constexpr (max_ft >= 192) {
+    if (best == 1) return launch_tile<192, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
+    if (best == 3) return launch_tile<192, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
+  }
+  if (best == 2) return launch_tile<128, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
+  if (best == 5) return launch_tile<128, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
+  return launch_tile<64, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
 }
 
 hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st) {
@@ -213,7 +232,7 @@ hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const 
 hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
                               const NormOut& no, const GemmScratch* scr, hipStream_t st) {
   if (e.ld != N) return hipErrorInvalidValue;
-  const int S = scr ? gemm_splits(N, T, K) : 1;
+  const int S = scr ? gemm_splits(N, T, K, scr->wgs) : 1;
   if (S > 1) {
     const size_t stride = (size_t)T * N;
     if (!scr->p || (size_t)S * stride > scr->floats || (long)N * K >= (1L << 31)) return hipErrorInvalidValue;
@@ -251,6 +270,44 @@ hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQK
   EpiQKV ep = e;
   ep.prepare();
   return launch_gemm(W, X, N, T, K, ep, nullptr, st);
+}
+
+
+// ---- training ----
+hipError_t gemm_store_split(const f16* W, const f16* X, int N, int T, int K, float* C,
+                            const GemmScratch* scr, hipStream_t st) {
+  return launch_gemm(W, X, N, T, K, EpiStore{C, N}, scr, st);
+}
+hipError_t gemm_wgrad(const f16* W, const f16* X, int N, int T, int K, float* g, int ld,
+                      bool accumulate, hipStream_t st) {
+  if (N % 4 || ld < N || (long)N * K >= (1L << 31) || (long)T * K >= (1L << 31))
+    return hipErrorInvalidValue;
+  if (ntiles(N, T, 128, 128) >= 2 * GEMM_CUS) {
+    if (accumulate) return launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiAccum{g, ld}, st);
+    return launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiStore{g, ld}, st);
+  }
+  if (accumulate) return launch_gemm(W, X, N, T, K, EpiAccum{g, ld}, nullptr, st);
+  return launch_gemm(W, X, N, T, K, EpiStore{g, ld}, nullptr, st);
+}
+hipError_t gemm_silu_bwd(const f16* W, const f16* X, int N, int T, int K, const EpiSiluBwd& e,
+                         hipStream_t st) {
+  if (N != e.hidden || N % 4 || e.tld < T) return hipErrorInvalidValue;
+  return launch_gemm(W, X, N, T, K, e, nullptr, st);
+}
+hipError_t gemm_heads(const f16* W, const f16* X, int N, int T, int K, const EpiHeads& e,
+                      hipStream_t st) {
+  if (N != e.H * e.hd || e.hd % 4 || e.rows < e.S) return hipErrorInvalidValue;
+  return launch_gemm(W, X, N, T, K, e, nullptr, st);
+}
+hipError_t gemm_store_batched(const f16* W, const f16* X, int N, int T, int K,
+                              const EpiStoreBatched& e, GemmBatch bt, hipStream_t st) {
+  if (N % 4 || e.ldc < N) return hipErrorInvalidValue;
+  return launch_gemm(W, X, N, T, K, e, nullptr, st, bt);
+}
+hipError_t gemm_attn_grad(const f16* W, const f16* X, int N, int T, int K, const EpiAttnGrad& e,
+                          GemmBatch bt, hipStream_t st) {
+  if (N != e.hd || e.hd % 4 || T != e.rows * e.hpz || e.rows < e.S) return hipErrorInvalidValue;
+  return launch_gemm(W, X, N, T, K, e, nullptr, st, bt);
 }
 
 }  // namespace hb

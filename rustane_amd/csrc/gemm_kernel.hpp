@@ -68,10 +68,17 @@ struct EpiAux<E, std::void_t<typename E::Aux>> {
 // Split-K: blockIdx.y selects one of gridDim.y contiguous ranges of 64-wide K
 // slices (kq slices each, the last one shorter); with gridDim.y = 1 the range
 // is all of K. Each split hands its partial sums to the epilogue (EpiSplit).
+//
+// Batches: blockIdx.z selects one of gridDim.z independent products whose
+// operands start wbs and xbs halfs apart (attention backward: one per
+// sequence and KV head); epilogues that care read blockIdx.z themselves.
 template <int FT, int TT, int WF, int WT, class Epi>
 __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __restrict__ W,
                                                                  const f16* __restrict__ X, int N,
-                                                                 int T, int K, int kq, Epi epi) {
+                                                                 int T, int K, int kq, Epi epi,
+                                                                 size_t wbs, size_t xbs) {
+  W += blockIdx.z * wbs;
+  X += blockIdx.z * xbs;
   constexpr int NT = WF * WT * 64;
   constexpr int WFT = FT / WF, WTT = TT / WT;
   constexpr int FM = WFT / 32, TM = WTT / 32;

@@ -10,11 +10,17 @@ namespace hb {
 struct GemmScratch {
   float* p;
   size_t floats;
+  int wgs = 256;  // workgroups the split count aims for (gemm_splits)
 };
 constexpr int GEMM_MAX_SPLITS = 8;
+// One product, or n of them with operands wbs / xbs halfs apart (blockIdx.z).
+struct GemmBatch {
+  int n = 1;
+  size_t wbs = 0, xbs = 0;
+};
 // Number of K splits the residual GEMM uses for this shape when given scratch
-// (1 = none); it needs splits * T * N floats.
-int gemm_splits(int N, int T, int K);
+// (1 = none), aiming at wgs workgroups; it needs splits * T * N floats.
+int gemm_splits(int N, int T, int K, int wgs = 256);
 hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st);
 hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
                          const GemmScratch* scr, hipStream_t st);
@@ -33,6 +39,27 @@ hipError_t gemm_logits(const f16* W, const f16* X, int N, int T, int K, const Ep
                        hipStream_t st);
 hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQKV& e,
                     hipStream_t st);
+
+// Training products (the epilogues are documented in epilogue.hpp). All take
+// K % 64 == 0; token-dimension (K = tokens) operands are zero-padded to it.
+// C = X W^T (fp32 store), split over K into scr when the shape leaves CUs idle
+// (gemm_splits), as the residual GEMMs are.
+hipError_t gemm_store_split(const f16* W, const f16* X, int N, int T, int K, float* C,
+                            const GemmScratch* scr, hipStream_t st);
+// Weight gradient g[t, f] (+)= sum_k X[t,k] W[f,k]: accumulate (EpiAccum) or,
+// when the arena is known to be zero, store. K (tokens) is short, so the fp32
+// read-modify-write dominates: 128x128 tiles (two per CU) when there are
+// enough of them.
+hipError_t gemm_wgrad(const f16* W, const f16* X, int N, int T, int K, float* g, int ld,
+                      bool accumulate, hipStream_t st);
+hipError_t gemm_silu_bwd(const f16* W, const f16* X, int N, int T, int K, const EpiSiluBwd& e,
+                         hipStream_t st);
+hipError_t gemm_heads(const f16* W, const f16* X, int N, int T, int K, const EpiHeads& e,
+                      hipStream_t st);
+hipError_t gemm_store_batched(const f16* W, const f16* X, int N, int T, int K,
+                              const EpiStoreBatched& e, GemmBatch bt, hipStream_t st);
+hipError_t gemm_attn_grad(const f16* W, const f16* X, int N, int T, int K, const EpiAttnGrad& e,
+                          GemmBatch bt, hipStream_t st);
 
 // ---- decode GEMV (gemv.hip): rows of X are the B <= 16 sequences ----
 // W arguments are decode copies in fragment-tiled order (tile_decode); N is a
@@ -166,5 +193,31 @@ struct ClipCfg {
 hipError_t grad_clip_scale(const double* partials, ClipCfg c, float* out, hipStream_t st);
 hipError_t scale_inplace(float* g, size_t n, const float* d_scale, hipStream_t st);
 hipError_t widen_f16(const f16* src, float* dst, size_t n, hipStream_t st);
+
+
+// ---- training backward (backward.hip) ----
+// dst[b][c][r] = src[b][r][c] (r < R, c < C; src rows lds apart, batches sbs /
+// dbs halfs apart); dst columns [R, ldd) are zeroed.
+hipError_t transpose_f16(const f16* src, int R, int C, int lds, size_t sbs, f16* dst, int ldd,
+                         size_t dbs, int batch, hipStream_t st);
+// dst[c][r] = fp16(scale * src[r][c]) with columns [R, ldd) zeroed; rm
+// (nullable) [R][C] gets the same fp16 values row-major.
+hipError_t cast_transpose(const float* src, int R, int C, float scale, f16* rm, f16* dst, int ldd,
+                          hipStream_t st);
+// dl [T][Vp] fp16 = (softmax(logits) - onehot) * gs (* (1 - (z/softcap)^2)).
+hipError_t ce_backward(const float* logits, const uint32_t* tgt, int T, int V, int Vp, float gs,
+                       float softcap, f16* dl, hipStream_t st);
+// out = res + RMSNorm-backward(dy) (res nullable); dgamma += gamma gradient.
+// rinv [T] and part [rmsnorm_backward_part_floats(dim)] are scratch.
+hipError_t rmsnorm_backward(const float* dy, const float* x, const float* gamma, const float* res,
+                            int T, int dim, float eps, float* out, float* rinv, float* part,
+                            float* dgamma, bool accumulate, hipStream_t st);
+size_t rmsnorm_backward_part_floats(int dim);
+// Causal softmax backward of nrows score rows of Sp keys (row g: position g % Sp).
+hipError_t attn_softmax_backward(const float* sc, const float* dp, long nrows, int Sp, int S,
+                                 float scale, f16* P, f16* dS, hipStream_t st);
+// dE[tok[t]] += dx[t], deterministic; tokens >= vocab are skipped.
+hipError_t embedding_backward(const float* dx, const uint32_t* tok, int T, int dim, int vocab,
+                              float* dE, hipStream_t st);
 
 }  // namespace hb

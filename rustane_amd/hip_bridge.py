@@ -156,6 +156,8 @@ SIGNATURES = {
     "hb_opt_step": [_P, _U32, C.POINTER(C.c_float)],
     "hb_opt_download_layer": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "hb_opt_download_embed": [_P, _I, _P, _P],
+    "hb_forward_backward": [_P, _P, _P, _P, _I, _I, _F, _P, _P],
+    "hb_forward_backward_device": [_P, _P, _P, _P, _I, _I, _F, _P, _P],
     "hb_rstk_read_header": [C.c_char_p, C.POINTER(hb_rstk_header)],
     "hb_model_load_rstk": [_P, _P, C.c_char_p, C.POINTER(C.c_uint32)],
     "hb_model_save_rstk": [_P, _P, _U32, C.c_char_p],
@@ -476,6 +478,29 @@ class Optimizer:
         out = C.c_float()
         call("hb_opt_step", self.handle, step, C.byref(out) if want_norm else None)
         return out.value if want_norm else None
+
+    def forward_backward(self, tokens, targets, batch: int, seq: int, loss_scale: float = 256.0,
+                         want_losses: bool = False):
+        """forward_ws + backward_ws (full_model.rs:187-331) of `batch`
+        sequences of `seq` tokens: the gradients of loss_scale * mean CE of
+        each sequence are ADDED to the gradient arena. Returns the mean loss
+        over all positions (and the per-position losses)."""
+        tok = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        tgt = np.ascontiguousarray(targets, dtype=np.uint32).reshape(-1)
+        n = batch * seq
+        if tok.size != n or tgt.size != n:
+            raise ValueError(f"expected {n} tokens and targets")
+        mean = C.c_float()
+        losses = np.empty(n, np.float32) if want_losses else None
+        call("hb_forward_backward", self.model.handle, self.handle, tok.ctypes.data, tgt.ctypes.data,
+             batch, seq, loss_scale, losses.ctypes.data if want_losses else None, C.byref(mean))
+        return (mean.value, losses) if want_losses else mean.value
+
+    def forward_backward_device(self, d_tokens: int, d_targets: int, batch: int, seq: int,
+                                loss_scale: float = 256.0, d_loss: int = 0, d_mean: int = 0) -> None:
+        """As forward_backward with the ids already in device memory (stream-ordered, no sync)."""
+        call("hb_forward_backward_device", self.model.handle, self.handle, d_tokens, d_targets,
+             batch, seq, loss_scale, d_loss or None, d_mean or None)
 
     def download_layer(self, layer: int, which: int = 0) -> dict:
         sh = self._layer_shapes()

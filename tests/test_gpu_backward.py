@@ -1,0 +1,253 @@
+"""Training forward + backward on the GPU (hb_forward_backward) against the
+backward oracle (oracle/backward.py, pinned by torch float64 autograd in
+tests/test_backward_oracle.py) on the same fp16-rounded weights.
+
+The device runs every product on fp16 MFMA inputs with fp32 accumulation (the
+activations, dlogits, dQKV, dH13 and attention probabilities are rounded to
+fp16 where they enter a GEMM), the oracle in fp32 throughout, so gradients
+agree to the fp16 rounding of those operands, not bit for bit. The bars below
+are per tensor:
+    max |dev - ref| <= GRAD_MAX_REL * max |ref|
+    ||dev - ref||_2 <= GRAD_L2_REL  * ||ref||_2
+and the loss within LOSS_RTOL. Accumulation (two calls add exactly twice one
+call) and run-to-run determinism are checked bit for bit.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import oracle.backward as OB
+from rustane_amd import engine as E
+from rustane_amd import hip_bridge as hb
+from rustane_amd.engine import CompiledKernels, ModelConfig, ModelWeights
+from tests._util import F32, f16_round, oracle_cfg, tiny_config, tokens_for
+
+pytestmark = pytest.mark.gpu
+
+# measured worst cases: max-rel 1.34e-3, l2-rel 1.24e-3 (tiny softcap, 48M)
+GRAD_MAX_REL = 5e-3
+GRAD_L2_REL = 5e-3
+LOSS_RTOL = 1e-3
+
+
+def _rounded_oracle_weights(w: ModelWeights):
+    ow = O.ModelW.of(w)
+    return O.ModelW(embed=f16_round(ow.embed), gamma_final=ow.gamma_final,
+                    layers=[O.LayerW(**{k: (f16_round(getattr(l, k)) if k.startswith("w") else getattr(l, k))
+                                        for k in O.LayerW.__dataclass_fields__}) for l in ow.layers])
+
+
+def _oracle(cfg, ow, tok, tgt, B, S, softcap, loss_scale):
+    """Sum over the B sequences of the oracle's per-sequence gradients."""
+    ocfg = oracle_cfg(cfg)
+    tot, losses, acc = None, [], None
+    for b in range(B):
+        loss, g = OB.model_forward_backward(ocfg, ow, tok[b * S:(b + 1) * S], tgt[b * S:(b + 1) * S],
+                                            softcap, loss_scale)
+        losses.append(loss)
+        if acc is None:
+            acc = g
+        else:
+            acc["embed"] = acc["embed"] + g["embed"]
+            acc["gamma_final"] = acc["gamma_final"] + g["gamma_final"]
+            for a, c in zip(acc["layers"], g["layers"]):
+                for k in OB.LAYER_TENSORS:
+                    a[k] = a[k] + c[k]
+    return float(np.mean(losses)), acc
+
+
+def _device_grads(opt, nlayers):
+    e, gf = opt.download_embed(hb.Optimizer.GRADS)
+    return {"embed": e, "gamma_final": gf,
+            "layers": [opt.download_layer(l, hb.Optimizer.GRADS) for l in range(nlayers)]}
+
+
+def _pairs(dev, ref):
+    out = [("embed", dev["embed"], ref["embed"]), ("gamma_final", dev["gamma_final"], ref["gamma_final"])]
+    for l, (a, b) in enumerate(zip(dev["layers"], ref["layers"])):
+        out += [(f"{l}.{k}", a[k], b[k]) for k in OB.LAYER_TENSORS]
+    return out
+
+
+def _compare(dev, ref, label):
+    worst_max, worst_l2 = 0.0, 0.0
+    fails = []
+    for name, a, b in _pairs(dev, ref):
+        a = np.asarray(a, np.float64).reshape(-1)
+        b = np.asarray(b, np.float64).reshape(-1)
+        emax = np.abs(a - b).max() / max(np.abs(b).max(), 1e-30)
+        el2 = np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+        worst_max, worst_l2 = max(worst_max, emax), max(worst_l2, el2)
+        if emax > GRAD_MAX_REL or el2 > GRAD_L2_REL:
+            fails.append((name, emax, el2))
+    print(f"{label}: worst max-rel {worst_max:.3e}, worst l2-rel {worst_l2:.3e}", flush=True)
+    assert not fails, fails
+
+
+def _run_case(cfg, B, S, seed, softcap=0.0, loss_scale=256.0, std=0.02):
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=seed, std=std)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    try:
+        k.set_softcap(softcap)
+        tok = tokens_for(cfg, B * S + 1, seed=seed + 100)
+        tokens, targets = tok[:-1], tok[1:]
+        print(f"case dim={cfg.dim} L={cfg.nlayers} H={cfg.heads}/{cfg.kv_heads} B={B} S={S} "
+              f"softcap={softcap}", flush=True)
+        st.opt.zero_grads()
+        mean, losses = st.opt.forward_backward(tokens, targets, B, S, loss_scale, want_losses=True)
+        dev = _device_grads(st.opt, cfg.nlayers)
+        ref_loss, ref = _oracle(cfg, _rounded_oracle_weights(w), tokens, targets, B, S, softcap,
+                                loss_scale)
+        print(f"loss device {mean:.6f} oracle {ref_loss:.6f}", flush=True)
+        assert abs(mean - ref_loss) <= LOSS_RTOL * ref_loss
+        assert abs(float(np.mean(losses)) - mean) <= 1e-5 * mean
+        _compare(dev, ref, f"B={B} S={S}")
+        return k, st, tokens, targets, dev
+    except BaseException:
+        st.close()
+        raise
+
+
+def test_tiny_mha_full_sequence():
+    cfg = tiny_config()
+    _, st, *_ = _run_case(cfg, 1, cfg.seq, seed=11)
+    st.close()
+
+
+def test_tiny_gqa_two_sequences_ragged_length():
+    """GQA (dK/dV summed over each group's query heads) and S = 33, not a
+    multiple of 64, so every padding row and column is exercised."""
+    cfg = tiny_config(heads=4, kv_heads=2)
+    _, st, *_ = _run_case(cfg, 2, 33, seed=12)
+    st.close()
+
+
+def test_tiny_softcap():
+    """Logits of about one softcap in size (|z|/c ~ 1), where tanh bends but
+    does not saturate. Deep in saturation the factor 1 - t^2 turns the fp16
+    GEMMs' relative logit error e into a relative gradient error of about
+    2 e |z| / c (|z|/c ~ 10 with std-0.3 weights gives ~2%), a property of the
+    fp16 forward, not of the backward."""
+    cfg = tiny_config()
+    _, st, *_ = _run_case(cfg, 1, cfg.seq, seed=13, softcap=0.5, std=0.05)
+    st.close()
+
+
+def test_48m_shape():
+    cfg = ModelConfig.llama_48m()
+    _, st, *_ = _run_case(cfg, 1, 128, seed=14)
+    st.close()
+
+
+def test_bars_catch_planted_oracle_mistakes():
+    """The same device gradients against an oracle with a plausible mistake
+    planted (on the CPU): the softmax-backward row sum dropped, the forward
+    RoPE rotation used for its inverse, the residual alpha left out. Each must
+    break the bars above."""
+    cfg = tiny_config()
+    k, st, tokens, targets, dev = _run_case(cfg, 1, cfg.seq, seed=18)
+    st.close()
+    ow = _rounded_oracle_weights(ModelWeights.synthetic(cfg, seed=18, std=0.02))
+    orig_sdpa, orig_rope, orig_layer = OB.sdpa_backward, OB.rope_backward_cf, OB.layer_backward
+
+    def no_row_sum(cfg_, q, kk, v, da, seq):
+        H, hd = cfg_.heads, cfg_.hd
+        scale = F32(1.0) / np.sqrt(F32(hd))
+        qh, kh, vh, dh = (np.asarray(a, F32).reshape(H, hd, seq).transpose(0, 2, 1) for a in (q, kk, v, da))
+        sc = (qh @ kh.transpose(0, 2, 1)) * scale + O.causal_mask(seq)[None]
+        p = np.exp(sc - sc.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        ds = p * (dh @ vh.transpose(0, 2, 1)) * scale
+        cf = lambda t: np.ascontiguousarray(t.transpose(0, 2, 1)).reshape(H * hd, seq).astype(F32)
+        return cf(ds @ kh), cf(ds.transpose(0, 2, 1) @ qh), cf(p.transpose(0, 2, 1) @ dh)
+
+    def forward_rotation(dx, heads, hd, seq, theta=10000.0):
+        return O.rope_apply_cf(dx, heads, hd, seq, *O.rope_table(seq, hd, theta))
+
+    def no_alpha(cfg_, lw, taps, x_in, dy, seq):
+        return orig_layer(O.Config(**{**cfg_.__dict__, "residual_alpha": 1.0}), lw, taps, x_in, dy, seq)
+
+    for name, fn in (("sdpa_backward", no_row_sum), ("rope_backward_cf", forward_rotation),
+                     ("layer_backward", no_alpha)):
+        setattr(OB, name, fn)
+        try:
+            _, ref = _oracle(cfg, ow, tokens, targets, 1, cfg.seq, 0.0, 256.0)
+            with pytest.raises(AssertionError):
+                _compare(dev, ref, f"planted {name}")
+        finally:
+            OB.sdpa_backward, OB.rope_backward_cf, OB.layer_backward = orig_sdpa, orig_rope, orig_layer
+
+
+def test_accumulation_and_determinism():
+    cfg = tiny_config(heads=4, kv_heads=1)
+    k, st, tokens, targets, one = _run_case(cfg, 2, cfg.seq, seed=15)
+    try:
+        st.opt.forward_backward(tokens, targets, 2, cfg.seq, 256.0)
+        two = _device_grads(st.opt, cfg.nlayers)
+        for name, a, b in _pairs(two, one):
+            if name == "embed":
+                # two additions per call (the dE product, then the token
+                # scatter-add): ((G + S) + G) + S is 2 (G + S) to fp32 rounding
+                np.testing.assert_allclose(a, np.asarray(b, F32) * 2, rtol=2e-6, atol=1e-7, err_msg=name)
+            else:
+                np.testing.assert_array_equal(a, np.asarray(b, F32) * 2, err_msg=name)
+        st.opt.zero_grads()
+        st.opt.forward_backward(tokens, targets, 2, cfg.seq, 256.0)
+        again = _device_grads(st.opt, cfg.nlayers)
+        for name, a, b in _pairs(again, one):
+            np.testing.assert_array_equal(a, b, err_msg=name)
+    finally:
+        st.close()
+
+
+def test_train_steps_lower_the_loss():
+    """hb_forward_backward + hb_opt_step as train_step (full_model.rs:661-714)
+    repeated on one batch: the loss must fall."""
+    cfg = tiny_config()
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=16, std=0.02)
+    st = E.ModelOptState(k, E.TrainConfig(max_lr=3e-3, warmup_steps=1, total_steps=100), weights=w)
+    try:
+        tok = tokens_for(cfg, cfg.seq + 1, seed=99)
+        losses = []
+        for step in range(8):
+            st.opt.zero_grads()
+            losses.append(st.opt.forward_backward(tok[:-1], tok[1:], 1, cfg.seq, 256.0))
+            st.opt.step(step, want_norm=False)
+        print("losses", [f"{x:.4f}" for x in losses], flush=True)
+        assert losses[-1] < losses[0] - 0.05
+        # the weights the forward reads changed with the steps
+        after = E.forward(cfg, k, None, tok[:-1], tok[1:])
+        assert abs(float(np.mean(after.losses)) - losses[-1]) < 0.5
+    finally:
+        st.close()
+
+
+def test_error_paths():
+    cfg = tiny_config()
+    k = CompiledKernels.compile(cfg)
+    k2 = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=17, std=0.02)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    other = hb.Optimizer(k2.model, E.TrainConfig())
+    try:
+        tok = tokens_for(cfg, cfg.seq + 1, seed=1)
+        for bad in (dict(loss_scale=0.0), dict(S=cfg.seq + 1)):
+            S = bad.get("S", cfg.seq)
+            t = np.resize(tok, S + 1)
+            with pytest.raises(hb.HipBridgeError) as e:
+                st.opt.forward_backward(t[:-1], t[1:], 1, S, bad.get("loss_scale", 256.0))
+            assert e.value.code == hb.HB_E_INVALID
+        # an optimizer of another model
+        with pytest.raises(hb.HipBridgeError):
+            hb.call("hb_forward_backward", k.model.handle, other.handle, tok.ctypes.data,
+                    tok.ctypes.data, 1, cfg.seq, 256.0, None, None)
+        # out-of-range ids are refused on the host
+        bad_tok = tok[:-1].copy()
+        bad_tok[3] = cfg.vocab
+        with pytest.raises(hb.HipBridgeError):
+            st.opt.forward_backward(bad_tok, tok[1:], 1, cfg.seq, 256.0)
+    finally:
+        other.close()
+        st.close()
