@@ -11,6 +11,8 @@ without changes:
   forward_ws         crates/engine/src/full_model.rs:187-247 -> mean loss
   forward_losses     crates/engine/src/full_model.rs:717-767 -> per-position losses
   Decoder            the single-token loop crates/metal-decode/src/lib.rs:1-8 plans
+  backward_ws        crates/engine/src/full_model.rs:250-331 (with forward_ws, one call)
+  train_step         crates/engine/src/full_model.rs:661-714
 
 All arithmetic runs on the GPU through the C ABI; this module only moves host
 arrays across it.
@@ -423,6 +425,39 @@ def optimizer_step(opt: ModelOptState, step: int) -> float:
     """The optimizer half of train_step (full_model.rs:697-711); returns the raw
     gradient norm."""
     return opt.opt.step(step)
+
+
+def backward_ws(cfg: ModelConfig, kernels: CompiledKernels, opt: ModelOptState, tokens, targets,
+                softcap: float, loss_scale: float, batch: int = 1) -> float:
+    """forward_ws + backward_ws (full_model.rs:187-331) in one device call
+    (hb_forward_backward): the gradients of loss_scale * mean CE of each of
+    the `batch` sequences are added to opt's gradient arena. Returns the mean
+    loss."""
+    kernels.set_softcap(softcap)
+    seq = len(np.asarray(tokens).reshape(-1)) // batch
+    return opt.opt.forward_backward(tokens, targets, batch, seq, loss_scale)
+
+
+def train_step(cfg: ModelConfig, kernels: CompiledKernels, opt: ModelOptState, data, step: int,
+               tc: TrainConfig) -> float:
+    """full_model.rs:661-714: zero the gradients, accum_steps microbatches of
+    one sequence at the LCG positions of 682, then the clip decision, the
+    learning rate and the AdamW update on the device. Returns the mean loss
+    of the microbatches."""
+    if opt.tc != tc:
+        raise ValueError("tc must be the TrainConfig the optimizer state was created with")
+    toks = data._t if isinstance(data, TokenData) else np.asarray(data)
+    seq = cfg.seq
+    max_pos = len(toks) - seq - 1
+    opt.zero_grads()
+    total = np.float32(0.0)
+    for micro in range(tc.accum_steps):
+        pos = random_position(step, micro, max_pos)
+        window = np.asarray(toks[pos:pos + seq + 1], dtype=np.uint32)
+        total = np.float32(total + np.float32(
+            backward_ws(cfg, kernels, opt, window[:-1], window[1:], tc.softcap, tc.loss_scale)))
+    opt.opt.step(step, want_norm=False)
+    return float(total / np.float32(tc.accum_steps))
 
 
 # ---------------------------------------------------------------------------

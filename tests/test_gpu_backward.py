@@ -224,6 +224,42 @@ def test_train_steps_lower_the_loss():
         st.close()
 
 
+def test_engine_train_step_accumulates_the_microbatches():
+    """engine.train_step (full_model.rs:661-714): accum_steps windows at the
+    LCG positions of full_model.rs:682, their gradients summed in the arena
+    (compared with the oracle's sum over the same windows), the mean loss
+    returned, then the update."""
+    import oracle.data as OD
+    cfg = tiny_config()
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=19, std=0.02)
+    tc = E.TrainConfig(accum_steps=3, warmup_steps=2, total_steps=50)
+    st = E.ModelOptState(k, tc, weights=w)
+    try:
+        data = tokens_for(cfg, 600, seed=7).astype(np.uint16)
+        step = 5
+        loss = E.train_step(cfg, k, st, data, step, tc)
+        dev = _device_grads(st.opt, cfg.nlayers)
+        ow = _rounded_oracle_weights(w)
+        max_pos = len(data) - cfg.seq - 1
+        toks, tgts = [], []
+        for micro in range(tc.accum_steps):
+            pos = OD.random_position(step, micro, max_pos)
+            toks.append(data[pos:pos + cfg.seq])
+            tgts.append(data[pos + 1:pos + cfg.seq + 1])
+        ref_loss, ref = _oracle(cfg, ow, np.concatenate(toks), np.concatenate(tgts), tc.accum_steps,
+                                cfg.seq, 0.0, tc.loss_scale)
+        print(f"train_step loss {loss:.6f} oracle {ref_loss:.6f}", flush=True)
+        assert abs(loss - ref_loss) <= LOSS_RTOL * ref_loss
+        _compare(dev, ref, "train_step arena")
+        # the update moved the master weights
+        assert np.abs(st.opt.download_layer(0, hb.Optimizer.WEIGHTS)["w2"] - w.layers[0].w2).max() > 0
+        with pytest.raises(ValueError):
+            E.train_step(cfg, k, st, data, step, E.TrainConfig())
+    finally:
+        st.close()
+
+
 def test_error_paths():
     cfg = tiny_config()
     k = CompiledKernels.compile(cfg)
