@@ -231,6 +231,9 @@ def main():
     # ---- training forward + backward and train_step ----
     if not args.no_train:
         extra["train"] = bench_train(k, cfg, stream, B, S)
+        if B == 1 and not args.no_b8:
+            # eight sequences per call: the weight-gradient products get K = 4096
+            extra["train"]["b8"] = bench_train(k, cfg, stream, 8, S, steps=2)
 
     # ---- CPU baseline (oracle, bounded sample) ----
     if not args.no_cpu_baseline:

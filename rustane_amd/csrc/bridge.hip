@@ -97,9 +97,9 @@ struct Workspace {
 
 }  // namespace
 
+
 namespace hb {
 struct TrainState;
-void train_free(TrainState* t);
 }  // namespace hb
 
 struct hb_model {
@@ -133,6 +133,49 @@ struct hb_model {
   TrainState* train = nullptr;
   bool wt_stale = true;
 };
+
+namespace hb {
+
+inline long round64(long v) { return (v + 63) & ~63L; }
+
+// Activations of one layer that the backward reads (the reference's per-layer
+// forward cache, layer.rs:684-806 with `cache`): token-major [T, features]
+// except Q/K/V, which are head-major [B][heads][Sp][hd] with Sp = S rounded up
+// to 64 (zero padding rows).
+struct LayerAct {
+  float *x, *x2, *h13;  // layer input, attention residual, FFN pre-activations h1|h3
+  f16 *xn, *x2n, *q, *k, *v, *attn, *gate;
+};
+
+struct TrainState {
+  // transposed fp16 weights for the dX products
+  void* wtbase = nullptr;
+  std::vector<f16*> wqkvT, woT, w13T, w2T;  // [dim][qkv], [q][dim], [dim][2h], [h][dim]
+  f16* eT = nullptr;                        // [dim][Vp], columns >= vocab zero
+  // activations and backward scratch for one (B, S)
+  void* abase = nullptr;
+  size_t abytes = 0;
+  int B = 0, S = 0;
+  std::vector<LayerAct> act;
+  float *xL = nullptr, *logits = nullptr, *loss = nullptr, *mean = nullptr;
+  f16* xf = nullptr;
+  uint32_t *tok = nullptr, *tgt = nullptr;
+  float *dy = nullptr, *dx2 = nullptr, *dtmp = nullptr, *rinv = nullptr, *part = nullptr;
+  float *sc = nullptr, *dp = nullptr;
+  f16 *d16 = nullptr, *d16T = nullptr, *dh = nullptr, *dhT = nullptr, *actT = nullptr;
+  f16 *dqkv = nullptr, *dqkvT = nullptr, *dl = nullptr, *dlT = nullptr;
+  f16 *dA = nullptr, *dAT = nullptr, *qT = nullptr, *kT = nullptr, *vt = nullptr;
+  f16 *P = nullptr, *PT = nullptr, *dS = nullptr, *dST = nullptr;
+};
+
+void train_free(TrainState* t) {
+  if (!t) return;
+  if (t->wtbase) (void)hipFree(t->wtbase);
+  if (t->abase) (void)hipFree(t->abase);
+  delete t;
+}
+
+}  // namespace hb
 
 struct hb_kv {
   hb_model* model = nullptr;
@@ -1032,15 +1075,41 @@ int opt_update(hb_opt* o, uint32_t t, float lr, float grad_scale, const float* d
   h.bc2 = 1.0f / (1.0f - powi_f32(tc.beta2, (int)t));
   h.gscale = grad_scale;
   const float matrix_lr = lr * tc.matrix_lr_scale, embed_lr = lr * tc.embed_lr_scale;
+  hb_model* mo = o->model;
+  TrainState* ts = mo->train;
+  const bool tiled = ts && ts->wtbase;  // keep the backward's transposed copies current
   for (const OptSeg& sg : o->segs) {
     AdamW hs = h;
     hs.lr = sg.group == OPT_MATRIX ? matrix_lr : sg.group == OPT_EMBED ? embed_lr : lr;
     hs.wd = sg.group == OPT_MATRIX ? tc.weight_decay : 0.0f;
+    if (tiled && sg.group != OPT_GAMMA) continue;
     HIP_TRY(adamw(o->p + sg.off, o->g + sg.off, o->m + sg.off, o->v + sg.off, sg.d16, sg.d32, sg.n,
                   hs, d_gscale, st));
   }
-  o->model->dec_stale = true;
-  o->model->wt_stale = true;
+  if (tiled) {
+    const hb_model_config& c = mo->cfg;
+    const int d = c.dim, q = c.q_dim, h2 = 2 * c.hidden, hh = c.hidden, qkv = c.q_dim + 2 * c.kv_dim;
+    AdamW hm = h, he = h;
+    hm.lr = matrix_lr;
+    hm.wd = tc.weight_decay;
+    he.lr = embed_lr;
+    he.wd = 0.0f;
+    auto upd = [&](size_t off, f16* dst, f16* dstT, int R, int C, int ldT, const AdamW& hp) {
+      return adamw_tiled(o->p + off, o->g + off, o->m + off, o->v + off, dst, dstT, R, C, ldT, hp,
+                         d_gscale, st);
+    };
+    for (int l = 0; l < c.nlayers; ++l) {
+      const OptLayerOff& lo = o->lo[l];
+      const LayerW& L = mo->layers[l];
+      HIP_TRY(upd(lo.wqkv, L.wqkv, ts->wqkvT[l], qkv, d, qkv, hm));
+      HIP_TRY(upd(lo.wo, L.wo, ts->woT[l], d, q, d, hm));
+      HIP_TRY(upd(lo.w13, L.w13, ts->w13T[l], h2, d, h2, hm));
+      HIP_TRY(upd(lo.w2, L.w2, ts->w2T[l], d, hh, d, hm));
+    }
+    HIP_TRY(upd(o->embed_off, mo->embed, ts->eT, c.vocab, d, (int)round64(c.vocab), he));
+  }
+  mo->dec_stale = true;
+  mo->wt_stale = !tiled;
   return HB_OK;
 }
 
@@ -2116,50 +2185,9 @@ extern "C" int hb_decode_greedy(hb_model* m, hb_kv* kv, const uint32_t* first, i
 // ---------------------------------------------------------------------------
 // training: forward with kept activations + backward into the gradient arena
 // ---------------------------------------------------------------------------
-namespace hb {
-
-// Activations of one layer that the backward reads (the reference's per-layer
-// forward cache, layer.rs:684-806 with `cache`): token-major [T, features]
-// except Q/K/V, which are head-major [B][heads][Sp][hd] with Sp = S rounded up
-// to 64 (zero padding rows).
-struct LayerAct {
-  float *x, *x2, *h13;  // layer input, attention residual, FFN pre-activations h1|h3
-  f16 *xn, *x2n, *q, *k, *v, *attn, *gate;
-};
-
-struct TrainState {
-  // transposed fp16 weights for the dX products
-  void* wtbase = nullptr;
-  std::vector<f16*> wqkvT, woT, w13T, w2T;  // [dim][qkv], [q][dim], [dim][2h], [h][dim]
-  f16* eT = nullptr;                        // [dim][Vp], columns >= vocab zero
-  // activations and backward scratch for one (B, S)
-  void* abase = nullptr;
-  size_t abytes = 0;
-  int B = 0, S = 0;
-  std::vector<LayerAct> act;
-  float *xL = nullptr, *logits = nullptr, *loss = nullptr, *mean = nullptr;
-  f16* xf = nullptr;
-  uint32_t *tok = nullptr, *tgt = nullptr;
-  float *dy = nullptr, *dx2 = nullptr, *dtmp = nullptr, *rinv = nullptr, *part = nullptr;
-  float *sc = nullptr, *dp = nullptr;
-  f16 *d16 = nullptr, *d16T = nullptr, *dh = nullptr, *dhT = nullptr, *actT = nullptr;
-  f16 *dqkv = nullptr, *dqkvT = nullptr, *dl = nullptr, *dlT = nullptr;
-  f16 *dA = nullptr, *dAT = nullptr, *qT = nullptr, *kT = nullptr, *vt = nullptr;
-  f16 *P = nullptr, *PT = nullptr, *dS = nullptr, *dST = nullptr;
-};
-
-void train_free(TrainState* t) {
-  if (!t) return;
-  if (t->wtbase) (void)hipFree(t->wtbase);
-  if (t->abase) (void)hipFree(t->abase);
-  delete t;
-}
-
-}  // namespace hb
 
 namespace {
 
-long round64(long v) { return (v + 63) & ~63L; }
 
 // Transposed copies of every matrix, rebuilt after any weight write.
 int train_weights(hb_model* m) {

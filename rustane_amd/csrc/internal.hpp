@@ -182,6 +182,10 @@ struct AdamW {
 // param is also written to dst16 (fp16 weights) or dst32 (fp32 gammas).
 hipError_t adamw(float* p, const float* g, float* m, float* v, f16* dst16, float* dst32, size_t n,
                  const AdamW& h, const float* d_gscale, hipStream_t st);
+// The same step for one matrix [R][C] that also writes its fp16 transpose
+// dstT [C][ldT] (ldT >= R, multiple of 8; columns [R, ldT) zero).
+hipError_t adamw_tiled(float* p, const float* g, float* m, float* v, f16* dst, f16* dstT, int R,
+                       int C, int ldT, const AdamW& h, const float* d_gscale, hipStream_t st);
 constexpr int SUMSQ_BLOCKS = 1024;
 // partials[SUMSQ_BLOCKS] = fp64 sums of squares of fixed shares of g[0, n).
 hipError_t grad_sumsq(const float* g, size_t n, double* partials, hipStream_t st);

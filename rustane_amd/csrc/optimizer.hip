@@ -19,34 +19,40 @@ namespace hb {
 // evaluated in that order with every operation rounded to fp32 (no fused
 // multiply-adds), so results match the reference formula bit for bit where
 // sqrt and division are correctly rounded, which they are here (no fast-math).
+// Four consecutive elements; both kernels below evaluate exactly this.
+HB_DEV void adamw4(const f32x4& pv, const f32x4& gv, const f32x4& mv, const f32x4& vv, float gs,
+                   const AdamW& h, f32x4& po, f32x4& mo, f32x4& vo) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float gg = gv[e] * gs;
+    const float a = h.b1 * mv[e];
+    const float b = h.omb1 * gg;
+    const float mi = a + b;
+    const float c = h.b2 * vv[e];
+    const float d = h.omb2 * gg;
+    const float vi = c + d * gg;
+    const float mh = mi * h.bc1;
+    const float vh = vi * h.bc2;
+    const float upd = mh / (sqrtf(vh) + h.eps);
+    const float wdp = h.wd * pv[e];
+    po[e] = pv[e] - h.lr * (upd + wdp);
+    mo[e] = mi;
+    vo[e] = vi;
+  }
+}
+
 template <bool F16DST>
 __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, const float* __restrict__ g,
                                                     float* __restrict__ m, float* __restrict__ v,
                                                     void* __restrict__ dst, size_t n4, AdamW h,
                                                     const float* __restrict__ d_gscale) {
-#pragma clang fp contract(off)
   const float gs = d_gscale ? *d_gscale : h.gscale;
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
     const f32x4 pv = ((const f32x4*)p)[i], gv = ((const f32x4*)g)[i];
     const f32x4 mv = ((const f32x4*)m)[i], vv = ((const f32x4*)v)[i];
     f32x4 po, mo, vo;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float gg = gv[e] * gs;
-      const float a = h.b1 * mv[e];
-      const float b = h.omb1 * gg;
-      const float mi = a + b;
-      const float c = h.b2 * vv[e];
-      const float d = h.omb2 * gg;
-      const float vi = c + d * gg;
-      const float mh = mi * h.bc1;
-      const float vh = vi * h.bc2;
-      const float upd = mh / (sqrtf(vh) + h.eps);
-      const float wdp = h.wd * pv[e];
-      po[e] = pv[e] - h.lr * (upd + wdp);
-      mo[e] = mi;
-      vo[e] = vi;
-    }
+    adamw4(pv, gv, mv, vv, gs, h, po, mo, vo);
     ((f32x4*)p)[i] = po;
     ((f32x4*)m)[i] = mo;
     ((f32x4*)v)[i] = vo;
@@ -79,6 +85,63 @@ hipError_t adamw(float* p, const float* g, float* m, float* v, f16* dst16, float
   else
     hipLaunchKernelGGL(adamw_kernel<false>, dim3(stream_blocks(n4)), dim3(256), 0, st, p, g, m, v,
                        (void*)dst32, n4, h, d_gscale);
+  return hipGetLastError();
+}
+
+// One matrix [R][C] (packed order) in 64x64 tiles: the same update, the fp16
+// weight written row-major (dst) and transposed (dstT [C][ldT], the copy the
+// training backward's dX products read), so an optimizer step leaves both
+// fp16 copies current without a separate transpose pass (+2 B per parameter
+// instead of reading and writing 4). Rows [R, ldT) of dstT's tiles are zero.
+__global__ __launch_bounds__(256) void adamw_tile_kernel(float* __restrict__ p,
+                                                         const float* __restrict__ g,
+                                                         float* __restrict__ m, float* __restrict__ v,
+                                                         f16* __restrict__ dst, f16* __restrict__ dstT,
+                                                         int R, int C, int ldT, AdamW h,
+                                                         const float* __restrict__ d_gscale) {
+  __shared__ f16x8 tile[64 * 9];  // [64 rows][72 halfs]
+  const float gs = d_gscale ? *d_gscale : h.gscale;
+  const int tid = threadIdx.x, c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  const int tx = tid & 15, ty = tid >> 4;
+  f16* t = (f16*)tile;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rl = ty + 16 * i, r = r0 + rl, c = c0 + tx * 4;
+    f16x4 o = {};
+    if (r < R && c < C) {
+      const size_t idx = (size_t)r * C + c;
+      const f32x4 pv = *(const f32x4*)(p + idx), gv = *(const f32x4*)(g + idx);
+      const f32x4 mv = *(const f32x4*)(m + idx), vv = *(const f32x4*)(v + idx);
+      f32x4 po, mo, vo;
+      adamw4(pv, gv, mv, vv, gs, h, po, mo, vo);
+      *(f32x4*)(p + idx) = po;
+      *(f32x4*)(m + idx) = mo;
+      *(f32x4*)(v + idx) = vo;
+      o.x = (f16)po.x;
+      o.y = (f16)po.y;
+      o.z = (f16)po.z;
+      o.w = (f16)po.w;
+      *(f16x4*)(dst + idx) = o;
+    }
+    *(f16x4*)(t + rl * 72 + tx * 4) = o;
+  }
+  __syncthreads();
+  const int lr = tid >> 3, lc = (tid & 7) * 8;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int cc = q * 32 + lr;
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = t[(lc + j) * 72 + cc];
+    if (c0 + cc < C && r0 + lc < ldT) *(f16x8*)(dstT + (size_t)(c0 + cc) * ldT + r0 + lc) = o;
+  }
+}
+
+hipError_t adamw_tiled(float* p, const float* g, float* m, float* v, f16* dst, f16* dstT, int R,
+                       int C, int ldT, const AdamW& h, const float* d_gscale, hipStream_t st) {
+  if (R < 1 || C < 4 || C % 4 || ldT < R || ldT % 8 || !dst || !dstT) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(adamw_tile_kernel, dim3((C + 63) / 64, (ldT + 63) / 64), dim3(256), 0, st, p, g,
+                     m, v, dst, dstT, R, C, ldT, h, d_gscale);
   return hipGetLastError();
 }
 

@@ -260,6 +260,57 @@ def test_engine_train_step_accumulates_the_microbatches():
         st.close()
 
 
+def test_optimizer_update_keeps_transposed_weights_current():
+    """Once a model trains, hb_opt updates its matrices with the tiled AdamW
+    kernel that also writes the transposed fp16 copies the backward reads:
+    weights and moments stay bit-exact with the oracle, and a backward after
+    the update equals, bit for bit, one on a fresh model uploaded with the
+    updated master weights (whose transposes are built from scratch)."""
+    import oracle.optimizer as OP
+    cfg = tiny_config(heads=4, kv_heads=2)
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=20, std=0.02)
+    tc = E.TrainConfig()
+    st = E.ModelOptState(k, tc, weights=w)
+    k2 = st2 = None
+    try:
+        tok = tokens_for(cfg, 2 * cfg.seq + 1, seed=21)
+        st.opt.zero_grads()
+        st.opt.forward_backward(tok[:-1], tok[1:], 2, cfg.seq, 256.0)
+        g = _device_grads(st.opt, cfg.nlayers)
+        ref = {"embed": np.array(w.embed, F32), "gamma_final": np.array(w.gamma_final, F32),
+               "layers": [{kk: np.array(getattr(lw, kk), F32) for kk in OP.LAYER_TENSORS} for lw in w.layers]}
+        mom = {"m": OP.zeros_like_state(ref), "v": OP.zeros_like_state(ref)}
+        for t in (1, 2):
+            OP.update_weights(ref, g, mom, t, F32(3e-3), tc, F32(1.0 / 256.0))
+            st.opt.update_weights(t, 3e-3, 1.0 / 256.0)
+        for which, want in ((hb.Optimizer.WEIGHTS, ref), (hb.Optimizer.M, mom["m"]), (hb.Optimizer.V, mom["v"])):
+            e, gf = st.opt.download_embed(which)
+            np.testing.assert_array_equal(e, want["embed"], err_msg=f"embed {which}")
+            for l in range(cfg.nlayers):
+                got = st.opt.download_layer(l, which)
+                for kk in OP.LAYER_TENSORS:
+                    np.testing.assert_array_equal(got[kk], want["layers"][l][kk], err_msg=f"{l}.{kk} {which}")
+        st.opt.zero_grads()
+        st.opt.forward_backward(tok[:-1], tok[1:], 2, cfg.seq, 256.0)
+        after = _device_grads(st.opt, cfg.nlayers)
+        # a fresh model with the updated master weights
+        e, gf = st.opt.download_embed(hb.Optimizer.WEIGHTS)
+        lws = [st.opt.download_layer(l, hb.Optimizer.WEIGHTS) for l in range(cfg.nlayers)]
+        w2 = ModelWeights(embed=e, gamma_final=gf, layers=[E.LayerWeights(**lw) for lw in lws])
+        k2 = CompiledKernels.compile(cfg)
+        st2 = E.ModelOptState(k2, tc, weights=w2)
+        st2.opt.zero_grads()
+        st2.opt.forward_backward(tok[:-1], tok[1:], 2, cfg.seq, 256.0)
+        fresh = _device_grads(st2.opt, cfg.nlayers)
+        for name, a, b in _pairs(after, fresh):
+            np.testing.assert_array_equal(a, b, err_msg=name)
+    finally:
+        st.close()
+        if st2 is not None:
+            st2.close()
+
+
 def test_error_paths():
     cfg = tiny_config()
     k = CompiledKernels.compile(cfg)
