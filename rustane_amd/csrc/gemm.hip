@@ -282,7 +282,10 @@ hipError_t gemm_wgrad(const f16* W, const f16* X, int N, int T, int K, float* g,
                       bool accumulate, hipStream_t st) {
   if (N % 4 || ld < N || (long)N * K >= (1L << 31) || (long)T * K >= (1L << 31))
     return hipErrorInvalidValue;
-  if (ntiles(N, T, 128, 128) >= 2 * GEMM_CUS) {
+  // short K (few tokens): the fp32 output traffic dominates, two 128x128
+  // tiles per CU overlap one's epilogue with the other's main loop; longer K
+  // is MFMA-bound and takes the usual tile choice
+  if (K <= 1024 && ntiles(N, T, 128, 128) >= 2 * GEMM_CUS) {
     if (accumulate) return launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiAccum{g, ld}, st);
     return launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiStore{g, ld}, st);
   }

@@ -47,8 +47,8 @@ hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQK
 hipError_t gemm_store_split(const f16* W, const f16* X, int N, int T, int K, float* C,
                             const GemmScratch* scr, hipStream_t st);
 // Weight gradient g[t, f] (+)= sum_k X[t,k] W[f,k]: accumulate (EpiAccum) or,
-// when the arena is known to be zero, store. K (tokens) is short, so the fp32
-// read-modify-write dominates: 128x128 tiles (two per CU) when there are
+// when the arena is known to be zero, store. With short K (<= 1024 tokens) the
+// fp32 read-modify-write dominates: 128x128 tiles (two per CU) when there are
 // enough of them.
 hipError_t gemm_wgrad(const f16* W, const f16* X, int N, int T, int K, float* g, int ld,
                       bool accumulate, hipStream_t st);
