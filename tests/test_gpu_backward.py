@@ -311,6 +311,35 @@ def test_optimizer_update_keeps_transposed_weights_current():
             st2.close()
 
 
+def test_shape_changes_leave_no_stale_padding():
+    """One model trained at (1, 40), then (2, 33) and (3, 21), then (1, 40)
+    again: the training buffers are reused or regrown and re-zeroed on every
+    shape change, so the last call reproduces the first bit for bit, and the
+    middle shapes agree with the oracle."""
+    cfg = tiny_config(heads=4, kv_heads=2)
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=22, std=0.02)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    try:
+        tok = tokens_for(cfg, 3 * cfg.seq + 1, seed=23)
+        ow = _rounded_oracle_weights(w)
+        runs = {}
+        for B, S in ((1, cfg.seq), (2, 33), (3, 21), (1, cfg.seq)):
+            st.opt.zero_grads()
+            n = B * S
+            st.opt.forward_backward(tok[:n], tok[1:n + 1], B, S, 256.0)
+            dev = _device_grads(st.opt, cfg.nlayers)
+            if (B, S) in runs:
+                for name, a, b in _pairs(dev, runs[(B, S)]):
+                    np.testing.assert_array_equal(a, b, err_msg=name)
+            else:
+                runs[(B, S)] = dev
+                _, ref = _oracle(cfg, ow, tok[:n], tok[1:n + 1], B, S, 0.0, 256.0)
+                _compare(dev, ref, f"B={B} S={S}")
+    finally:
+        st.close()
+
+
 def test_error_paths():
     cfg = tiny_config()
     k = CompiledKernels.compile(cfg)
