@@ -231,6 +231,8 @@ def main():
     # ---- training forward + backward and train_step ----
     if not args.no_train:
         extra["train"] = bench_train(k, cfg, stream, B, S)
+        if B == 1 and not args.no_cpu_baseline:
+            extra["train"]["cpu_baseline"] = cpu_baseline_train(cfg, S)
         if B == 1 and not args.no_b8:
             # eight sequences per call: the weight-gradient products get K = 4096
             extra["train"]["b8"] = bench_train(k, cfg, stream, 8, S, steps=2)
@@ -509,6 +511,61 @@ def cpu_baseline(cfg, S):
                          f"7B-shape forward at B=1 S={S} (best of 2); full forward = "
                          f"{cfg.nlayers} x {min(lt)*1e3:.0f} ms + {min(ht)*1e3:.0f} ms = {t_full:.2f} s"}
         log(f"[bench] cpu baseline: {res}")
+        return res
+    finally:
+        if ctx is not None:
+            ctx.unregister() if hasattr(ctx, "unregister") else None
+
+
+def cpu_baseline_train(cfg, S):
+    """fp32 oracle on the host: the forward (with its taps) and the backward of
+    one of the 32 layers of the 7B-shape model at one sequence of S tokens,
+    the head's forward + backward (final norm, logits, CE, dlogits, dE, dX)
+    once; a whole forward + backward is estimated as 32 x layer + head."""
+    import oracle as O
+    import oracle.backward as OB
+    from rustane_amd import hip_bridge as hb
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    cores = min(16, os.cpu_count() or 1)
+    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
+    try:
+        oc = O.Config.of(cfg)
+        d, q, kv, h, V = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden, cfg.vocab
+        n = lambda tid, cnt: hb.synth_normal(SEED, tid, cnt, STD)
+        lw = O.LayerW(wq=n(0, d * q), wk=n(1, d * kv), wv=n(2, d * kv), wo=n(3, q * d), w1=n(4, d * h),
+                      w3=n(5, d * h), w2=n(6, d * h), gamma1=np.ones(d, np.float32),
+                      gamma2=np.ones(d, np.float32))
+        E = n(hb.HB_SYNTH_EMBED_ID, V * d)
+        tok = hb.synth_tokens(42, 0, V, S + 1)
+        x = O.mtrans(O.embedding_forward(E, d, tok[:-1]), S, d)
+        rope = O.rope_table(S, cfg.hd)
+        gf = np.ones(d, np.float32)
+        t0 = time.perf_counter()
+        xl, taps = O.layer_forward(oc, lw, x, S, rope)
+        t_lf = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        xf, rinv = O.rmsnorm_channel_first(xl, gf, d, S)
+        logits = O.sgemm_at(O.mtrans(xf, d, S), S, d, E, V, np.zeros(S * V, np.float32))
+        _, dlog = OB.cross_entropy_fwd_bwd(logits, tok[1:], V, np.float32(1.0 / S))
+        dl = (dlog * np.float32(256.0)).reshape(S, V)
+        xf2 = np.asarray(xf, np.float32).reshape(d, S)
+        _ = (dl.T @ xf2.T).astype(np.float32)
+        dxf = (E.reshape(V, d).T @ dl.T).astype(np.float32).reshape(-1)
+        dy, _ = OB.rmsnorm_backward_cf(dxf, xl, gf, rinv, d, S)
+        t_head = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        OB.layer_backward(oc, lw, taps, x, dy, S)
+        t_lb = time.perf_counter() - t0
+        t_full = cfg.nlayers * (t_lf + t_lb) + t_head
+        res = {"value": round(S / t_full, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+               "sample": f"fp32 numpy oracle: forward + backward of 1 of {cfg.nlayers} layers and the "
+                         f"head of the 7B-shape model at one sequence of {S}; full fwd+bwd = "
+                         f"{cfg.nlayers} x ({t_lf*1e3:.0f} + {t_lb*1e3:.0f}) ms + {t_head*1e3:.0f} ms "
+                         f"= {t_full:.1f} s"}
+        log(f"[bench] cpu baseline (train): {res}")
         return res
     finally:
         if ctx is not None:
