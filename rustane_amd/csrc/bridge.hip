@@ -2413,7 +2413,8 @@ int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
     const OptLayerOff& go = o->lo[l];
     // FFN: x_out = x2 + alpha * W2 (silu(W1 x2n) * W3 x2n)
     HIP_TRY(cast_transpose(ts->dy, T, d, alpha, ts->d16, ts->d16T, Tp, st));
-    HIP_TRY(gemm_silu_bwd(ts->w2T[l], ts->d16, h, T, d, EpiSiluBwd{A.h13, ts->dh, ts->dhT, h, Tp}, st));
+    HIP_TRY(gemm_silu_bwd(ts->w2T[l], ts->d16, h, T, d, EpiSiluBwd{A.h13, ts->dh, h}, st));
+    HIP_TRY(transpose_f16(ts->dh, T, 2 * h, 2 * h, 0, ts->dhT, Tp, 0, 1, st));
     GemmScratch s13, sqkv;
     TRY(residual_scratch(m, d, T, 2 * h, s13, 512));
     HIP_TRY(gemm_store_split(ts->w13T[l], ts->dh, d, T, 2 * h, ts->dtmp, &s13, st));

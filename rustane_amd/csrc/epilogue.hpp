@@ -255,16 +255,15 @@ struct EpiAccum {
 // units u..u+3 of token t; with h1, h3 the forward pre-activations (tap [T][2h]
 // = h1 | h3) and sig = 1/(1+exp(-h1)):
 //   dh3 = dgate * h1 sig,   dh1 = dgate * h3 * sig (1 + h1 (1 - sig)).
-// The result is written in the packed W1|W3 row order (see EpiSwiGLU) — eight
-// consecutive halfs dh1[u], dh1[u+1], dh3[u], dh3[u+1], dh1[u+2], dh1[u+3],
-// dh3[u+2], dh3[u+3] — once token-major (dh [T][2h], input of dX = dH W13) and
-// once feature-major (dht [2h][tld], tokens contiguous, operand of dW13 = dH^T X);
-// the feature-major stores are 64-byte runs across the 32 lanes of a row.
+// The result is written token-major (dh [T][2h], input of dX = dH W13) in the
+// packed W1|W3 row order (see EpiSwiGLU): eight consecutive halfs dh1[u],
+// dh1[u+1], dh3[u], dh3[u+1], dh1[u+2], dh1[u+3], dh3[u+2], dh3[u+3], one
+// 16-byte store. (Its feature-major copy for dW13 is made by a separate
+// 16-byte-access transpose: eight 2-byte scatters per lane here cost more.)
 struct EpiSiluBwd {
   const float* tap;  // [T][2h] = h1 | h3
   f16* dh;           // [T][2h]
-  f16* dht;          // [2h][tld]
-  int hidden, tld;
+  int hidden;
   HB_DEV void operator()(int t, int f0, f32x4 v) const {
     const float* r = tap + (size_t)t * 2 * hidden;
     const f32x4 h1 = *(const f32x4*)(r + f0), h3 = *(const f32x4*)(r + hidden + f0);
@@ -281,10 +280,7 @@ struct EpiSiluBwd {
     f16x8 h;
 #pragma unroll
     for (int i = 0; i < 8; ++i) h[i] = (f16)o[i];
-    const int c0 = 2 * f0;
-    *(f16x8*)(dh + (size_t)t * 2 * hidden + c0) = h;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dht[(size_t)(c0 + i) * tld + t] = h[i];
+    *(f16x8*)(dh + (size_t)t * 2 * hidden + 2 * f0) = h;
   }
 };
 

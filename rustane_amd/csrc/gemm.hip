@@ -294,7 +294,7 @@ hipError_t gemm_wgrad(const f16* W, const f16* X, int N, int T, int K, float* g,
 }
 hipError_t gemm_silu_bwd(const f16* W, const f16* X, int N, int T, int K, const EpiSiluBwd& e,
                          hipStream_t st) {
-  if (N != e.hidden || N % 4 || e.tld < T) return hipErrorInvalidValue;
+  if (N != e.hidden || N % 4) return hipErrorInvalidValue;
   return launch_gemm(W, X, N, T, K, e, nullptr, st);
 }
 hipError_t gemm_heads(const f16* W, const f16* X, int N, int T, int K, const EpiHeads& e,
