@@ -12,6 +12,10 @@
  *   crates/engine/src/full_model.rs:187-247   forward_ws (model forward + mean loss)
  *   crates/engine/src/full_model.rs:717-767   forward_losses (per-position losses)
  *   crates/metal-decode/src/lib.rs:1-8        planned single-token decode (placeholder)
+ * and, for training, the rows next to that path:
+ *   crates/engine/src/full_model.rs:250-331   backward_ws (with layer.rs:1606-1858)
+ *   crates/engine/src/full_model.rs:487-714   update_weights / grad_norm / train_step
+ *   crates/engine/src/bin/train.rs:123-202    validation loop, RSTK checkpoints
  *
  * Conventions
  *   - Every entry point returns int: 0 (HB_OK) on success, a negative HB_E_* code
@@ -315,7 +319,10 @@ int hb_opt_upload_grads_embed(hb_opt* opt, const float* dembed, const float* dga
 /* ModelGrads::zero_out (train_step, full_model.rs:670). */
 int hb_opt_zero_grads(hb_opt* opt);
 /* The device gradient arena (fp32, packed order) for producers on the device:
- * pointer and length in floats. */
+ * pointer and length in floats. After this call the library no longer
+ * assumes a zeroed arena stays untouched, so hb_forward_backward always adds
+ * (it otherwise stores onto an arena that hb_opt_zero_grads just cleared:
+ * the same values with half the gradient traffic). */
 int hb_opt_grad_arena(hb_opt* opt, float** d_grads, uint64_t* n_floats);
 /* grad_norm (full_model.rs:600-622): global L2 norm of all gradients. */
 int hb_opt_grad_norm(hb_opt* opt, float* out_norm);

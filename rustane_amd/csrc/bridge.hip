@@ -883,7 +883,10 @@ struct hb_opt {
   float* scal = nullptr;  // [0] norm, [1] train_step scale, [2] clip_grads factor
   // The gradient arena holds zeros (creation, hb_opt_zero_grads) and nothing
   // has written it since: the next training backward stores instead of adding.
+  // Never set again once hb_opt_grad_arena has handed out the raw pointer
+  // (the caller may write through it at any time).
   bool grads_zero = true;
+  bool arena_exposed = false;
 };
 
 extern "C" int hb_learning_rate(const hb_train_config* tc, uint32_t step, float* out) {
@@ -1222,7 +1225,7 @@ extern "C" int hb_opt_zero_grads(hb_opt* o) {
   HB_OPT_CHECK(o);
   DeviceGuard g(o->device);
   HIP_TRY(fill_f32(o->g, 0.0f, o->n, o->model->ctx->stream()));
-  o->grads_zero = true;
+  o->grads_zero = !o->arena_exposed;
   return HB_OK;
 }
 
@@ -1231,7 +1234,8 @@ extern "C" int hb_opt_grad_arena(hb_opt* o, float** d_grads, uint64_t* n_floats)
   if (!d_grads || !n_floats) return fail(HB_E_INVALID, "null argument");
   *d_grads = o->g;
   *n_floats = o->n;
-  o->grads_zero = false;  // the caller may write through the pointer
+  o->grads_zero = false;  // the caller may write through the pointer from now on
+  o->arena_exposed = true;
   return HB_OK;
 }
 

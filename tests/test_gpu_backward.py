@@ -340,6 +340,37 @@ def test_shape_changes_leave_no_stale_padding():
         st.close()
 
 
+def test_writes_through_the_raw_arena_pointer_are_kept():
+    """After hb_opt_grad_arena hands out the pointer, a zeroed arena may be
+    written by the caller, so the backward must add to it, not overwrite."""
+    import torch
+    cfg = tiny_config()
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=24, std=0.02)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    try:
+        tok = tokens_for(cfg, cfg.seq + 1, seed=25)
+        st.opt.zero_grads()
+        st.opt.forward_backward(tok[:-1], tok[1:], 1, cfg.seq, 256.0)
+        base = _device_grads(st.opt, cfg.nlayers)
+        ptr, n = st.opt.grad_arena()
+        st.opt.zero_grads()
+
+        class _Arr:
+            __cuda_array_interface__ = {"shape": (n,), "typestr": "<f4", "data": (ptr, False), "version": 3}
+        torch.as_tensor(_Arr(), device="cuda").fill_(0.5)
+        torch.cuda.synchronize()
+        st.opt.forward_backward(tok[:-1], tok[1:], 1, cfg.seq, 256.0)
+        got = _device_grads(st.opt, cfg.nlayers)
+        for name, a, b in _pairs(got, base):
+            if name == "embed":
+                np.testing.assert_allclose(a, np.asarray(b, F32) + F32(0.5), rtol=1e-6, atol=1e-6, err_msg=name)
+            else:
+                np.testing.assert_array_equal(a, np.asarray(b, F32) + F32(0.5), err_msg=name)
+    finally:
+        st.close()
+
+
 def test_error_paths():
     cfg = tiny_config()
     k = CompiledKernels.compile(cfg)
