@@ -180,3 +180,19 @@ def test_learning_rate_matches_oracle():
         assert abs(int(a) - int(b)) <= 2, s
     with pytest.raises(hb.HipBridgeError):
         hb.learning_rate(E.TrainConfig(warmup_steps=0), 1)
+
+
+def test_training_entry_points_reject_null_arguments():
+    """hb_forward_backward(_device) check their handles and id pointers before
+    touching a device (no GPU needed)."""
+    import ctypes as C
+    lib = hb.lib()
+    ids = (C.c_uint32 * 4)()
+    for name in ("hb_forward_backward", "hb_forward_backward_device"):
+        f = getattr(lib, name)
+        f.restype = C.c_int
+        for args in ((None, None, ids, ids), (C.c_void_p(1), None, ids, ids),
+                     (C.c_void_p(1), C.c_void_p(1), None, ids), (C.c_void_p(1), C.c_void_p(1), ids, None)):
+            rc = f(*args, C.c_int(1), C.c_int(4), C.c_float(256.0), None, None)
+            assert rc == hb.HB_E_INVALID, (name, rc)
+            assert b"null" in lib.hb_last_error()
