@@ -123,6 +123,12 @@ def main():
                 d_loss.data_ptr(), None, d_mean.data_ptr())
 
     if args.train_only:
+        # the same 1 GiB reference copy as --kernel-only, for scaling counters
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
         print(json.dumps({"train": bench_train(k, cfg, stream, B, S, steps=args.steps)}), flush=True)
         return
 
@@ -442,13 +448,17 @@ def bench_train(k, cfg, stream, B, S, steps=4):
     finally:
         opt.close()
     fl = train_flops(cfg, B, S)
+    tfs = fl / (fb_ms / 1e3) / 1e12
     res = {"batch": B, "seq": S, "ms_per_fwd_bwd": round(fb_ms, 3),
            "tok_per_s_fwd_bwd": round(B * S / fb_ms * 1e3, 1),
            "tflop_per_s": round(fl / fb_ms / 1e9, 1), "mfma_frac": round(fl / (fb_ms / 1e3) / MFMA_PEAK_F16, 4),
            "tflop_per_fwd_bwd": round(fl / 1e12, 3),
            "ms_per_train_step": round(step_ms, 3), "tok_per_s_train_step": round(B * S / step_ms * 1e3, 1),
            "loss_first": round(loss0, 5), "loss_after_steps": round(loss1, 5),
-           "grad_norm_x_loss_scale": round(norm, 3)}
+           "grad_norm_x_loss_scale": round(norm, 3),
+           "roofline": {"bound": "mfma", "achieved": round(tfs, 1), "peak": MFMA_PEAK_F16 / 1e12,
+                        "unit": "TFLOP/s", "frac": round(tfs * 1e12 / MFMA_PEAK_F16, 4), "traffic": None,
+                        "kernel": "whole training forward + backward (algorithmic flops)"}}
     log(f"[bench] train: {res}")
     return res
 
