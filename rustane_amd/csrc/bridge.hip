@@ -2401,14 +2401,23 @@ int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
   float* g = o->g;
   // every gradient element is written below: onto zeros, store instead of add
   const bool acc = !o->grads_zero;
-  // head: dlogits, dX of the tied embedding, dE, final norm
-  HIP_TRY(ce_backward(ts->logits, ts->tgt, T, c.vocab, Vp, loss_scale / (float)S, c.softcap, ts->dl, st));
+  // head: dlogits, dX of the tied embedding, dE, final norm. |dlogits| <= gs
+  // = loss_scale/S while most entries are p*gs with p ~ 1/vocab: in fp16 they
+  // would sit at or below the subnormal range (the reference keeps this head
+  // in fp32, full_model.rs:250-331). So dl is stored as fp16(dl * f) with the
+  // power of two f that puts gs near 2^14, and both products divide f back
+  // out in their epilogues (exact).
+  const float gs = loss_scale / (float)S;
+  int fexp = 0;
+  (void)frexpf(16384.0f / gs, &fexp);
+  const float f = ldexpf(1.0f, fexp - 1), inv_f = ldexpf(1.0f, 1 - fexp);
+  HIP_TRY(ce_backward(ts->logits, ts->tgt, T, c.vocab, Vp, gs * f, c.softcap, ts->dl, st));
   HIP_TRY(transpose_f16(ts->dl, T, c.vocab, Vp, 0, ts->dlT, Tp, 0, 1, st));
   GemmScratch se;
   TRY(residual_scratch(m, d, T, Vp, se, 512));
-  HIP_TRY(gemm_store_split(ts->eT, ts->dl, d, T, Vp, ts->dtmp, &se, st));
+  HIP_TRY(gemm_store_split(ts->eT, ts->dl, d, T, Vp, ts->dtmp, &se, st, inv_f));
   HIP_TRY(transpose_f16(ts->xf, T, d, d, 0, ts->actT, Tp, 0, 1, st));
-  HIP_TRY(gemm_wgrad(ts->actT, ts->dlT, d, c.vocab, Tp, g + o->embed_off, d, acc, st));
+  HIP_TRY(gemm_wgrad(ts->actT, ts->dlT, d, c.vocab, Tp, g + o->embed_off, d, acc, st, inv_f));
   HIP_TRY(rmsnorm_backward(ts->dtmp, ts->xL, m->gamma_f, nullptr, T, d, c.norm_eps, ts->dy, ts->rinv,
                            ts->part, g + o->gf_off, acc, st));
   for (int l = c.nlayers - 1; l >= 0; --l) {

@@ -7,12 +7,19 @@
 
 namespace hb {
 
-// C[t, f0..f0+3] = v (fp32). Plain GEMM output.
+// C[t, f0..f0+3] = v * scale (fp32). Plain GEMM output; scale undoes a
+// power-of-two pre-scale of an fp16 operand (exact), 1 otherwise.
 struct EpiStore {
   float* c;
   int ldc;
+  float scale = 1.0f;
   HB_DEV void operator()(int t, int f0, f32x4 v) const {
-    *(f32x4*)(c + (size_t)t * ldc + f0) = v;
+    f32x4 o;
+    o.x = v.x * scale;
+    o.y = v.y * scale;
+    o.z = v.z * scale;
+    o.w = v.w * scale;
+    *(f32x4*)(c + (size_t)t * ldc + f0) = o;
   }
 };
 
@@ -238,14 +245,15 @@ struct EpiStoreBatched {
 struct EpiAccum {
   float* g;
   int ld;
+  float scale = 1.0f;  // as EpiStore
   using Aux = f32x4;
   HB_DEV f32x4 load(int t, int f0, int = 0) const { return *(const f32x4*)(g + (size_t)t * ld + f0); }
   HB_DEV void operator()(int t, int f0, f32x4 v, const f32x4& a, int = 0) const {
     f32x4 o;
-    o.x = a.x + v.x;
-    o.y = a.y + v.y;
-    o.z = a.z + v.z;
-    o.w = a.w + v.w;
+    o.x = a.x + v.x * scale;
+    o.y = a.y + v.y * scale;
+    o.z = a.z + v.z * scale;
+    o.w = a.w + v.w * scale;
     *(f32x4*)(g + (size_t)t * ld + f0) = o;
   }
   HB_DEV void operator()(int t, int f0, f32x4 v) const { (*this)(t, f0, v, load(t, f0)); }

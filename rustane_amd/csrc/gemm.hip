@@ -275,22 +275,22 @@ hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQK
 
 // ---- training ----
 hipError_t gemm_store_split(const f16* W, const f16* X, int N, int T, int K, float* C,
-                            const GemmScratch* scr, hipStream_t st) {
-  return launch_gemm(W, X, N, T, K, EpiStore{C, N}, scr, st);
+                            const GemmScratch* scr, hipStream_t st, float scale) {
+  return launch_gemm(W, X, N, T, K, EpiStore{C, N, scale}, scr, st);
 }
 hipError_t gemm_wgrad(const f16* W, const f16* X, int N, int T, int K, float* g, int ld,
-                      bool accumulate, hipStream_t st) {
+                      bool accumulate, hipStream_t st, float scale) {
   if (N % 4 || ld < N || (long)N * K >= (1L << 31) || (long)T * K >= (1L << 31))
     return hipErrorInvalidValue;
   // short K (few tokens): the fp32 output traffic dominates, two 128x128
   // tiles per CU overlap one's epilogue with the other's main loop; longer K
   // is MFMA-bound and takes the usual tile choice
   if (K <= 1024 && ntiles(N, T, 128, 128) >= 2 * GEMM_CUS) {
-    if (accumulate) return launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiAccum{g, ld}, st);
-    return launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiStore{g, ld}, st);
+    if (accumulate) return launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiAccum{g, ld, scale}, st);
+    return launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiStore{g, ld, scale}, st);
   }
-  if (accumulate) return launch_gemm(W, X, N, T, K, EpiAccum{g, ld}, nullptr, st);
-  return launch_gemm(W, X, N, T, K, EpiStore{g, ld}, nullptr, st);
+  if (accumulate) return launch_gemm(W, X, N, T, K, EpiAccum{g, ld, scale}, nullptr, st);
+  return launch_gemm(W, X, N, T, K, EpiStore{g, ld, scale}, nullptr, st);
 }
 hipError_t gemm_silu_bwd(const f16* W, const f16* X, int N, int T, int K, const EpiSiluBwd& e,
                          hipStream_t st) {

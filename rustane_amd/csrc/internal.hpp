@@ -45,13 +45,13 @@ hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQK
 // C = X W^T (fp32 store), split over K into scr when the shape leaves CUs idle
 // (gemm_splits), as the residual GEMMs are.
 hipError_t gemm_store_split(const f16* W, const f16* X, int N, int T, int K, float* C,
-                            const GemmScratch* scr, hipStream_t st);
+                            const GemmScratch* scr, hipStream_t st, float scale = 1.0f);
 // Weight gradient g[t, f] (+)= sum_k X[t,k] W[f,k]: accumulate (EpiAccum) or,
 // when the arena is known to be zero, store. With short K (<= 1024 tokens) the
 // fp32 read-modify-write dominates: 128x128 tiles (two per CU) when there are
 // enough of them.
 hipError_t gemm_wgrad(const f16* W, const f16* X, int N, int T, int K, float* g, int ld,
-                      bool accumulate, hipStream_t st);
+                      bool accumulate, hipStream_t st, float scale = 1.0f);
 hipError_t gemm_silu_bwd(const f16* W, const f16* X, int N, int T, int K, const EpiSiluBwd& e,
                          hipStream_t st);
 hipError_t gemm_heads(const f16* W, const f16* X, int N, int T, int K, const EpiHeads& e,

@@ -123,6 +123,13 @@ def test_tiny_gqa_two_sequences_ragged_length():
     st.close()
 
 
+def test_head_dim_128_gqa():
+    """hd = 128, the 7B/600M head size (the other cases use 64), with GQA."""
+    cfg = tiny_config(dim=256, hidden=512, heads=4, kv_heads=2, hd=128)
+    _, st, *_ = _run_case(cfg, 2, 37, seed=26)
+    st.close()
+
+
 def test_tiny_softcap():
     """Logits of about one softcap in size (|z|/c ~ 1), where tanh bends but
     does not saturate. Deep in saturation the factor 1 - t^2 turns the fp16
