@@ -316,7 +316,11 @@ int hb_opt_upload_grads_layer(hb_opt* opt, int layer, const float* dwq, const fl
                               const float* dw3, const float* dw2, const float* dgamma1,
                               const float* dgamma2);
 int hb_opt_upload_grads_embed(hb_opt* opt, const float* dembed, const float* dgamma_final);
-/* ModelGrads::zero_out (train_step, full_model.rs:670). */
+/* ModelGrads::zero_out (train_step, full_model.rs:670). Until the arena's
+ * pointer has been handed out (hb_opt_grad_arena) the clearing is deferred:
+ * every hb_opt_* call that reads or partly writes the gradients clears them
+ * first, and hb_forward_backward stores every element instead (the 27 GB
+ * fill of a 7B arena is then never done). */
 int hb_opt_zero_grads(hb_opt* opt);
 /* The device gradient arena (fp32, packed order) for producers on the device:
  * pointer and length in floats. After this call the library no longer

@@ -887,6 +887,10 @@ struct hb_opt {
   // (the caller may write through it at any time).
   bool grads_zero = true;
   bool arena_exposed = false;
+  // hb_opt_zero_grads left the clearing to the first consumer: the arena is
+  // logically zero but its memory is stale until opt_materialize (or a
+  // training backward, which stores every element) runs.
+  bool lazy_zero = false;
 };
 
 extern "C" int hb_learning_rate(const hb_train_config* tc, uint32_t step, float* out) {
@@ -1131,6 +1135,15 @@ int opt_read_norm(hb_opt* o, float* out) {
 }
 }  // namespace
 
+// Clears a lazily zeroed gradient arena before anything but a training
+// backward reads it or writes part of it.
+static int opt_materialize(hb_opt* o) {
+  if (!o->lazy_zero) return HB_OK;
+  HIP_TRY(fill_f32(o->g, 0.0f, o->n, o->model->ctx->stream()));
+  o->lazy_zero = false;
+  return HB_OK;
+}
+
 #define HB_OPT_CHECK(o)                                        \
   do {                                                         \
     HB_INJECT_CHECK();                                         \
@@ -1209,6 +1222,7 @@ extern "C" int hb_opt_upload_grads_layer(hb_opt* o, int layer, const float* dwq,
   for (const float* x : w)
     if (!x) return fail(HB_E_INVALID, "null gradient pointer");
   DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   o->grads_zero = false;
   return opt_put_layer(o, o->g, false, layer, w);
 }
@@ -1217,6 +1231,7 @@ extern "C" int hb_opt_upload_grads_embed(hb_opt* o, const float* dembed, const f
   HB_OPT_CHECK(o);
   if (!dembed || !dgamma_final) return fail(HB_E_INVALID, "null argument");
   DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   o->grads_zero = false;
   return opt_put_embed(o, o->g, false, dembed, dgamma_final);
 }
@@ -1224,14 +1239,23 @@ extern "C" int hb_opt_upload_grads_embed(hb_opt* o, const float* dembed, const f
 extern "C" int hb_opt_zero_grads(hb_opt* o) {
   HB_OPT_CHECK(o);
   DeviceGuard g(o->device);
-  HIP_TRY(fill_f32(o->g, 0.0f, o->n, o->model->ctx->stream()));
-  o->grads_zero = !o->arena_exposed;
+  if (o->arena_exposed) {
+    // the caller may read or write the memory directly: clear it now
+    HIP_TRY(fill_f32(o->g, 0.0f, o->n, o->model->ctx->stream()));
+    o->grads_zero = false;
+    o->lazy_zero = false;
+  } else {
+    o->grads_zero = true;
+    o->lazy_zero = true;
+  }
   return HB_OK;
 }
 
 extern "C" int hb_opt_grad_arena(hb_opt* o, float** d_grads, uint64_t* n_floats) {
   HB_OPT_CHECK(o);
   if (!d_grads || !n_floats) return fail(HB_E_INVALID, "null argument");
+  DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   *d_grads = o->g;
   *n_floats = o->n;
   o->grads_zero = false;  // the caller may write through the pointer from now on
@@ -1243,6 +1267,7 @@ extern "C" int hb_opt_grad_norm(hb_opt* o, float* out_norm) {
   HB_OPT_CHECK(o);
   if (!out_norm) return fail(HB_E_INVALID, "null argument");
   DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   TRY(opt_norm(o, ClipCfg{1.0f, o->tc.grad_clip}));
   return opt_read_norm(o, out_norm);
 }
@@ -1251,6 +1276,7 @@ extern "C" int hb_opt_clip_grads(hb_opt* o, float max_norm, float* out_norm) {
   HB_OPT_CHECK(o);
   if (!(max_norm > 0.f)) return fail(HB_E_INVALID, "max_norm must be positive");
   DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   TRY(opt_norm(o, ClipCfg{1.0f, max_norm}));
   HIP_TRY(scale_inplace(o->g, o->n, o->scal + 2, o->model->ctx->stream()));
   return out_norm ? opt_read_norm(o, out_norm) : HB_OK;
@@ -1260,12 +1286,14 @@ extern "C" int hb_opt_update_weights(hb_opt* o, uint32_t t, float lr, float grad
   HB_OPT_CHECK(o);
   if (t == 0) return fail(HB_E_INVALID, "t is 1-based");
   DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   return opt_update(o, t, lr, grad_scale, nullptr);
 }
 
 extern "C" int hb_opt_step(hb_opt* o, uint32_t step, float* out_norm) {
   HB_OPT_CHECK(o);
   DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   const hb_train_config& tc = o->tc;
   const float gsc = 1.0f / ((float)tc.accum_steps * tc.loss_scale);
   TRY(opt_norm(o, ClipCfg{gsc, tc.grad_clip}));
@@ -1285,6 +1313,7 @@ extern "C" int hb_opt_download_layer(hb_opt* o, int layer, int which, float* wq,
   for (float* x : w)
     if (!x) return fail(HB_E_INVALID, "null output pointer");
   DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   const OptLayerOff& lo = o->lo[layer];
   const int d = c.dim, q = c.q_dim, kv = c.kv_dim, h = c.hidden;
   const size_t n = lo.g2 + d - lo.wqkv;
@@ -1311,6 +1340,7 @@ extern "C" int hb_opt_download_embed(hb_opt* o, int which, float* embed, float* 
   if (!a) return fail(HB_E_INVALID, "which must be 0 (weights), 1 (m), 2 (v) or 3 (gradients)");
   if (!embed || !gamma_final) return fail(HB_E_INVALID, "null output pointer");
   DeviceGuard g(o->device);
+  TRY(opt_materialize(o));
   const hb_model_config& c = o->model->cfg;
   hipStream_t st = o->model->ctx->stream();
   HIP_TRY(hipMemcpyAsync(embed, a + o->embed_off, (size_t)c.vocab * c.dim * 4, hipMemcpyDeviceToHost, st));
@@ -2452,6 +2482,7 @@ int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
   }
   HIP_TRY(embedding_backward(ts->dy, ts->tok, T, d, c.vocab, g + o->embed_off, st));
   o->grads_zero = false;
+  o->lazy_zero = false;  // every element was stored above
   return HB_OK;
 }
 

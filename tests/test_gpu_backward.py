@@ -378,6 +378,45 @@ def test_writes_through_the_raw_arena_pointer_are_kept():
         st.close()
 
 
+def test_lazy_zero_grads_reads_as_zero():
+    """hb_opt_zero_grads defers the clearing to the first consumer: reads,
+    partial uploads and norms see zeros, and a training backward overwrites
+    every element."""
+    import oracle.optimizer as OP
+    cfg = tiny_config()
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=27, std=0.02)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    try:
+        rng = np.random.default_rng(28)
+        noise = {kk: rng.standard_normal(v.size).astype(F32) for kk, v in st.opt.download_layer(0, 3).items()}
+        for l in range(cfg.nlayers):
+            st.opt.upload_grads_layer(l, noise)
+        st.opt.zero_grads()
+        assert st.opt.grad_norm() == 0.0
+        st.opt.upload_grads_layer(1, noise)
+        st.opt.zero_grads()
+        st.opt.upload_grads_layer(0, noise)  # partial write onto a lazily zeroed arena
+        ref = np.sqrt(sum(float(np.sum(v.astype(np.float64) ** 2)) for v in noise.values()))
+        assert abs(st.opt.grad_norm() - ref) <= 1e-6 * ref
+        for kk, v in st.opt.download_layer(1, 3).items():
+            assert not v.any(), kk
+        # zero, then a backward: equal to the backward on a freshly created optimizer
+        tok = tokens_for(cfg, cfg.seq + 1, seed=29)
+        st.opt.zero_grads()
+        st.opt.forward_backward(tok[:-1], tok[1:], 1, cfg.seq, 256.0)
+        got = _device_grads(st.opt, cfg.nlayers)
+        st2 = E.ModelOptState(k, E.TrainConfig(), weights=w)
+        try:
+            st2.opt.forward_backward(tok[:-1], tok[1:], 1, cfg.seq, 256.0)
+            for name, a, b in _pairs(got, _device_grads(st2.opt, cfg.nlayers)):
+                np.testing.assert_array_equal(a, b, err_msg=name)
+        finally:
+            st2.close()
+    finally:
+        st.close()
+
+
 def test_error_paths():
     cfg = tiny_config()
     k = CompiledKernels.compile(cfg)
