@@ -319,10 +319,11 @@ def test_optimizer_update_keeps_transposed_weights_current():
 
 
 def test_shape_changes_leave_no_stale_padding():
-    """One model trained at (1, 40), then (2, 33) and (3, 21), then (1, 40)
-    again: the training buffers are reused or regrown and re-zeroed on every
-    shape change, so the last call reproduces the first bit for bit, and the
-    middle shapes agree with the oracle."""
+    """One model trained at (1, 40), then (2, 33), (3, 21) and (3, 1) -- one
+    token per sequence -- then (1, 40) again: the training buffers are reused
+    or regrown and re-zeroed on every shape change, so the last call
+    reproduces the first bit for bit, and the other shapes agree with the
+    oracle."""
     cfg = tiny_config(heads=4, kv_heads=2)
     k = CompiledKernels.compile(cfg)
     w = ModelWeights.synthetic(cfg, seed=22, std=0.02)
@@ -331,7 +332,7 @@ def test_shape_changes_leave_no_stale_padding():
         tok = tokens_for(cfg, 3 * cfg.seq + 1, seed=23)
         ow = _rounded_oracle_weights(w)
         runs = {}
-        for B, S in ((1, cfg.seq), (2, 33), (3, 21), (1, cfg.seq)):
+        for B, S in ((1, cfg.seq), (2, 33), (3, 21), (3, 1), (1, cfg.seq)):
             st.opt.zero_grads()
             n = B * S
             st.opt.forward_backward(tok[:n], tok[1:n + 1], B, S, 256.0)
