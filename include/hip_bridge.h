@@ -344,6 +344,10 @@ int hb_opt_update_weights(hb_opt* opt, uint32_t t, float lr, float grad_scale);
  * learning_rate(step), update_weights(t = step + 1). out_norm (nullable)
  * receives the raw norm, which waits for the step to finish. */
 int hb_opt_step(hb_opt* opt, uint32_t step, float* out_norm);
+/* (After hb_forward_backward the norm of hb_opt_step / hb_opt_grad_norm is
+ * assembled from sums of squares the backward took while writing the
+ * gradients -- no second pass over the arena -- until anything else writes
+ * the gradients.) */
 /* Read state back in the reference layouts: which = 0 master weights, 1 m,
  * 2 v, 3 gradients. */
 int hb_opt_download_layer(hb_opt* opt, int layer, int which, float* wq, float* wk, float* wv,

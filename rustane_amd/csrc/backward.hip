@@ -215,24 +215,33 @@ __global__ __launch_bounds__(256) void gamma_partial_kernel(const float* __restr
   part[(size_t)p * dim + d] = s;
 }
 __global__ __launch_bounds__(256) void gamma_reduce_kernel(const float* __restrict__ part, int dim,
-                                                           float* __restrict__ dgamma, int acc) {
+                                                           float* __restrict__ dgamma, int acc,
+                                                           float* __restrict__ sq) {
+  __shared__ float red[4];
   const int d = blockIdx.x * 256 + threadIdx.x;
-  if (d >= dim) return;
-  float s = 0.f;
-  for (int p = 0; p < NORM_PARTS; ++p) s += part[(size_t)p * dim + d];
-  dgamma[d] = acc ? dgamma[d] + s : s;
+  float val = 0.f;
+  if (d < dim) {
+    float s = 0.f;
+    for (int p = 0; p < NORM_PARTS; ++p) s += part[(size_t)p * dim + d];
+    val = acc ? dgamma[d] + s : s;
+    dgamma[d] = val;
+  }
+  if (sq) {
+    const float t = block_sum<4>(val * val, red);
+    if (threadIdx.x == 0) sq[blockIdx.x] = t;
+  }
 }
 
 hipError_t rmsnorm_backward(const float* dy, const float* x, const float* gamma, const float* res,
                             int T, int dim, float eps, float* out, float* rinv, float* part,
-                            float* dgamma, bool accumulate, hipStream_t st) {
+                            float* dgamma, bool accumulate, hipStream_t st, float* sq) {
   if (T < 1 || dim < 4 || dim % 4) return hipErrorInvalidValue;
   hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3(T), dim3(256), 0, st, dy, x, gamma, res, out, rinv, dim,
                      eps);
   hipLaunchKernelGGL(gamma_partial_kernel, dim3((dim + 255) / 256, NORM_PARTS), dim3(256), 0, st, dy,
                      x, rinv, T, dim, part);
   hipLaunchKernelGGL(gamma_reduce_kernel, dim3((dim + 255) / 256), dim3(256), 0, st, part, dim,
-                     dgamma, accumulate ? 1 : 0);
+                     dgamma, accumulate ? 1 : 0, sq);
   return hipGetLastError();
 }
 size_t rmsnorm_backward_part_floats(int dim) { return (size_t)NORM_PARTS * dim; }

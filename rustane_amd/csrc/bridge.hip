@@ -891,6 +891,14 @@ struct hb_opt {
   // logically zero but its memory is stale until opt_materialize (or a
   // training backward, which stores every element) runs.
   bool lazy_zero = false;
+  // Sums of squares taken while a training backward wrote the gradients (one
+  // fp32 per output tile or gamma block, then the embedding's fp64 partials):
+  // valid (sq_ready) until anything else writes the arena; the norm then
+  // needs no second pass over it.
+  float* sq_slots = nullptr;
+  long sq_cap = 0, sq_n = 0;
+  double* sq_embed = nullptr;  // [SUMSQ_BLOCKS]
+  bool sq_ready = false;
 };
 
 extern "C" int hb_learning_rate(const hb_train_config* tc, uint32_t step, float* out) {
@@ -997,6 +1005,8 @@ extern "C" int hb_opt_destroy(hb_opt* o) {
   DeviceGuard g(o->device);
   (void)hipDeviceSynchronize();
   (void)hipFree(o->base);
+  if (o->sq_slots) (void)hipFree(o->sq_slots);
+  if (o->sq_embed) (void)hipFree(o->sq_embed);
   delete o;
   return HB_OK;
 }
@@ -1122,7 +1132,10 @@ int opt_update(hb_opt* o, uint32_t t, float lr, float grad_scale, const float* d
 
 int opt_norm(hb_opt* o, ClipCfg cc) {
   hipStream_t st = o->model->ctx->stream();
-  HIP_TRY(grad_sumsq(o->g, o->n, o->partials, st));
+  if (o->sq_ready)
+    HIP_TRY(combine_sumsq(o->sq_slots, o->sq_n, o->sq_embed, o->partials, st));
+  else
+    HIP_TRY(grad_sumsq(o->g, o->n, o->partials, st));
   HIP_TRY(grad_clip_scale(o->partials, cc, o->scal, st));
   return HB_OK;
 }
@@ -1224,6 +1237,7 @@ extern "C" int hb_opt_upload_grads_layer(hb_opt* o, int layer, const float* dwq,
   DeviceGuard g(o->device);
   TRY(opt_materialize(o));
   o->grads_zero = false;
+  o->sq_ready = false;
   return opt_put_layer(o, o->g, false, layer, w);
 }
 
@@ -1233,12 +1247,14 @@ extern "C" int hb_opt_upload_grads_embed(hb_opt* o, const float* dembed, const f
   DeviceGuard g(o->device);
   TRY(opt_materialize(o));
   o->grads_zero = false;
+  o->sq_ready = false;
   return opt_put_embed(o, o->g, false, dembed, dgamma_final);
 }
 
 extern "C" int hb_opt_zero_grads(hb_opt* o) {
   HB_OPT_CHECK(o);
   DeviceGuard g(o->device);
+  o->sq_ready = false;
   if (o->arena_exposed) {
     // the caller may read or write the memory directly: clear it now
     HIP_TRY(fill_f32(o->g, 0.0f, o->n, o->model->ctx->stream()));
@@ -1260,6 +1276,7 @@ extern "C" int hb_opt_grad_arena(hb_opt* o, float** d_grads, uint64_t* n_floats)
   *n_floats = o->n;
   o->grads_zero = false;  // the caller may write through the pointer from now on
   o->arena_exposed = true;
+  o->sq_ready = false;
   return HB_OK;
 }
 
@@ -1279,6 +1296,7 @@ extern "C" int hb_opt_clip_grads(hb_opt* o, float max_norm, float* out_norm) {
   TRY(opt_materialize(o));
   TRY(opt_norm(o, ClipCfg{1.0f, max_norm}));
   HIP_TRY(scale_inplace(o->g, o->n, o->scal + 2, o->model->ctx->stream()));
+  o->sq_ready = false;
   return out_norm ? opt_read_norm(o, out_norm) : HB_OK;
 }
 
@@ -2431,6 +2449,28 @@ int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
   float* g = o->g;
   // every gradient element is written below: onto zeros, store instead of add
   const bool acc = !o->grads_zero;
+  // sums of squares of the written gradient (for the norm): one slot per
+  // weight-gradient tile and per 256 gamma entries; the embedding is summed
+  // after its scatter-add
+  const long gblk = (d + 255) / 256;
+  const long cap = c.nlayers * (gemm_wgrad_max_tiles(h, d) + gemm_wgrad_max_tiles(d, 2 * h) +
+                                gemm_wgrad_max_tiles(q, d) + gemm_wgrad_max_tiles(d, qkv) + 2 * gblk) +
+                   gblk;
+  if (o->sq_cap < cap) {
+    HIP_TRY(hipStreamSynchronize(st));
+    if (o->sq_slots) HIP_TRY(hipFree(o->sq_slots));
+    o->sq_slots = nullptr;
+    o->sq_cap = 0;
+    HIP_TRY(hipMalloc(&o->sq_slots, cap * sizeof(float)));
+    o->sq_cap = cap;
+  }
+  if (!o->sq_embed) HIP_TRY(hipMalloc(&o->sq_embed, SUMSQ_BLOCKS * sizeof(double)));
+  o->sq_ready = false;
+  long ns = 0;
+  // slots for the next writer (at most `need`), checked before its launch
+  auto slot = [&](long need) -> float* { return ns + need <= o->sq_cap ? o->sq_slots + ns : nullptr; };
+  float* sq = nullptr;
+  int nt = 0;
   // head: dlogits, dX of the tied embedding, dE, final norm. |dlogits| <= gs
   // = loss_scale/S while most entries are p*gs with p ~ 1/vocab: in fp16 they
   // would sit at or below the subnormal range (the reference keeps this head
@@ -2448,8 +2488,10 @@ int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
   HIP_TRY(gemm_store_split(ts->eT, ts->dl, d, T, Vp, ts->dtmp, &se, st, inv_f));
   HIP_TRY(transpose_f16(ts->xf, T, d, d, 0, ts->actT, Tp, 0, 1, st));
   HIP_TRY(gemm_wgrad(ts->actT, ts->dlT, d, c.vocab, Tp, g + o->embed_off, d, acc, st, inv_f));
+  if (!(sq = slot(gblk))) return fail(HB_E_STATE, "gradient norm slots exhausted");
   HIP_TRY(rmsnorm_backward(ts->dtmp, ts->xL, m->gamma_f, nullptr, T, d, c.norm_eps, ts->dy, ts->rinv,
-                           ts->part, g + o->gf_off, acc, st));
+                           ts->part, g + o->gf_off, acc, st, sq));
+  ns += gblk;
   for (int l = c.nlayers - 1; l >= 0; --l) {
     const LayerW& L = m->layers[l];
     const LayerAct& A = ts->act[l];
@@ -2462,25 +2504,40 @@ int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
     TRY(residual_scratch(m, d, T, 2 * h, s13, 512));
     HIP_TRY(gemm_store_split(ts->w13T[l], ts->dh, d, T, 2 * h, ts->dtmp, &s13, st));
     HIP_TRY(transpose_f16(A.gate, T, h, h, 0, ts->actT, Tp, 0, 1, st));
-    HIP_TRY(gemm_wgrad(ts->actT, ts->d16T, h, d, Tp, g + go.w2, h, acc, st));
+    if (!(sq = slot(gemm_wgrad_max_tiles(h, d)))) return fail(HB_E_STATE, "gradient norm slots exhausted");
+    HIP_TRY(gemm_wgrad(ts->actT, ts->d16T, h, d, Tp, g + go.w2, h, acc, st, 1.0f, sq, &nt));
+    ns += nt;
     HIP_TRY(transpose_f16(A.x2n, T, d, d, 0, ts->actT, Tp, 0, 1, st));
-    HIP_TRY(gemm_wgrad(ts->actT, ts->dhT, d, 2 * h, Tp, g + go.w13, d, acc, st));
+    if (!(sq = slot(gemm_wgrad_max_tiles(d, 2 * h)))) return fail(HB_E_STATE, "gradient norm slots exhausted");
+    HIP_TRY(gemm_wgrad(ts->actT, ts->dhT, d, 2 * h, Tp, g + go.w13, d, acc, st, 1.0f, sq, &nt));
+    ns += nt;
+    if (!(sq = slot(gblk))) return fail(HB_E_STATE, "gradient norm slots exhausted");
     HIP_TRY(rmsnorm_backward(ts->dtmp, A.x2, L.g2, ts->dy, T, d, c.norm_eps, ts->dx2, ts->rinv, ts->part,
-                             g + go.g2, acc, st));
+                             g + go.g2, acc, st, sq));
+    ns += gblk;
     // attention: x2 = x + alpha * Wo attn(x n)
     HIP_TRY(cast_transpose(ts->dx2, T, d, alpha, ts->d16, ts->d16T, Tp, st));
     HIP_TRY(gemm_heads(ts->woT[l], ts->d16, q, T, d, EpiHeads{ts->dA, S, c.heads, c.hd, Sp}, st));
     HIP_TRY(transpose_f16(A.attn, T, q, q, 0, ts->actT, Tp, 0, 1, st));
-    HIP_TRY(gemm_wgrad(ts->actT, ts->d16T, q, d, Tp, g + go.wo, q, acc, st));
+    if (!(sq = slot(gemm_wgrad_max_tiles(q, d)))) return fail(HB_E_STATE, "gradient norm slots exhausted");
+    HIP_TRY(gemm_wgrad(ts->actT, ts->d16T, q, d, Tp, g + go.wo, q, acc, st, 1.0f, sq, &nt));
+    ns += nt;
     TRY(attention_backward(m, A, B, S));
     TRY(residual_scratch(m, d, T, qkv, sqkv, 512));
     HIP_TRY(gemm_store_split(ts->wqkvT[l], ts->dqkv, d, T, qkv, ts->dtmp, &sqkv, st));
     HIP_TRY(transpose_f16(A.xn, T, d, d, 0, ts->actT, Tp, 0, 1, st));
-    HIP_TRY(gemm_wgrad(ts->actT, ts->dqkvT, d, qkv, Tp, g + go.wqkv, d, acc, st));
+    if (!(sq = slot(gemm_wgrad_max_tiles(d, qkv)))) return fail(HB_E_STATE, "gradient norm slots exhausted");
+    HIP_TRY(gemm_wgrad(ts->actT, ts->dqkvT, d, qkv, Tp, g + go.wqkv, d, acc, st, 1.0f, sq, &nt));
+    ns += nt;
+    if (!(sq = slot(gblk))) return fail(HB_E_STATE, "gradient norm slots exhausted");
     HIP_TRY(rmsnorm_backward(ts->dtmp, A.x, L.g1, ts->dx2, T, d, c.norm_eps, ts->dy, ts->rinv, ts->part,
-                             g + go.g1, acc, st));
+                             g + go.g1, acc, st, sq));
+    ns += gblk;
   }
   HIP_TRY(embedding_backward(ts->dy, ts->tok, T, d, c.vocab, g + o->embed_off, st));
+  HIP_TRY(grad_sumsq(g + o->embed_off, (size_t)c.vocab * d, o->sq_embed, st));
+  o->sq_n = ns;
+  o->sq_ready = true;
   o->grads_zero = false;
   o->lazy_zero = false;  // every element was stored above
   return HB_OK;

@@ -259,6 +259,46 @@ struct EpiAccum {
   HB_DEV void operator()(int t, int f0, f32x4 v) const { (*this)(t, f0, v, load(t, f0)); }
 };
 
+// The same two with the sum of squares of the stored values returned to the
+// GEMM, which writes one total per output tile to sq_out (the gradient norm's
+// partial sums, taken while the gradient is written instead of by a second
+// pass over the arena).
+struct EpiStoreSq {
+  static constexpr bool kSumSq = true;
+  float* c;
+  int ldc;
+  float scale;
+  float* sq_out;
+  HB_DEV float operator()(int t, int f0, f32x4 v) const {
+    f32x4 o;
+    o.x = v.x * scale;
+    o.y = v.y * scale;
+    o.z = v.z * scale;
+    o.w = v.w * scale;
+    *(f32x4*)(c + (size_t)t * ldc + f0) = o;
+    return o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+  }
+};
+struct EpiAccumSq {
+  static constexpr bool kSumSq = true;
+  float* g;
+  int ld;
+  float scale;
+  float* sq_out;
+  using Aux = f32x4;
+  HB_DEV f32x4 load(int t, int f0, int = 0) const { return *(const f32x4*)(g + (size_t)t * ld + f0); }
+  HB_DEV float operator()(int t, int f0, f32x4 v, const f32x4& a, int = 0) const {
+    f32x4 o;
+    o.x = a.x + v.x * scale;
+    o.y = a.y + v.y * scale;
+    o.z = a.z + v.z * scale;
+    o.w = a.w + v.w * scale;
+    *(f32x4*)(g + (size_t)t * ld + f0) = o;
+    return o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+  }
+  HB_DEV float operator()(int t, int f0, f32x4 v) const { return (*this)(t, f0, v, load(t, f0)); }
+};
+
 // SwiGLU backward (layer.rs:1657-1666, cpu/silu.rs:20-33): v = dgate of hidden
 // units u..u+3 of token t; with h1, h3 the forward pre-activations (tap [T][2h]
 // = h1 | h3) and sig = 1/(1+exp(-h1)):

@@ -37,16 +37,24 @@ template <class E, class = void>
 struct EpiAux {
   struct type {};
   static HB_DEV type load(const E&, int, int, int) { return {}; }
-  static HB_DEV void apply(const E& e, int t, int f0, f32x4 v, const type&, int) { e(t, f0, v); }
+  static HB_DEV auto apply(const E& e, int t, int f0, f32x4 v, const type&, int) { return e(t, f0, v); }
 };
 template <class E>
 struct EpiAux<E, std::void_t<typename E::Aux>> {
   using type = typename E::Aux;
   static HB_DEV type load(const E& e, int t, int f0, int fb) { return e.load(t, f0, fb); }
-  static HB_DEV void apply(const E& e, int t, int f0, f32x4 v, const type& a, int fb) {
-    e(t, f0, v, a, fb);
+  static HB_DEV auto apply(const E& e, int t, int f0, f32x4 v, const type& a, int fb) {
+    return e(t, f0, v, a, fb);
   }
 };
+
+// Epilogues with kSumSq return the sum of squares of the four values they
+// stored; the kernel adds them up per workgroup and writes the total to
+// epi.sq_out[tile] (one slot per output tile, fixed order for the reader).
+template <class E, class = void>
+struct EpiSumSq : std::false_type {};
+template <class E>
+struct EpiSumSq<E, std::void_t<decltype(E::kSumSq)>> : std::bool_constant<E::kSumSq> {};
 
 // Pipeline: two 64-wide K slices are in flight in registers while the MFMAs
 // consume a third from LDS. Iteration k computes slice k from LDS buffer k&1,
@@ -253,6 +261,7 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   // cannot be moved above stores that might alias them, so a load-store-load
   // chain per quad would expose the load latency once per quad.
   if constexpr (!HOIST) load_row(std::integral_constant<int, 0>{});
+  float lane_sq = 0.f;
   static_for<0, FM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     if constexpr (!HOIST && i + 1 < FM) load_row(std::integral_constant<int, i + 1>{});
@@ -266,10 +275,27 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
         v.y = acc[i][j][4 * g + 1];
         v.z = acc[i][j][4 * g + 2];
         v.w = acc[i][j][4 * g + 3];
-        AX::apply(epi, t, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
+        if constexpr (EpiSumSq<Epi>::value)
+          lane_sq += AX::apply(epi, t, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
+        else
+          AX::apply(epi, t, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
       }
     });
   });
+  if constexpr (EpiSumSq<Epi>::value) {
+    // The main loop ended on a barrier after its last LDS reads, so the
+    // operand buffers are free for the per-wave totals.
+    float* red = (float*)&sW[0][0];
+    const float s = wave_sum(lane_sq);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    if (tid == 0) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < WF * WT; ++w) tot += red[w];
+      epi.sq_out[tile] = tot;
+    }
+  }
 }
 
 }  // namespace hb

@@ -50,8 +50,12 @@ hipError_t gemm_store_split(const f16* W, const f16* X, int N, int T, int K, flo
 // when the arena is known to be zero, store. With short K (<= 1024 tokens) the
 // fp32 read-modify-write dominates: 128x128 tiles (two per CU) when there are
 // enough of them.
+// With sq_out, one sum of squares of the written gradient per output tile
+// goes to sq_out[0 .. *sq_tiles) (gemm_wgrad_max_tiles bounds the count).
 hipError_t gemm_wgrad(const f16* W, const f16* X, int N, int T, int K, float* g, int ld,
-                      bool accumulate, hipStream_t st, float scale = 1.0f);
+                      bool accumulate, hipStream_t st, float scale = 1.0f, float* sq_out = nullptr,
+                      int* sq_tiles = nullptr);
+inline long gemm_wgrad_max_tiles(int N, int T) { return (long)((N + 127) / 128) * ((T + 127) / 128); }
 hipError_t gemm_silu_bwd(const f16* W, const f16* X, int N, int T, int K, const EpiSiluBwd& e,
                          hipStream_t st);
 hipError_t gemm_heads(const f16* W, const f16* X, int N, int T, int K, const EpiHeads& e,
@@ -187,6 +191,10 @@ hipError_t adamw(float* p, const float* g, float* m, float* v, f16* dst16, float
 hipError_t adamw_tiled(float* p, const float* g, float* m, float* v, f16* dst, f16* dstT, int R,
                        int C, int ldT, const AdamW& h, const float* d_gscale, hipStream_t st);
 constexpr int SUMSQ_BLOCKS = 1024;
+// partials[SUMSQ_BLOCKS] (fp64) from n per-tile fp32 sums of squares plus
+// SUMSQ_BLOCKS fp64 partials of another region, in a fixed order.
+hipError_t combine_sumsq(const float* slots, long n, const double* extra, double* partials,
+                         hipStream_t st);
 // partials[SUMSQ_BLOCKS] = fp64 sums of squares of fixed shares of g[0, n).
 hipError_t grad_sumsq(const float* g, size_t n, double* partials, hipStream_t st);
 struct ClipCfg {
@@ -213,9 +221,11 @@ hipError_t ce_backward(const float* logits, const uint32_t* tgt, int T, int V, i
                        float softcap, f16* dl, hipStream_t st);
 // out = res + RMSNorm-backward(dy) (res nullable); dgamma += gamma gradient.
 // rinv [T] and part [rmsnorm_backward_part_floats(dim)] are scratch.
+// With sq (nullable), the sums of squares of the new dgamma values go to
+// sq[0 .. ceil(dim / 256)).
 hipError_t rmsnorm_backward(const float* dy, const float* x, const float* gamma, const float* res,
                             int T, int dim, float eps, float* out, float* rinv, float* part,
-                            float* dgamma, bool accumulate, hipStream_t st);
+                            float* dgamma, bool accumulate, hipStream_t st, float* sq = nullptr);
 size_t rmsnorm_backward_part_floats(int dim);
 // Causal softmax backward of nrows score rows of Sp keys (row g: position g % Sp).
 hipError_t attn_softmax_backward(const float* sc, const float* dp, long nrows, int Sp, int S,

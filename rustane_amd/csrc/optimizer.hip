@@ -145,6 +145,32 @@ hipError_t adamw_tiled(float* p, const float* g, float* m, float* v, f16* dst, f
   return hipGetLastError();
 }
 
+// ---- gradient norm from partial sums taken while the gradient was written ----
+// Block i folds slots i, i + SUMSQ_BLOCKS, ... (each thread a fixed strided
+// share, in fp64) and adds extra[i]: the same order on every run.
+__global__ __launch_bounds__(256) void combine_sumsq_kernel(const float* __restrict__ slots, long n,
+                                                            const double* __restrict__ extra,
+                                                            double* __restrict__ partials) {
+  __shared__ double red[4];
+  double s = 0.0;
+  for (long j = blockIdx.x + (long)SUMSQ_BLOCKS * threadIdx.x; j < n; j += (long)SUMSQ_BLOCKS * 256)
+    s += (double)slots[j];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) partials[blockIdx.x] = red[0] + red[1] + red[2] + red[3] + extra[blockIdx.x];
+}
+
+hipError_t combine_sumsq(const float* slots, long n, const double* extra, double* partials,
+                         hipStream_t st) {
+  if (n < 0 || !extra || !partials) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(combine_sumsq_kernel, dim3(SUMSQ_BLOCKS), dim3(256), 0, st, slots, n, extra,
+                     partials);
+  return hipGetLastError();
+}
+
 // ---- global gradient norm (full_model.rs:600-622) ----------------------------
 // A fixed grid of SUMSQ_BLOCKS workgroups, each summing a fixed strided share
 // of the squares in fp64 and writing one partial: the same result on every

@@ -418,6 +418,33 @@ def test_lazy_zero_grads_reads_as_zero():
         st.close()
 
 
+def test_gradient_norm_from_backward_partials():
+    """After a training backward the norm is assembled from sums of squares
+    taken while the gradients were written (per weight-gradient tile, per
+    gamma block, plus the embedding after its scatter-add) instead of a
+    second pass over the arena: equal to the float64 norm of the downloaded
+    gradients and to the full pass, after a stored and an accumulated call."""
+    cfg = tiny_config(heads=4, kv_heads=2)
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=30, std=0.02)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    try:
+        tok = tokens_for(cfg, 2 * cfg.seq + 1, seed=31)
+        st.opt.zero_grads()
+        for call in range(2):  # store, then accumulate
+            st.opt.forward_backward(tok[:-1], tok[1:], 2, cfg.seq, 256.0)
+            fused = st.opt.grad_norm()
+            dev = _device_grads(st.opt, cfg.nlayers)
+            ref = np.sqrt(sum(float(np.sum(np.asarray(a, np.float64) ** 2)) for _, a, _ in _pairs(dev, dev)))
+            print(f"call {call}: fused norm {fused:.7e} float64 {ref:.7e}", flush=True)
+            assert abs(fused - ref) <= 1e-6 * ref
+        st.opt.grad_arena()  # hands out the pointer: the next norm is a full pass
+        full = st.opt.grad_norm()
+        assert abs(fused - full) <= 1e-6 * full
+    finally:
+        st.close()
+
+
 def test_error_paths():
     cfg = tiny_config()
     k = CompiledKernels.compile(cfg)
