@@ -147,6 +147,22 @@ def test_48m_shape():
     st.close()
 
 
+def test_many_sequences_long_token_dimension():
+    """26 sequences of 40: 1040 tokens, so the weight-gradient products have
+    K = 1088 > 1024 and take the 256x256 tiles (with the gradient-norm sums)
+    instead of the short-K 128x128 ones."""
+    cfg = tiny_config()
+    k, st, *_ = _run_case(cfg, 26, cfg.seq, seed=32)
+    try:
+        fused = st.opt.grad_norm()
+        dev = _device_grads(st.opt, cfg.nlayers)
+        ref = np.sqrt(sum(float(np.sum(np.asarray(a, np.float64) ** 2)) for _, a, _ in _pairs(dev, dev)))
+        print(f"B=26: fused norm {fused:.7e} float64 {ref:.7e}", flush=True)
+        assert abs(fused - ref) <= 1e-6 * ref
+    finally:
+        st.close()
+
+
 def test_bars_catch_planted_oracle_mistakes():
     """The same device gradients against an oracle with a plausible mistake
     planted (on the CPU): the softmax-backward row sum dropped, the forward
