@@ -10,11 +10,15 @@ Also reported on the same line:
   roofline      the dominant kernel (the FFN up-projection GEMM with the SwiGLU
                 epilogue, 2*512*22016*4096 flop per launch) timed alone with HIP
                 events on the stream it runs on, against 2.5 PFLOP/s dense fp16;
-  decode        7B-shape greedy decode at batch 1 (and 16 with --decode-b16):
-                2048-token seeded prefill into the preallocated KV cache, then
-                256 steps replayed from one HIP graph; tok/s and HBM GB/s;
+  decode        7B-shape greedy decode at batch 1 and 16: 2048-token seeded
+                prefill into the preallocated KV cache, then 256 steps
+                replayed from one HIP graph; tok/s and HBM GB/s;
   prefill_b8    the same forward at batch 8;
-  cpu_baseline  the fp32 CPU oracle timed on this host on a bounded sample.
+  prefill       every other prefill workload: 7B seq 2048 at batch 1 and 8,
+                600M-shape at batch 1 and 8, 5B-shape at batch 4 (seq 512);
+  cpu_baseline  the fp32 CPU oracle timed on this host's CPU share on bounded
+                samples: the 7B forward (headline), each prefill workload's
+                forward and the 7B batch-1 decode step.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -75,7 +79,9 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--decode-ctx", type=int, default=2048)
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--decode-b16", action="store_true")
+    ap.add_argument("--no-decode-b16", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the 600M / 5B / 7B-seq-2048 prefill workloads")
     ap.add_argument("--no-b8", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-optimizer", action="store_true")
@@ -100,7 +106,7 @@ def main():
     stream = torch.cuda.Stream()  # default priority
     torch.cuda.set_stream(stream)
 
-    cfg = ModelConfig.llama_7b(seq=max(args.seq, 512))
+    cfg = ModelConfig.llama_7b(seq=max(args.seq, 2048))
     log(f"[bench] 7B-shape model: {cfg.param_count()/1e9:.3f}B params")
     k = CompiledKernels.compile(cfg)
     k.ctx.set_stream(stream.cuda_stream)
@@ -195,10 +201,14 @@ def main():
                                "loss": round(float(m8.cpu()[0]), 5)}
         log(f"[bench] prefill B=8: {ms8:.3f} ms, {extra['prefill_b8']}")
 
+    # ---- the other prefill workloads ----
+    if not args.no_configs and B == 1 and S == 512:
+        extra["prefill"] = bench_prefill_configs(k, cfg, stream, cpu=not args.no_cpu_baseline)
+
     # ---- decode ----
     if not args.no_decode:
         from rustane_amd.engine import Decoder
-        batches = [1] + ([16] if args.decode_b16 else [])
+        batches = [1] + ([] if args.no_decode_b16 else [16])
         dec_res = {}
         for DB in batches:
             P, n = args.decode_ctx, args.decode_steps
@@ -224,6 +234,8 @@ def main():
                                  "first_tokens": out[:4, 0].tolist()}
             log(f"[bench] decode B={DB}: {dec_res[f'b{DB}']}")
             dec.kv.close()
+        if not args.no_cpu_baseline:
+            dec_res["cpu_baseline_b1"] = cpu_baseline_decode(cfg, args.decode_ctx)
         extra["decode"] = dec_res
 
     # ---- validation loop (windows of a resident token stream) ----
@@ -482,49 +494,210 @@ def cpu_baseline_adam(n_params, sample=1 << 26):
                       f"whole model {n_params * best / sample:.1f} s"}
 
 
-def cpu_baseline(cfg, S):
-    """fp32 oracle on the host: one of the 32 layers plus the head (final norm,
-    logits, CE) of the same 7B-shape forward at batch 1; the full forward is
-    estimated as 32 x layer + head."""
-    import oracle as O
-    from rustane_amd import hip_bridge as hb
+def cpu_threads():
+    """Host threads the CPU baselines use: this process's CPU share. A GPU box
+    allots each GPU a share of its host (OMP_NUM_THREADS, 16 per GPU there);
+    elsewhere every CPU this process may run on."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return min(share, avail) if share > 0 else avail
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _threads_limited():
     try:
         from threadpoolctl import threadpool_limits
     except ImportError:  # pragma: no cover
-        threadpool_limits = None
-    cores = min(16, os.cpu_count() or 1)
-    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
+        return None
+    return threadpool_limits(limits=cpu_threads())
+
+
+def _oracle_layer(cfg):
+    import oracle as O
+    from rustane_amd import hip_bridge as hb
+    d, q, kv, h = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden
+    n = lambda tid, cnt: hb.synth_normal(SEED, tid, cnt, STD)
+    return O.LayerW(wq=n(0, d * q), wk=n(1, d * kv), wv=n(2, d * kv), wo=n(3, q * d), w1=n(4, d * h),
+                    w3=n(5, d * h), w2=n(6, d * h), gamma1=np.ones(d, np.float32),
+                    gamma2=np.ones(d, np.float32))
+
+
+_CPU_SAMPLES = {}
+
+
+def cpu_forward_sample(cfg, B, S, full_below_layers=9):
+    """fp32 oracle forward of one sequence of S tokens on the host (the
+    reference has no batch dimension: B sequences take B times as long).
+    Models of up to `full_below_layers` layers run whole; deeper ones run one
+    layer plus the head (final norm, logits, CE) and are scaled to nlayers x
+    layer + head. Best of 2. Returns (seconds per B-sequence forward, note)."""
+    key = (cfg.dim, cfg.hidden, cfg.nlayers, cfg.heads, cfg.vocab, S)
+    if key in _CPU_SAMPLES:
+        t_seq, note = _CPU_SAMPLES[key]
+        return B * t_seq, note
+    import oracle as O
+    from rustane_amd import hip_bridge as hb
+    oc = O.Config.of(cfg)
+    d = cfg.dim
+    lw = _oracle_layer(cfg)
+    E = hb.synth_normal(SEED, hb.HB_SYNTH_EMBED_ID, cfg.vocab * d, STD)
+    tok = hb.synth_tokens(42, 0, cfg.vocab, S + 1)
+    x0 = O.mtrans(O.embedding_forward(E, d, tok[:-1]), S, d)
+    rope = O.rope_table(S, cfg.hd)
+    whole = cfg.nlayers < full_below_layers
+    lt, ht = [], []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        x = x0
+        for _l in range(cfg.nlayers if whole else 1):
+            x, _ = O.layer_forward(oc, lw, x, S, rope)
+        lt.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        xf, _ = O.rmsnorm_channel_first(x, np.ones(d, np.float32), d, S)
+        logits = O.sgemm_at(O.mtrans(xf, d, S), S, d, E, cfg.vocab, np.zeros(S * cfg.vocab, np.float32))
+        O.cross_entropy_batch(logits, tok[1:], cfg.vocab)
+        ht.append(time.perf_counter() - t0)
+    if whole:
+        t_seq = min(lt) + min(ht)
+        note = f"whole forward {t_seq:.2f} s"
+    else:
+        t_seq = cfg.nlayers * min(lt) + min(ht)
+        note = f"{cfg.nlayers} x {min(lt)*1e3:.0f} ms (1 layer timed) + {min(ht)*1e3:.0f} ms head = {t_seq:.2f} s"
+    _CPU_SAMPLES[key] = (t_seq, note)
+    return B * t_seq, note
+
+
+def cpu_baseline(cfg, S):
+    """Headline CPU baseline: the fp32 oracle's 7B-shape forward at B=1 on this
+    host's CPU share (one layer + the head timed, scaled to 32 layers)."""
+    ctx = _threads_limited()
     try:
-        oc = O.Config.of(cfg)
-        d, q, kv, h = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden
-        n = lambda tid, cnt: hb.synth_normal(SEED, tid, cnt, STD)
-        lw = O.LayerW(wq=n(0, d * q), wk=n(1, d * kv), wv=n(2, d * kv), wo=n(3, q * d), w1=n(4, d * h),
-                      w3=n(5, d * h), w2=n(6, d * h), gamma1=np.ones(d, np.float32),
-                      gamma2=np.ones(d, np.float32))
-        E = n(hb.HB_SYNTH_EMBED_ID, cfg.vocab * d)
-        tok = hb.synth_tokens(42, 0, cfg.vocab, S + 1)
-        x = O.mtrans(O.embedding_forward(E, d, tok[:-1]), S, d)
-        rope = O.rope_table(S, cfg.hd)
-        lt, ht = [], []
-        for _ in range(2):
-            t0 = time.perf_counter()
-            xl, _ = O.layer_forward(oc, lw, x, S, rope)
-            lt.append(time.perf_counter() - t0)
-            t0 = time.perf_counter()
-            xf, _ = O.rmsnorm_channel_first(xl, np.ones(d, np.float32), d, S)
-            logits = O.sgemm_at(O.mtrans(xf, d, S), S, d, E, cfg.vocab, np.zeros(S * cfg.vocab, np.float32))
-            O.cross_entropy_batch(logits, tok[1:], cfg.vocab)
-            ht.append(time.perf_counter() - t0)
-        t_full = cfg.nlayers * min(lt) + min(ht)
-        res = {"value": round(S / t_full, 2), "unit": "tok/s", "cores": cores, "kind": "port",
-               "sample": f"fp32 numpy oracle: 1 of {cfg.nlayers} layers + final norm/logits/CE of the "
-                         f"7B-shape forward at B=1 S={S} (best of 2); full forward = "
-                         f"{cfg.nlayers} x {min(lt)*1e3:.0f} ms + {min(ht)*1e3:.0f} ms = {t_full:.2f} s"}
+        t, note = cpu_forward_sample(cfg, 1, S)
+        res = {"value": round(S / t, 2), "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
+               "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
+               "sample": f"fp32 numpy oracle, 7B-shape forward at B=1 S={S}: {note} (best of 2)"}
         log(f"[bench] cpu baseline: {res}")
         return res
     finally:
-        if ctx is not None:
-            ctx.unregister() if hasattr(ctx, "unregister") else None
+        if ctx is not None and hasattr(ctx, "unregister"):
+            ctx.unregister()
+
+
+def cpu_baseline_decode(cfg, ctx_len=2048):
+    """fp32 oracle decode step (DecodeOracle.step) of the 7B shape at batch 1
+    and position ctx_len on the host: one step through a 1-layer and a
+    2-layer model with a filled K/V cache gives the per-layer and the head
+    cost; a 32-layer step is head + 32 x layer. Median of 3 steps each."""
+    import dataclasses
+
+    import oracle as O
+    from rustane_amd import hip_bridge as hb
+    lim = _threads_limited()
+    try:
+        lw = _oracle_layer(cfg)
+        E = hb.synth_normal(SEED, hb.HB_SYNTH_EMBED_ID, cfg.vocab * cfg.dim, STD)
+        times = {}
+        for L in (1, 2):
+            oc = dataclasses.replace(O.Config.of(cfg), nlayers=L, seq=ctx_len + 8)
+            w = O.ModelW(embed=E, layers=[lw] * L, gamma_final=np.ones(cfg.dim, np.float32))
+            dec = O.DecodeOracle(oc, w, ctx_max=ctx_len + 8)
+            rng = np.random.default_rng(L)
+            dec.k[:] = rng.standard_normal(dec.k.shape, dtype=np.float32)
+            dec.v[:] = rng.standard_normal(dec.v.shape, dtype=np.float32)
+            dec.pos = ctx_len
+            ts = []
+            for i in range(3):
+                t0 = time.perf_counter()
+                dec.step(int(i))
+                ts.append(time.perf_counter() - t0)
+            times[L] = sorted(ts)[1]
+        layer = max(times[2] - times[1], 1e-6)
+        head = max(times[1] - layer, 0.0)
+        step = head + cfg.nlayers * layer
+        res = {"value": round(1.0 / step, 3), "unit": "tok/s", "ms_per_step": round(step * 1e3, 1),
+               "cores": cpu_threads(), "kind": "port", "cpu_model": cpu_model(),
+               "sample": f"fp32 numpy DecodeOracle.step at position {ctx_len}, B=1: {cfg.nlayers} x "
+                         f"{layer*1e3:.1f} ms per layer + {head*1e3:.1f} ms embedding/head (median of 3 "
+                         f"steps of 1- and 2-layer models with a filled K/V cache)"}
+        log(f"[bench] cpu baseline (decode): {res}")
+        return res
+    finally:
+        if lim is not None and hasattr(lim, "unregister"):
+            lim.unregister()
+
+
+def bench_prefill_configs(k7, cfg7, stream, cpu=True):
+    """Prefill forwards (embedding .. per-position CE) of the other workloads:
+    7B-shape at seq 2048 (batch 1 and 8, on the headline model), 600M-shape
+    (1536d/4096h/20L, 12x128) at batch 1 and 8 and 5B-shape (2560d/6912h/60L,
+    20x128) at batch 4, both seq 512, each on seeded N(0, 0.02) device
+    weights; wall time over repeated hb_forward_device calls."""
+    import torch
+    from rustane_amd import hip_bridge as hb
+    from rustane_amd.engine import CompiledKernels, ModelConfig
+
+    def run(k, cfg, B, S, reps):
+        tok = hb.synth_tokens(42, 500 + B, cfg.vocab, B * (S + 1)).reshape(B, S + 1)
+        dt = torch.from_numpy(tok[:, :-1].astype(np.int32).copy()).cuda()
+        dg = torch.from_numpy(tok[:, 1:].astype(np.int32).copy()).cuda()
+        dl = torch.empty(B * S, device="cuda")
+        dm = torch.empty(1, device="cuda")
+        k.model.reserve(B, S)
+        f = lambda: hb.call("hb_forward_device", k.model.handle, dt.data_ptr(), dg.data_ptr(), B, S,
+                            dl.data_ptr(), None, dm.data_ptr())
+        f()
+        f()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            f()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        k.ctx.synchronize()
+        fl = fwd_flops(cfg, B, S)
+        r = {"ms_per_forward": round(ms, 3), "tok_per_s": round(B * S / ms * 1e3, 1),
+             "tflop_per_s": round(fl / ms / 1e9, 1), "mfma_frac": round(fl / (ms / 1e3) / MFMA_PEAK_F16, 4),
+             "tflop_per_forward": round(fl / 1e12, 3), "loss": round(float(dm.cpu()[0]), 5)}
+        if cpu:
+            lim = _threads_limited()
+            try:
+                t, note = cpu_forward_sample(cfg, B, S)
+            finally:
+                if lim is not None and hasattr(lim, "unregister"):
+                    lim.unregister()
+            r["cpu_baseline"] = {"value": round(B * S / t, 2), "unit": "tok/s", "cores": cpu_threads(),
+                                 "kind": "port", "sample": f"fp32 numpy oracle, one sequence: {note}; x{B}"}
+        return r
+
+    out = {}
+    for B in (1, 8):
+        out[f"7b_s2048_b{B}"] = run(k7, cfg7, B, 2048, 3 if B == 1 else 2)
+        log(f"[bench] prefill 7B S=2048 B={B}: {out[f'7b_s2048_b{B}']}")
+    for name, mk, batches in (("600m", ModelConfig.llama_600m, (1, 8)), ("5b", ModelConfig.llama_5b, (4,))):
+        cfg = mk()
+        k = CompiledKernels.compile(cfg)
+        k.ctx.set_stream(stream.cuda_stream)
+        try:
+            k.init_synthetic(SEED, STD)
+            for B in batches:
+                out[f"{name}_s512_b{B}"] = run(k, cfg, B, 512, 10 if B == 1 else 5)
+                log(f"[bench] prefill {name} S=512 B={B}: {out[f'{name}_s512_b{B}']}")
+        finally:
+            torch.cuda.synchronize()
+            k.model.close()
+            k.ctx.close()
+    return out
 
 
 def cpu_baseline_train(cfg, S):
@@ -539,7 +712,7 @@ def cpu_baseline_train(cfg, S):
         from threadpoolctl import threadpool_limits
     except ImportError:  # pragma: no cover
         threadpool_limits = None
-    cores = min(16, os.cpu_count() or 1)
+    cores = cpu_threads()
     ctx = threadpool_limits(limits=cores) if threadpool_limits else None
     try:
         oc = O.Config.of(cfg)

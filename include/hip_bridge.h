@@ -378,6 +378,42 @@ int hb_forward_backward_device(hb_model* m, hb_opt* opt, const uint32_t* d_token
                                const uint32_t* d_targets, int B, int S, float loss_scale,
                                float* d_loss, float* d_mean);
 
+/* The reference's forward/backward pair, split across two calls.
+ *
+ * ForwardResult (full_model.rs:73-81): host views that forward() returns
+ * besides the loss and the per-layer caches, each nullable, B sequences one
+ * after another in the reference's per-sequence layouts:
+ *   dlogits       [B*S*vocab]  (softmax - onehot(target)) / S, the gradient
+ *                              of the sequence's mean CE (cross_entropy.rs:58-96)
+ *   x_final       [B][dim][S]  channel-first, after the final RMSNorm
+ *   x_prenorm     [B][dim][S]  channel-first, before it
+ *   rms_inv_final [B*S]
+ *   logits_capped [B*S*vocab]  tanh(logits / softcap), written only when the
+ *                              model's softcap is > 0 (the reference leaves it
+ *                              empty otherwise) */
+typedef struct hb_forward_result {
+  float* dlogits;
+  float* x_final;
+  float* x_prenorm;
+  float* rms_inv_final;
+  float* logits_capped;
+} hb_forward_result;
+
+/* forward (full_model.rs:345-410) for training: the forward of
+ * hb_forward_backward on B sequences of S tokens (host ids, synchronous),
+ * keeping every layer's activations on the device -- ForwardResult.caches --
+ * for the next hb_train_backward on this model. Per-position losses
+ * (nullable, [B*S]), their mean (nullable) and the views in *out (nullable)
+ * are returned. Any other training call on the model drops the kept caches. */
+int hb_train_forward(hb_model* m, const uint32_t* h_tokens, const uint32_t* h_targets, int B, int S,
+                     float* h_per_pos_loss, float* h_mean_loss, const hb_forward_result* out);
+/* backward (full_model.rs:414-483) from the caches of the last
+ * hb_train_forward: ADDS the gradients of loss_scale * (mean CE of each
+ * sequence) to opt's gradient arena, as hb_forward_backward does.
+ * HB_E_STATE without a kept forward (each forward serves one backward).
+ * Synchronous. */
+int hb_train_backward(hb_model* m, hb_opt* opt, float loss_scale);
+
 /* ---- RSTK checkpoints (bin/train.rs:165-202) ------------------------------ */
 
 /* Header of the reference's checkpoint file: "RSTK", then little-endian u32

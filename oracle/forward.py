@@ -29,7 +29,7 @@ __all__ = [
     "rmsnorm_channel_first", "rope_table", "rope_apply_cf", "rope_backward_cf", "causal_mask",
     "sdpa_fwd", "dyn_matmul", "vsma", "silu_gate", "ffn_fused", "layer_forward",
     "cross_entropy_forward", "cross_entropy_batch", "model_forward", "forward_batch",
-    "DecodeOracle", "sgemm_at",
+    "DecodeOracle", "sgemm_at", "softcap_forward",
 ]
 
 
@@ -314,6 +314,16 @@ def layer_forward(cfg: Config, lw: LayerW, x_cf: np.ndarray, seq: int, rope=None
     return f["x_next"].reshape(-1), taps
 
 
+def softcap_forward(logits: np.ndarray, softcap: float) -> np.ndarray:
+    """full_model.rs:234-239 / 388-393, in the reference's operation order:
+    logits *= 1/c (vDSP sscal by the f32 reciprocal), t = tanh(logits),
+    logits = t * c (vsmul). Dividing by c instead rounds differently whenever
+    1/c is not a power of two."""
+    c = F32(softcap)
+    t = np.tanh((np.asarray(logits, F32) * (F32(1.0) / c)).astype(F32)).astype(F32)
+    return (t * c).astype(F32)
+
+
 def model_forward(cfg: Config, w: ModelW, tokens, targets=None, softcap: float = 0.0,
                   want_logits: bool = True, keep_taps=False):
     """full_model.rs:345-410 / 717-767 for one sequence: embedding + mtrans (201-202) ->
@@ -337,7 +347,7 @@ def model_forward(cfg: Config, w: ModelW, tokens, targets=None, softcap: float =
     x_final_row = mtrans(x_final, d, seq)
     logits = sgemm_at(x_final_row, seq, d, w.embed, V, np.zeros(seq * V, F32))
     if softcap > 0.0:
-        logits = (F32(softcap) * np.tanh(logits / F32(softcap))).astype(F32)
+        logits = softcap_forward(logits, softcap)
     out = {"logits": logits if want_logits else None, "x_final_cf": x_final, "taps": taps,
            "x_prenorm_cf": x}
     if targets is not None:
@@ -426,6 +436,6 @@ class DecodeOracle:
         xf, _ = rmsnorm_channel_first(x, w.gamma_final, d, 1, cfg.norm_eps)
         logits = sgemm_at(xf.reshape(1, d), 1, d, w.embed, cfg.vocab, np.zeros(cfg.vocab, F32))
         if cfg.softcap > 0:
-            logits = (F32(cfg.softcap) * np.tanh(logits / F32(cfg.softcap))).astype(F32)
+            logits = softcap_forward(logits, cfg.softcap)
         self.pos += 1
         return logits.reshape(-1)

@@ -150,6 +150,69 @@ hipError_t ce_backward(const float* logits, const uint32_t* tgt, int T, int V, i
   return hipGetLastError();
 }
 
+// ---- ForwardResult views (full_model.rs:73-81) -------------------------------------
+// dlogits as forward() returns them (cpu/cross_entropy.rs:58-96, scaled by
+// 1/seq): e = exp(z - max), d = e * (1/sum e), d[y] -= 1, d *= inv_seq; and
+// logits_capped = tanh(raw / softcap) (full_model.rs:388-393), recovered from
+// the stored capped logits z = softcap * t as z * (1/softcap). fp32 [T][V].
+__global__ __launch_bounds__(256) void ce_grad_views_kernel(const float* __restrict__ logits,
+                                                            const uint32_t* __restrict__ tgt, int V,
+                                                            float inv_seq, float softcap,
+                                                            float* __restrict__ dl,
+                                                            float* __restrict__ tcap) {
+  __shared__ float red[4];
+  const int t = blockIdx.x;
+  const float* z = logits + (size_t)t * V;
+  float m = -INFINITY;
+  for (int v = threadIdx.x; v < V; v += 256) m = fmaxf(m, z[v]);
+  m = block_max<4>(m, red);
+  float se = 0.f;
+  for (int v = threadIdx.x; v < V; v += 256) se += expf(z[v] - m);
+  se = block_sum<4>(se, red);
+  const float inv = 1.0f / se, ic = softcap > 0.f ? 1.0f / softcap : 0.f;
+  const uint32_t y = tgt[t];
+  for (int v = threadIdx.x; v < V; v += 256) {
+    const float zv = z[v];
+    if (dl) dl[(size_t)t * V + v] = (expf(zv - m) * inv - ((uint32_t)v == y ? 1.0f : 0.0f)) * inv_seq;
+    if (tcap) tcap[(size_t)t * V + v] = zv * ic;
+  }
+}
+
+hipError_t ce_grad_views(const float* logits, const uint32_t* tgt, int T, int V, float inv_seq,
+                         float softcap, float* dl, float* tcap, hipStream_t st) {
+  if (T < 0 || V < 1) return hipErrorInvalidValue;
+  if (T == 0 || (!dl && !tcap)) return hipSuccess;
+  hipLaunchKernelGGL(ce_grad_views_kernel, dim3(T), dim3(256), 0, st, logits, tgt, V, inv_seq,
+                     softcap > 0.f ? softcap : 0.f, dl, tcap);
+  return hipGetLastError();
+}
+
+// x_prenorm and x_final = x * rinv * gamma (cpu/rmsnorm.rs:149-183 order) for
+// token t = b*S + s, written channel-first per sequence: [b][c][s].
+__global__ __launch_bounds__(256) void final_norm_views_kernel(const float* __restrict__ x,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ rinv, int S,
+                                                               int d, float* __restrict__ pre,
+                                                               float* __restrict__ fin) {
+  const int t = blockIdx.x, b = t / S, s = t - b * S;
+  const float r = rinv[t];
+  for (int c = threadIdx.x; c < d; c += 256) {
+    const float v = x[(size_t)t * d + c];
+    const size_t o = ((size_t)b * d + c) * S + s;
+    if (pre) pre[o] = v;
+    if (fin) fin[o] = v * r * gamma[c];
+  }
+}
+
+hipError_t final_norm_views(const float* x, const float* gamma, const float* rinv, int B, int S, int d,
+                            float* pre, float* fin, hipStream_t st) {
+  if (B < 0 || S < 1 || d < 1) return hipErrorInvalidValue;
+  if (B == 0 || (!pre && !fin)) return hipSuccess;
+  hipLaunchKernelGGL(final_norm_views_kernel, dim3(B * S), dim3(256), 0, st, x, gamma, rinv, S, d, pre,
+                     fin);
+  return hipGetLastError();
+}
+
 // ---- RMSNorm backward -----------------------------------------------------------
 // cpu/rmsnorm.rs:190-236 per row t, with r = 1/sqrt(mean(x^2) + eps)
 // recomputed from x as the forward computes it:

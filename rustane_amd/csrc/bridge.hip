@@ -166,12 +166,19 @@ struct TrainState {
   f16 *dqkv = nullptr, *dqkvT = nullptr, *dl = nullptr, *dlT = nullptr;
   f16 *dA = nullptr, *dAT = nullptr, *qT = nullptr, *kT = nullptr, *vt = nullptr;
   f16 *P = nullptr, *PT = nullptr, *dS = nullptr, *dST = nullptr;
+  // hb_train_forward left its activations for hb_train_backward (the
+  // reference's ForwardResult.caches); any other training call clears it.
+  bool kept = false;
+  // device staging of ForwardResult's host views, grown on demand
+  float* views = nullptr;
+  size_t views_floats = 0;
 };
 
 void train_free(TrainState* t) {
   if (!t) return;
   if (t->wtbase) (void)hipFree(t->wtbase);
   if (t->abase) (void)hipFree(t->abase);
+  if (t->views) (void)hipFree(t->views);
   delete t;
 }
 
@@ -329,6 +336,20 @@ int ensure_workspace(hb_model* m, long T, long Tpad) {
 }
 
 int S_pad_of(int S) { return (S + 31) & ~31; }
+
+// The forward kernels index activations with 32-bit element offsets (row x K
+// in the GEMM loads, row x vocab in the logits and loss kernels, token x
+// q_dim in attention) and launch one grid layer per sequence. Rejects B x S
+// token counts whose largest activation, rounded up to the GEMM's 64-row
+// tile, would not fit, before anything is allocated or launched.
+int check_token_count(const hb_model_config& c, long B, long S) {
+  const long T = B * S, Tp = B * S_pad_of((int)std::min<long>(S, 1L << 30));
+  const long widest = std::max({(long)c.vocab, 2L * c.hidden, (long)c.q_dim + 2L * c.kv_dim, (long)c.dim});
+  if (B > 65535 || round64(T) * widest >= (1L << 31) || round64(Tp) * (long)c.q_dim >= (1L << 31))
+    return fail(HB_E_INVALID, "B=%ld S=%ld: %ld tokens x %ld features exceeds the 2^31-element activation limit",
+                B, S, T, widest);
+  return HB_OK;
+}
 
 // Scratch for a residual GEMM of this shape: grown on demand (outside any
 // capture: prefill is never captured), empty when the shape does not split.
@@ -1642,8 +1663,9 @@ extern "C" int hb_validate(hb_model* m, const hb_tokens* val, const int32_t* tok
   if (val->n < (uint64_t)S + 2)
     return fail(HB_E_INVALID, "%llu tokens: need at least seq + 2 = %d", (unsigned long long)val->n, S + 2);
   if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
-  DeviceGuard g(m->ctx->device);
   const int B = std::min(batch, steps);
+  TRY(check_token_count(c, B, S));
+  DeviceGuard g(m->ctx->device);
   TRY(ensure_workspace(m, (long)B * S, (long)B * S_pad_of(S)));
   Workspace& w = m->ws;
   hipStream_t st = m->ctx->stream();
@@ -1718,6 +1740,7 @@ extern "C" int hb_synth_tokens(uint64_t seed, uint64_t stream, uint32_t vocab, u
 extern "C" int hb_model_reserve(hb_model* m, int B, int S) {
   HB_INJECT_CHECK();
   if (!m || B <= 0 || S <= 0) return fail(HB_E_INVALID, "bad argument");
+  TRY(check_token_count(m->cfg, B, S));
   DeviceGuard g(m->ctx->device);
   return ensure_workspace(m, (long)B * S, (long)B * S_pad_of(S));
 }
@@ -1726,6 +1749,7 @@ static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint
                                int B, int S, float* d_loss, float* d_logits, float* d_mean) {
   const hb_model_config& c = m->cfg;
   if (B <= 0 || S <= 0 || S > c.seq) return fail(HB_E_INVALID, "need B >= 1 and 1 <= S <= seq (%d)", c.seq);
+  TRY(check_token_count(c, B, S));
   if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
   if (!d_tokens) return fail(HB_E_INVALID, "null tokens");
   const long T = (long)B * S, Tp = (long)B * S_pad_of(S);
@@ -1768,6 +1792,7 @@ extern "C" int hb_forward(hb_model* m, const uint32_t* tokens, const uint32_t* t
   HB_INJECT_CHECK();
   if (!m || !tokens) return fail(HB_E_INVALID, "null argument");
   if (B <= 0 || S <= 0 || S > m->cfg.seq) return fail(HB_E_INVALID, "need B >= 1 and 1 <= S <= seq (%d)", m->cfg.seq);
+  TRY(check_token_count(m->cfg, B, S));
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
   const size_t T = (size_t)B * S;
@@ -1795,6 +1820,7 @@ extern "C" int hb_op_rmsnorm(hb_ctx* ctx, const float* x, const float* gamma, in
   HB_INJECT_CHECK();
   if (!ctx || !x || !gamma || !out) return fail(HB_E_INVALID, "null argument");
   if (T < 0 || dim <= 0 || dim % 4) return fail(HB_E_INVALID, "need T >= 0 and dim %% 4 == 0");
+  if ((long)T * dim >= (1L << 31)) return fail(HB_E_INVALID, "T x dim exceeds 2^31 elements");
   DeviceGuard g(ctx->device);
   HIP_TRY(rmsnorm(x, dim, gamma, T, dim, eps, (f16*)out, rms_inv, ctx->stream()));
   return HB_OK;
@@ -1804,6 +1830,7 @@ extern "C" int hb_op_embedding(hb_model* m, const uint32_t* tok, int T, float* x
   HB_INJECT_CHECK();
   if (!m || !tok || !x) return fail(HB_E_INVALID, "null argument");
   if (!m->embed_uploaded) return fail(HB_E_STATE, "embedding not uploaded");
+  if (T < 0 || (long)T * m->cfg.dim >= (1L << 31)) return fail(HB_E_INVALID, "need 0 <= T x dim < 2^31");
   DeviceGuard g(m->ctx->device);
   HIP_TRY(embedding(m->embed, tok, T, m->cfg.dim, m->cfg.vocab, x, m->ctx->d_err, m->ctx->stream()));
   return HB_OK;
@@ -1816,6 +1843,7 @@ extern "C" int hb_op_sdpa_fwd(hb_model* m, int layer, const void* xnorm, int B, 
   if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
     return fail(HB_E_STATE, "layer %d not available", layer);
   if (B <= 0 || S <= 0 || S > m->cfg.seq) return fail(HB_E_INVALID, "bad B/S");
+  TRY(check_token_count(m->cfg, B, S));
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
   const int T = B * S, Sp = S_pad_of(S);
@@ -1845,6 +1873,7 @@ extern "C" int hb_op_wo_fwd(hb_model* m, int layer, const void* attn, const floa
   if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
     return fail(HB_E_STATE, "layer %d not available", layer);
   if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  TRY(check_token_count(m->cfg, 1, T));
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
   GemmScratch so;
@@ -1861,6 +1890,7 @@ extern "C" int hb_op_ffn_fused(hb_model* m, int layer, const void* x2norm, const
   if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
     return fail(HB_E_STATE, "layer %d not available", layer);
   if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  TRY(check_token_count(m->cfg, 1, T));
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
   f16* gate = (f16*)gate_out;
@@ -1884,6 +1914,7 @@ extern "C" int hb_op_ffn_up(hb_model* m, int layer, const void* x2norm, int T, v
   if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
     return fail(HB_E_STATE, "layer %d not available", layer);
   if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  TRY(check_token_count(m->cfg, 1, T));
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
   HIP_TRY(gemm_swiglu(m->layers[layer].w13, (const f16*)x2norm, 2 * c.hidden, T, c.dim,
@@ -1898,6 +1929,7 @@ extern "C" int hb_op_logits_ce(hb_model* m, const void* xf, const uint32_t* targ
   if (!logits) return fail(HB_E_INVALID, "logits buffer required");
   if (!m->embed_uploaded) return fail(HB_E_STATE, "embedding not uploaded");
   if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  TRY(check_token_count(m->cfg, 1, T));
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
   hipStream_t st = m->ctx->stream();
@@ -1911,6 +1943,8 @@ extern "C" int hb_op_gemm_nt(hb_ctx* ctx, const void* a, const void* b, float* c
   HB_INJECT_CHECK();
   if (!ctx || !a || !b || !cmat) return fail(HB_E_INVALID, "null argument");
   if (M <= 0 || N <= 0 || K <= 0 || K % 64 || N % 4) return fail(HB_E_INVALID, "need K %% 64 == 0 and N %% 4 == 0");
+  if (round64(std::max(M, N)) * std::max<long>(K, std::min(M, N)) >= (1L << 31))
+    return fail(HB_E_INVALID, "M=%d N=%d K=%d exceeds the 2^31-element operand limit", M, N, K);
   DeviceGuard g(ctx->device);
   HIP_TRY(gemm_store((const f16*)b, (const f16*)a, N, M, K, cmat, ctx->stream()));
   return HB_OK;
@@ -2153,6 +2187,7 @@ extern "C" int hb_prefill(hb_model* m, hb_kv* kv, const uint32_t* tokens, int S,
   if (kv->model != m) return fail(HB_E_INVALID, "kv cache belongs to another model");
   if (kv->len != 0) return fail(HB_E_STATE, "prefill needs an empty cache (length %d)", kv->len);
   if (S < 1 || S > kv->ctx_max) return fail(HB_E_INVALID, "S must be in [1, ctx_max]");
+  TRY(check_token_count(m->cfg, kv->B, S));
   if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
   DeviceGuard g(m->ctx->device);
   const hb_model_config& c = m->cfg;
@@ -2439,7 +2474,7 @@ int attention_backward(hb_model* m, const LayerAct& A, int B, int S) {
 // backward_ws (full_model.rs:250-331) with layer::backward_into
 // (layer.rs:1606-1858) per layer, accumulating into the optimizer's fp32
 // gradient arena (packed order, element for element like the fp16 weights).
-int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
+int train_backward_impl(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
   const hb_model_config& c = m->cfg;
   TrainState* ts = m->train;
   hipStream_t st = m->ctx->stream();
@@ -2537,18 +2572,40 @@ int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
   HIP_TRY(embedding_backward(ts->dy, ts->tok, T, d, c.vocab, g + o->embed_off, st));
   HIP_TRY(grad_sumsq(g + o->embed_off, (size_t)c.vocab * d, o->sq_embed, st));
   o->sq_n = ns;
-  o->sq_ready = true;
-  o->grads_zero = false;
-  o->lazy_zero = false;  // every element was stored above
   return HB_OK;
 }
 
-// Checks the call and brings the transposed weights and the (B, S) buffers up to date.
-int train_prepare(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
-  const hb_model_config& c = m->cfg;
-  if (!o || o->model != m) return fail(HB_E_INVALID, "optimizer belongs to another model");
-  if (B <= 0 || S <= 0 || S > c.seq) return fail(HB_E_INVALID, "need B >= 1 and 1 <= S <= seq (%d)", c.seq);
+// Runs the backward and settles the arena's state flags. The per-tile sums of
+// squares stand for the arena only while nobody else can write it: once
+// hb_opt_grad_arena has handed out the raw pointer, a caller's later write
+// would be missing from them, so the norm then takes the full pass. A
+// backward that fails part way leaves a partly written arena: one that held
+// zeros is marked for clearing by its next consumer, so no stale half-result
+// is read as a gradient.
+int train_backward(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
+  const bool was_zero = o->grads_zero;
+  o->sq_ready = false;
+  const int r = train_backward_impl(m, o, B, S, loss_scale);
+  if (r != HB_OK) {
+    o->grads_zero = o->lazy_zero = was_zero;
+    return r;
+  }
+  o->sq_ready = !o->arena_exposed;
+  o->grads_zero = false;
+  o->lazy_zero = false;  // every element was stored
+  return HB_OK;
+}
+
+int check_loss_scale(float loss_scale) {
   if (!(loss_scale > 0.f) || !std::isfinite(loss_scale)) return fail(HB_E_INVALID, "loss_scale must be positive");
+  return HB_OK;
+}
+
+// Checks a training forward of (B, S) and brings the transposed weights and
+// the (B, S) buffers up to date.
+int train_prepare_model(hb_model* m, int B, int S) {
+  const hb_model_config& c = m->cfg;
+  if (B <= 0 || S <= 0 || S > c.seq) return fail(HB_E_INVALID, "need B >= 1 and 1 <= S <= seq (%d)", c.seq);
   if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
   if (c.dim > 8192) return fail(HB_E_CONFIG, "training needs dim <= 8192");
   const long T = (long)B * S, Sp = round64(S);
@@ -2556,8 +2613,61 @@ int train_prepare(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
       (long)c.heads / c.kv_heads * Sp * Sp >= (1L << 31) || (long)B * c.kv_heads > 65535)
     return fail(HB_E_INVALID, "B=%d S=%d too large for one training call", B, S);
   if (!m->train) m->train = new TrainState();
+  m->train->kept = false;
   TRY(train_weights(m));
   TRY(train_buffers(m, B, S));
+  return HB_OK;
+}
+
+int train_prepare(hb_model* m, hb_opt* o, int B, int S, float loss_scale) {
+  if (!o || o->model != m) return fail(HB_E_INVALID, "optimizer belongs to another model");
+  TRY(check_loss_scale(loss_scale));
+  return train_prepare_model(m, B, S);
+}
+
+// ForwardResult's host views (full_model.rs:73-81) of the training forward
+// just run, copied out in the reference's layouts.
+int train_forward_views(hb_model* m, int B, int S, const hb_forward_result* r) {
+  const hb_model_config& c = m->cfg;
+  TrainState* ts = m->train;
+  hipStream_t st = m->ctx->stream();
+  const size_t T = (size_t)B * S, TV = T * c.vocab, Td = T * c.dim;
+  const bool want_cap = r->logits_capped && c.softcap > 0.f;
+  const size_t need = (r->dlogits ? TV : 0) + (want_cap ? TV : 0) + (r->x_prenorm ? Td : 0) +
+                      (r->x_final ? Td : 0) + T;
+  if (need > ts->views_floats) {
+    HIP_TRY(hipStreamSynchronize(st));
+    if (ts->views) HIP_TRY(hipFree(ts->views));
+    ts->views = nullptr;
+    ts->views_floats = 0;
+    HIP_TRY(hipMalloc(&ts->views, need * 4));
+    ts->views_floats = need;
+  }
+  float* p = ts->views;
+  auto take = [&](bool want, size_t n) {
+    float* q = want ? p : nullptr;
+    p += want ? n : 0;
+    return q;
+  };
+  float* d_dl = take(r->dlogits != nullptr, TV);
+  float* d_cap = take(want_cap, TV);
+  float* d_pre = take(r->x_prenorm != nullptr, Td);
+  float* d_fin = take(r->x_final != nullptr, Td);
+  float* d_rinv = take(true, T);
+  if (d_dl || d_cap)
+    HIP_TRY(ce_grad_views(ts->logits, ts->tgt, (int)T, c.vocab, 1.0f / (float)S, c.softcap, d_dl, d_cap, st));
+  // the forward's own rms_inv (same kernel, same reduction order)
+  HIP_TRY(rmsnorm(ts->xL, c.dim, m->gamma_f, (int)T, c.dim, c.norm_eps, ts->xf, d_rinv, st));
+  if (d_pre || d_fin)
+    HIP_TRY(final_norm_views(ts->xL, m->gamma_f, d_rinv, B, S, c.dim, d_pre, d_fin, st));
+  auto down = [&](float* h, const float* d, size_t n) -> hipError_t {
+    return h && d ? hipMemcpyAsync(h, d, n * 4, hipMemcpyDeviceToHost, st) : hipSuccess;
+  };
+  HIP_TRY(down(r->dlogits, d_dl, TV));
+  HIP_TRY(down(r->logits_capped, d_cap, TV));
+  HIP_TRY(down(r->x_prenorm, d_pre, Td));
+  HIP_TRY(down(r->x_final, d_fin, Td));
+  HIP_TRY(down(r->rms_inv_final, d_rinv, T));
   return HB_OK;
 }
 
@@ -2580,6 +2690,46 @@ extern "C" int hb_forward_backward_device(hb_model* m, hb_opt* o, const uint32_t
   if (d_loss) HIP_TRY(hipMemcpyAsync(d_loss, ts->loss, T * 4, hipMemcpyDeviceToDevice, st));
   if (d_mean) HIP_TRY(hipMemcpyAsync(d_mean, ts->mean, 4, hipMemcpyDeviceToDevice, st));
   return HB_OK;
+}
+
+extern "C" int hb_train_forward(hb_model* m, const uint32_t* tokens, const uint32_t* targets, int B, int S,
+                                float* per_pos_loss, float* mean_loss, const hb_forward_result* out) {
+  HB_INJECT_CHECK();
+  if (!m || !tokens || !targets) return fail(HB_E_INVALID, "null argument");
+  DeviceGuard g(m->ctx->device);
+  TRY(train_prepare_model(m, B, S));
+  const size_t T = (size_t)B * S;
+  TRY(check_ids(tokens, T, m->cfg.vocab, "tokens"));
+  TRY(check_ids(targets, T, m->cfg.vocab, "targets"));
+  TrainState* ts = m->train;
+  hipStream_t st = m->ctx->stream();
+  HIP_TRY(hipMemcpyAsync(ts->tok, tokens, T * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(ts->tgt, targets, T * 4, hipMemcpyHostToDevice, st));
+  TRY(train_forward(m, B, S));
+  if (out) TRY(train_forward_views(m, B, S, out));
+  if (per_pos_loss) HIP_TRY(hipMemcpyAsync(per_pos_loss, ts->loss, T * 4, hipMemcpyDeviceToHost, st));
+  if (mean_loss) HIP_TRY(hipMemcpyAsync(mean_loss, ts->mean, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  TRY(check_err_word(m->ctx));
+  ts->kept = true;
+  return HB_OK;
+}
+
+extern "C" int hb_train_backward(hb_model* m, hb_opt* o, float loss_scale) {
+  HB_INJECT_CHECK();
+  if (!m || !o) return fail(HB_E_INVALID, "null argument");
+  if (o->model != m) return fail(HB_E_INVALID, "optimizer belongs to another model");
+  TRY(check_loss_scale(loss_scale));
+  TrainState* ts = m->train;
+  if (!ts || !ts->kept) return fail(HB_E_STATE, "no kept training forward (call hb_train_forward first)");
+  DeviceGuard g(m->ctx->device);
+  ts->kept = false;
+  // the weights may have been written since the forward: the backward uses
+  // the current ones, as the reference's backward takes `weights` afresh
+  TRY(train_weights(m));
+  TRY(train_backward(m, o, ts->B, ts->S, loss_scale));
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
+  return check_err_word(m->ctx);
 }
 
 extern "C" int hb_forward_backward(hb_model* m, hb_opt* o, const uint32_t* tokens,

@@ -216,6 +216,13 @@ hipError_t transpose_f16(const f16* src, int R, int C, int lds, size_t sbs, f16*
 // (nullable) [R][C] gets the same fp16 values row-major.
 hipError_t cast_transpose(const float* src, int R, int C, float scale, f16* rm, f16* dst, int ldd,
                           hipStream_t st);
+// ForwardResult's fp32 views: dlogits [T][V] = (softmax - onehot) * inv_seq
+// and logits_capped [T][V] = z / softcap (each nullable).
+hipError_t ce_grad_views(const float* logits, const uint32_t* tgt, int T, int V, float inv_seq,
+                         float softcap, float* dl, float* tcap, hipStream_t st);
+// x_prenorm / x_final (each nullable) channel-first [b][c][s] from x [B*S][d].
+hipError_t final_norm_views(const float* x, const float* gamma, const float* rinv, int B, int S, int d,
+                            float* pre, float* fin, hipStream_t st);
 // dl [T][Vp] fp16 = (softmax(logits) - onehot) * gs (* (1 - (z/softcap)^2)).
 hipError_t ce_backward(const float* logits, const uint32_t* tgt, int T, int V, int Vp, float gs,
                        float softcap, f16* dl, hipStream_t st);

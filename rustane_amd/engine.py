@@ -248,8 +248,10 @@ class CompiledKernels:
 
 
 @dataclass
-class ForwardResult:
-    """full_model.rs:73-81 (forward-only fields)."""
+class ForwardLogits:
+    """What an inference forward returns (forward_ws's loss with
+    forward_losses' per-position losses, full_model.rs:187-247 and 717-767,
+    plus the logits the reference keeps in ws.logits, full_model.rs:159,230)."""
     loss: float
     losses: np.ndarray
     logits: Optional[np.ndarray] = None
@@ -272,10 +274,71 @@ def _run(cfg, kernels, weights, tokens, targets, softcap, want_logits, batch=1):
     return float(mean[0]), losses, logits
 
 
-def forward(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights], tokens,
-            targets, softcap: float = 0.0, want_logits: bool = True, batch: int = 1) -> ForwardResult:
+def forward_logits(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights], tokens,
+                   targets, softcap: float = 0.0, want_logits: bool = True, batch: int = 1) -> ForwardLogits:
+    """Inference forward (hb_forward): mean loss, per-position losses and the logits."""
     loss, losses, logits = _run(cfg, kernels, weights, tokens, targets, softcap, want_logits, batch)
-    return ForwardResult(loss=loss, losses=losses, logits=logits)
+    return ForwardLogits(loss=loss, losses=losses, logits=logits)
+
+
+@dataclass
+class ForwardCaches:
+    """ForwardResult.caches (full_model.rs:75; layer.rs ForwardCache per layer):
+    every layer's activations, kept on the device by the training forward for
+    one backward of the same model. Only handles live here."""
+    kernels: "CompiledKernels"
+    batch: int
+    seq: int
+
+
+@dataclass
+class ForwardResult:
+    """full_model.rs:73-81: everything backward needs from forward. The
+    arrays are the reference's layouts for one sequence (dlogits [S*V],
+    x_final / x_prenorm [dim*S] channel-first, rms_inv_final [S],
+    logits_capped [S*V] or empty without softcap); with batch > 1 the
+    sequences follow one another."""
+    loss: float
+    caches: ForwardCaches
+    dlogits: np.ndarray
+    x_final: np.ndarray
+    x_prenorm: np.ndarray
+    rms_inv_final: np.ndarray
+    logits_capped: np.ndarray
+
+
+def forward(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights], tokens,
+            targets, softcap: float = 0.0, batch: int = 1) -> ForwardResult:
+    """full_model.rs:345-410 (hb_train_forward): embedding, layers, final norm,
+    logits, softcap, cross-entropy with its gradient; the per-layer caches stay
+    on the device for backward()."""
+    kernels.ensure_weights(weights)
+    kernels.set_softcap(softcap)
+    tok = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+    if tok.size % batch:
+        raise ValueError("token count not divisible by batch")
+    S = tok.size // batch
+    views = ["dlogits", "x_final", "x_prenorm", "rms_inv_final"] + (["logits_capped"] if softcap > 0 else [])
+    loss, _, v = kernels.model.train_forward(tok, targets, batch, S, views)
+    flat = (lambda a: a.reshape(-1)) if batch == 1 else (lambda a: a)
+    return ForwardResult(loss=loss, caches=ForwardCaches(kernels, batch, S), dlogits=v["dlogits"],
+                         x_final=flat(v["x_final"]), x_prenorm=flat(v["x_prenorm"]),
+                         rms_inv_final=v["rms_inv_final"],
+                         logits_capped=v.get("logits_capped", np.zeros(0, np.float32)))
+
+
+def backward(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights],
+             fwd: ForwardResult, tokens, softcap: float, loss_scale: float, grads: "ModelOptState",
+             ws=None) -> None:
+    """full_model.rs:414-483 from fwd.caches (hb_train_backward): the
+    gradients of loss_scale * mean CE are ADDED to grads (the device gradient
+    arena of a ModelOptState). `tokens` and `softcap` are the forward's (kept
+    on the device with the caches); `ws` is accepted for the reference's
+    signature, the workspace lives on the device."""
+    if fwd.caches.kernels is not kernels or grads.kernels is not kernels:
+        raise ValueError("fwd and grads must belong to these kernels")
+    kernels.ensure_weights(weights)
+    grads.opt.backward(loss_scale)
 
 
 def forward_ws(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights], tokens,

@@ -87,6 +87,12 @@ class hb_train_config(C.Structure):
     ]
 
 
+class hb_forward_result(C.Structure):
+    """ForwardResult's host views (full_model.rs:73-81); each pointer nullable."""
+    _fields_ = [(n, C.c_void_p) for n in ("dlogits", "x_final", "x_prenorm", "rms_inv_final",
+                                          "logits_capped")]
+
+
 class hb_rstk_header(C.Structure):
     """RSTK checkpoint header (bin/train.rs:175-183) after the magic."""
     _fields_ = [(n, C.c_uint32) for n in ("version", "step", "dim", "nlayers", "vocab", "seq")]
@@ -158,6 +164,8 @@ SIGNATURES = {
     "hb_opt_download_embed": [_P, _I, _P, _P],
     "hb_forward_backward": [_P, _P, _P, _P, _I, _I, _F, _P, _P],
     "hb_forward_backward_device": [_P, _P, _P, _P, _I, _I, _F, _P, _P],
+    "hb_train_forward": [_P, _P, _P, _I, _I, _P, _P, C.POINTER(hb_forward_result)],
+    "hb_train_backward": [_P, _P, _F],
     "hb_rstk_read_header": [C.c_char_p, C.POINTER(hb_rstk_header)],
     "hb_model_load_rstk": [_P, _P, C.c_char_p, C.POINTER(C.c_uint32)],
     "hb_model_save_rstk": [_P, _P, _U32, C.c_char_p],
@@ -332,6 +340,29 @@ class Model:
     def reserve(self, B: int, S: int) -> None:
         call("hb_model_reserve", self.handle, B, S)
 
+    def train_forward(self, tokens, targets, batch: int, seq: int, views=()):
+        """hb_train_forward: the training forward of `batch` sequences of `seq`
+        tokens, its activations kept on the device for the next backward.
+        `views` names the ForwardResult fields to download (dlogits, x_final,
+        x_prenorm, rms_inv_final, logits_capped). Returns (mean loss,
+        per-position losses, {name: array})."""
+        import numpy as np
+        c = self.config
+        tok = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        tgt = np.ascontiguousarray(targets, dtype=np.uint32).reshape(-1)
+        n = batch * seq
+        if tok.size != n or tgt.size != n:
+            raise ValueError(f"expected {n} tokens and targets")
+        shapes = {"dlogits": (n * c.vocab,), "logits_capped": (n * c.vocab,), "rms_inv_final": (n,),
+                  "x_final": (batch, c.dim, seq), "x_prenorm": (batch, c.dim, seq)}
+        out = {k: np.zeros(shapes[k], np.float32) for k in views}
+        r = hb_forward_result(**{k: v.ctypes.data for k, v in out.items()})
+        mean = C.c_float()
+        losses = np.empty(n, np.float32)
+        call("hb_train_forward", self.handle, tok.ctypes.data, tgt.ctypes.data, batch, seq,
+             losses.ctypes.data, C.byref(mean), C.byref(r))
+        return mean.value, losses, out
+
     def close(self) -> None:
         if self.handle and not _exiting:
             lib().hb_model_destroy(self.handle)
@@ -495,6 +526,11 @@ class Optimizer:
         call("hb_forward_backward", self.model.handle, self.handle, tok.ctypes.data, tgt.ctypes.data,
              batch, seq, loss_scale, losses.ctypes.data if want_losses else None, C.byref(mean))
         return (mean.value, losses) if want_losses else mean.value
+
+    def backward(self, loss_scale: float = 256.0) -> None:
+        """hb_train_backward: the backward of the model's last hb_train_forward,
+        added to this optimizer's gradient arena."""
+        call("hb_train_backward", self.model.handle, self.handle, loss_scale)
 
     def forward_backward_device(self, d_tokens: int, d_targets: int, batch: int, seq: int,
                                 loss_scale: float = 256.0, d_loss: int = 0, d_mean: int = 0) -> None:

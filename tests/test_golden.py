@@ -42,7 +42,7 @@ def test_device_matches_fixture(gpu, name):
     k = E.CompiledKernels.compile(cfg)
     k.init_synthetic(G.CASES[name][2], G.STD)  # device-side generation of the same weights
     S = len(tok) - 1
-    res = E.forward(cfg, k, None, tok[:-1], tok[1:])
+    res = E.forward_logits(cfg, k, None, tok[:-1], tok[1:])
     logits = res.logits.reshape(S, cfg.vocab)
     rel = np.abs(res.losses - fx["losses"]) / fx["losses"]
     err = np.abs(logits[fx["logit_rows"]][:, :512] - fx["logits_sub"]).max()

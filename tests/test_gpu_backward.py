@@ -241,7 +241,7 @@ def test_train_steps_lower_the_loss():
         print("losses", [f"{x:.4f}" for x in losses], flush=True)
         assert losses[-1] < losses[0] - 0.05
         # the weights the forward reads changed with the steps
-        after = E.forward(cfg, k, None, tok[:-1], tok[1:])
+        after = E.forward_logits(cfg, k, None, tok[:-1], tok[1:])
         assert abs(float(np.mean(after.losses)) - losses[-1]) < 0.5
     finally:
         st.close()
@@ -457,6 +457,98 @@ def test_gradient_norm_from_backward_partials():
         st.opt.grad_arena()  # hands out the pointer: the next norm is a full pass
         full = st.opt.grad_norm()
         assert abs(fused - full) <= 1e-6 * full
+    finally:
+        st.close()
+
+
+def test_gradient_norm_sees_writes_through_the_handed_out_arena():
+    """Once hb_opt_grad_arena has handed out the raw pointer, a backward's
+    per-tile sums of squares no longer stand for the arena: the caller may
+    write through the pointer after the backward. The norm must include such
+    a write (here 1e-3 added to every gradient element through the pointer)."""
+    import ctypes as C
+    import os
+    import torch
+    hip = C.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    D2D = 3  # hipMemcpyDeviceToDevice
+    cfg = tiny_config()
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=32, std=0.02)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    try:
+        tok = tokens_for(cfg, cfg.seq + 1, seed=33)
+        st.opt.zero_grads()
+        ptr, n = st.opt.grad_arena()
+        st.opt.forward_backward(tok[:-1], tok[1:], 1, cfg.seq, 256.0)
+        k.ctx.synchronize()
+        buf = torch.empty(n, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        assert hip.hipMemcpy(buf.data_ptr(), ptr, 4 * n, D2D) == 0
+        buf += 1e-3
+        torch.cuda.synchronize()
+        assert hip.hipMemcpy(ptr, buf.data_ptr(), 4 * n, D2D) == 0
+        dev = _device_grads(st.opt, cfg.nlayers)
+        ref = np.sqrt(sum(float(np.sum(np.asarray(a, np.float64) ** 2)) for _, a, _ in _pairs(dev, dev)))
+        norm = st.opt.grad_norm()
+        print(f"norm after the caller's write {norm:.7e}, float64 of the arena {ref:.7e}", flush=True)
+        assert abs(norm - ref) <= 1e-6 * ref
+    finally:
+        st.close()
+
+
+def _rel_max(a, b):
+    a, b = np.asarray(a, np.float64).reshape(-1), np.asarray(b, np.float64).reshape(-1)
+    return np.abs(a - b).max() / max(np.abs(b).max(), 1e-30)
+
+
+@pytest.mark.parametrize("softcap", [0.0, 0.5])
+def test_forward_result_then_backward(softcap):
+    """The reference's pair forward() -> ForwardResult -> backward()
+    (full_model.rs:73-81, 345-483) through hb_train_forward / hb_train_backward:
+    ForwardResult's fields against the oracle on the device's weights, and the
+    pair's gradients equal to hb_forward_backward's bit for bit."""
+    cfg = tiny_config(heads=4, kv_heads=2)
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=40, std=0.05 if softcap else 0.02)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    try:
+        S, V, d = cfg.seq, cfg.vocab, cfg.dim
+        tok = tokens_for(cfg, S + 1, seed=41)
+        ocfg, ow = oracle_cfg(cfg), _rounded_oracle_weights(w)
+        ref = O.model_forward(ocfg, ow, tok[:-1], tok[1:], softcap=softcap)
+        raw = O.model_forward(ocfg, ow, tok[:-1], tok[1:])["logits"]
+        _, dref = OB.cross_entropy_fwd_bwd(ref["logits"], tok[1:], V, F32(1) / F32(S))
+        _, rinv_ref = O.rmsnorm_channel_first(ref["x_prenorm_cf"], ow.gamma_final, d, S)
+        st.opt.zero_grads()
+        fwd = E.forward(cfg, k, None, tok[:-1], tok[1:], softcap=softcap)
+        assert fwd.dlogits.shape == (S * V,) and fwd.rms_inv_final.shape == (S,)
+        assert fwd.x_final.shape == (d * S,) and fwd.x_prenorm.shape == (d * S,)
+        errs = {"loss": abs(fwd.loss - float(ref["loss"])) / float(ref["loss"]),
+                "dlogits": _rel_max(fwd.dlogits, dref),
+                "x_final": _rel_max(fwd.x_final, ref["x_final_cf"]),
+                "x_prenorm": _rel_max(fwd.x_prenorm, ref["x_prenorm_cf"]),
+                "rms_inv_final": _rel_max(fwd.rms_inv_final, rinv_ref)}
+        if softcap:
+            errs["logits_capped"] = _rel_max(fwd.logits_capped, np.tanh(raw * (F32(1) / F32(softcap))))
+        else:
+            assert fwd.logits_capped.size == 0
+        print(f"softcap {softcap}: " + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()), flush=True)
+        assert errs.pop("loss") <= LOSS_RTOL
+        assert max(errs.values()) <= 5e-3, errs
+        E.backward(cfg, k, None, fwd, tok[:-1], softcap, 256.0, st)
+        pair = _device_grads(st.opt, cfg.nlayers)
+        with pytest.raises(hb.HipBridgeError) as e:  # one backward per kept forward
+            E.backward(cfg, k, None, fwd, tok[:-1], softcap, 256.0, st)
+        assert e.value.code == hb.HB_E_STATE
+        st.opt.zero_grads()
+        st.opt.forward_backward(tok[:-1], tok[1:], 1, S, 256.0)
+        fused = _device_grads(st.opt, cfg.nlayers)
+        for name, a, b in _pairs(pair, fused):
+            np.testing.assert_array_equal(a, b, err_msg=name)
+        with pytest.raises(hb.HipBridgeError) as e:  # hb_forward_backward keeps nothing
+            st.opt.backward(256.0)
+        assert e.value.code == hb.HB_E_STATE
     finally:
         st.close()
 

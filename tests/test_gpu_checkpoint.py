@@ -21,8 +21,8 @@ def test_load_equals_direct_upload(gpu, tmp_path):
     assert E.load_checkpoint(p, k1) == 5
     k2 = CompiledKernels.compile(cfg)
     tok = tokens_for(cfg, cfg.seq + 1, seed=12)
-    a = E.forward(cfg, k1, None, tok[:-1], tok[1:])
-    b = E.forward(cfg, k2, w, tok[:-1], tok[1:])
+    a = E.forward_logits(cfg, k1, None, tok[:-1], tok[1:])
+    b = E.forward_logits(cfg, k2, w, tok[:-1], tok[1:])
     np.testing.assert_array_equal(a.logits, b.logits)
     np.testing.assert_array_equal(a.losses, b.losses)
 

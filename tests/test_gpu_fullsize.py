@@ -87,7 +87,7 @@ class _Full:
         self.ow_f32 = synthetic_oracle_weights(cfg, SEED, STD, cache=cache_f32)
 
     def forward(self, inp, tgt, B):
-        return E.forward(self.cfg, self.k, None, inp, tgt, batch=B)
+        return E.forward_logits(self.cfg, self.k, None, inp, tgt, batch=B)
 
     def close(self):
         self.k.model.close()

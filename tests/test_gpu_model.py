@@ -24,7 +24,7 @@ TOP1_MIN = 0.995
 def _compare_forward(cfg, w, kernels, B, S, seed=42):
     tok = tokens_for(cfg, B * (S + 1), seed=seed).reshape(B, S + 1)
     inp, tgt = tok[:, :-1].copy(), tok[:, 1:].copy()
-    res = E.forward(cfg, kernels, w, inp, tgt, batch=B)
+    res = E.forward_logits(cfg, kernels, w, inp, tgt, batch=B)
     ref = O.forward_batch(oracle_cfg(cfg), oracle_weights(w), inp, tgt, B=B)
     gl = res.logits.reshape(B, S, cfg.vocab)
     rl = ref["logits"]
@@ -68,7 +68,7 @@ def test_softcap_forward_matches_oracle(gpu):
     k = CompiledKernels.compile(cfg)
     tok = tokens_for(cfg, cfg.seq + 1, seed=3)
     # logits here have std ~0.25: a cap of 0.3 bends most of them
-    res = E.forward(cfg, k, w, tok[:-1], tok[1:], softcap=0.3)
+    res = E.forward_logits(cfg, k, w, tok[:-1], tok[1:], softcap=0.3)
     ref = O.model_forward(oracle_cfg(cfg), oracle_weights(w), tok[:-1], tok[1:], softcap=0.3)
     raw = O.model_forward(oracle_cfg(cfg), oracle_weights(w), tok[:-1], tok[1:])
     assert np.abs(raw["logits"]).max() > 0.6  # the cap is active
@@ -76,7 +76,7 @@ def test_softcap_forward_matches_oracle(gpu):
     assert np.abs(res.logits).max() <= 0.3
     np.testing.assert_allclose(res.losses, ref["losses"], rtol=LOSS_RTOL)
     # back to no softcap: the next forward matches the uncapped oracle
-    res0 = E.forward(cfg, k, w, tok[:-1], tok[1:], softcap=0.0)
+    res0 = E.forward_logits(cfg, k, w, tok[:-1], tok[1:], softcap=0.0)
     assert np.abs(res0.logits.reshape(-1) - raw["logits"].reshape(-1)).max() < LOGIT_ATOL
 
 
@@ -89,7 +89,7 @@ def test_split_k_forward_matches_oracle(gpu):
     k = CompiledKernels.compile(cfg)
     err, rel, top1, res, ref = _compare_forward(cfg, w, k, B=1, S=cfg.seq, seed=9)
     assert err < LOGIT_ATOL and rel < LOSS_RTOL and top1 >= TOP1_MIN
-    again = E.forward(cfg, k, w, *(lambda t: (t[:-1], t[1:]))(tokens_for(cfg, cfg.seq + 1, seed=9)))
+    again = E.forward_logits(cfg, k, w, *(lambda t: (t[:-1], t[1:]))(tokens_for(cfg, cfg.seq + 1, seed=9)))
     np.testing.assert_array_equal(again.logits, res.logits.reshape(again.logits.shape))
 
 
@@ -117,9 +117,9 @@ def test_48m_batch_rows_equal_single_sequences(m48):
     cfg, w, k = m48
     B, S = 3, 128
     tok = tokens_for(cfg, B * S, seed=11).reshape(B, S)
-    batched = E.forward(cfg, k, w, tok, None, batch=B).logits.reshape(B, S, cfg.vocab)
+    batched = E.forward_logits(cfg, k, w, tok, None, batch=B).logits.reshape(B, S, cfg.vocab)
     for b in range(B):
-        one = E.forward(cfg, k, w, tok[b], None).logits.reshape(S, cfg.vocab)
+        one = E.forward_logits(cfg, k, w, tok[b], None).logits.reshape(S, cfg.vocab)
         np.testing.assert_array_equal(batched[b], one)
 
 
@@ -127,8 +127,8 @@ def test_48m_forward_deterministic(m48):
     # auto_fwd_rebalance_staging.rs:23-49: repeated forwards are bit-identical
     cfg, w, k = m48
     tok = tokens_for(cfg, cfg.seq + 1, seed=2)
-    a = E.forward(cfg, k, w, tok[:-1], tok[1:])
-    b = E.forward(cfg, k, w, tok[:-1], tok[1:])
+    a = E.forward_logits(cfg, k, w, tok[:-1], tok[1:])
+    b = E.forward_logits(cfg, k, w, tok[:-1], tok[1:])
     np.testing.assert_array_equal(a.logits, b.logits)
     np.testing.assert_array_equal(a.losses, b.losses)
 
@@ -160,7 +160,7 @@ def test_decode_equals_prefill_rows_on_gpu(m48):
     cfg, w, k = m48
     S = 64
     tok = tokens_for(cfg, S, seed=31)
-    full = E.forward(cfg, k, w, tok, None).logits.reshape(S, cfg.vocab)
+    full = E.forward_logits(cfg, k, w, tok, None).logits.reshape(S, cfg.vocab)
     dec = E.Decoder(k, batch=1, ctx_max=S)
     gl, _ = dec.prefill(tok[:40])
     assert np.abs(gl[0] - full[39]).max() < 2e-3
@@ -275,3 +275,35 @@ def test_error_paths(gpu):
     with pytest.raises(hb.HipBridgeError) as e:
         dec.step([1])
     assert e.value.code == hb.HB_E_STATE
+
+
+def test_oversize_token_counts_are_rejected_before_any_allocation(gpu):
+    """B x S tokens whose widest activation (the vocab-wide logits here) reaches
+    2^31 elements would wrap the kernels' 32-bit offsets: every forward entry
+    point refuses them with HB_E_INVALID before it allocates or launches."""
+    import torch
+    S = 1 << 17  # 131072 tokens x 32000 logits > 2^31
+    cfg = tiny_config(vocab=32000, seq=S)
+    k = CompiledKernels.compile(cfg)
+    k.init_synthetic(1)
+    kv = hb.KVCache(k.model, 1, S)
+    tok = np.zeros(S, np.uint32)
+    dtok = torch.zeros(S, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    calls = [("hb_forward", (k.model.handle, hb.ptr(tok), None, 1, S, None, None, None)),
+             ("hb_forward_device", (k.model.handle, dtok.data_ptr(), None, 1, S, None, None, None)),
+             ("hb_model_reserve", (k.model.handle, 1, S)),
+             ("hb_prefill", (k.model.handle, kv.handle, hb.ptr(tok), S, None, None)),
+             ("hb_op_logits_ce", (k.model.handle, dtok.data_ptr(), None, S, dtok.data_ptr(), None))]
+    for name, args in calls:
+        with pytest.raises(hb.HipBridgeError) as e:
+            hb.call(name, *args)
+        assert e.value.code == hb.HB_E_INVALID, name
+        assert "2^31" in hb.last_error(), (name, hb.last_error())
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] >= free0 - (4 << 20)
+    kv.close()
+    # the largest accepted count is reserved normally
+    S_ok = (1 << 31) // 32000 // 64 * 64 - 64
+    hb.call("hb_model_reserve", k.model.handle, 1, S_ok)

@@ -139,12 +139,12 @@ def test_forward_and_decode_use_updated_weights(tiny_opt):
         st.opt.upload_layer(l, lw)
     st.opt.upload_embed(w.embed, w.gamma_final)
     tok = tokens_for(cfg, cfg.seq + 1, seed=5)
-    before = E.forward(cfg, k, None, tok[:-1], tok[1:]).logits
+    before = E.forward_logits(cfg, k, None, tok[:-1], tok[1:]).logits
     ref = _state_of(w)
     for s in range(3):
         _upload_grads(st.opt, _random_grads(ref, seed=40 + s, std=1.0))
         st.opt.step(s, want_norm=False)
-    after = E.forward(cfg, k, None, tok[:-1], tok[1:])
+    after = E.forward_logits(cfg, k, None, tok[:-1], tok[1:])
     dev = _device_state(st.opt, 0, cfg.nlayers)
     ow = O.ModelW(embed=f16_round(dev["embed"]), gamma_final=dev["gamma_final"],
                   layers=[O.LayerW(**{kk: (f16_round(lw[kk]) if kk.startswith("w") else lw[kk])
@@ -197,9 +197,9 @@ def test_synthetic_master_matches_host_values(gpu):
         # and the model's fp16 weights are the same values rounded
         k._uploaded = ("synthetic", 77, 0.02)
         tok = tokens_for(cfg, cfg.seq + 1, seed=6)
-        a = E.forward(cfg, k, None, tok[:-1], tok[1:]).logits
+        a = E.forward_logits(cfg, k, None, tok[:-1], tok[1:]).logits
         k2 = CompiledKernels.compile(cfg)
-        b = E.forward(cfg, k2, w, tok[:-1], tok[1:]).logits
+        b = E.forward_logits(cfg, k2, w, tok[:-1], tok[1:]).logits
         np.testing.assert_array_equal(a, b)
     finally:
         opt.close()

@@ -333,6 +333,32 @@ def test_softcap_bounds_logits():
     np.testing.assert_allclose(capped, 3.0 * np.tanh(raw / 3.0), atol=1e-5)
 
 
+def test_softcap_uses_the_reference_operation_order():
+    """full_model.rs:388-393 scales by the f32 reciprocal 1/c before tanh and
+    multiplies by c after. For c = 3, x * fl(1/3) and x / 3 differ in fp32 for
+    about a third of inputs; the forward oracle, the decode oracle and the
+    backward oracle (which stores the same tanh for the softcap derivative)
+    must all take the reciprocal route, bit for bit."""
+    import oracle.backward as OB
+    x = np.linspace(-40, 40, 4001, dtype=F32)
+    recip = (x * (F32(1) / F32(3))).astype(F32)
+    div = (x / F32(3)).astype(F32)
+    assert (recip != div).mean() > 0.1  # the two orders are distinguishable here
+    got = O.softcap_forward(x, 3.0)
+    want = (np.tanh(recip).astype(F32) * F32(3)).astype(F32)
+    np.testing.assert_array_equal(got, want)
+    assert (got != (np.tanh(div).astype(F32) * F32(3)).astype(F32)).any()
+    # whole-model paths: forward, decode and the backward's forward agree exactly
+    cfg = tiny_cfg(softcap=3.0)
+    w = tiny_weights(cfg, std=0.5)
+    tok = np.arange(cfg.seq + 1) % cfg.vocab
+    fwd = O.model_forward(cfg, w, tok[:-1], tok[1:], softcap=3.0)
+    raw = O.model_forward(cfg, w, tok[:-1], tok[1:])["logits"]
+    np.testing.assert_array_equal(fwd["logits"], O.softcap_forward(raw, 3.0))
+    loss_b, _ = OB.model_forward_backward(cfg, w, tok[:-1], tok[1:], 3.0, 1.0)
+    assert loss_b == pytest.approx(float(fwd["loss"]), rel=1e-6)
+
+
 def test_decode_oracle_equals_prefill_rows():
     cfg = tiny_cfg()
     w = tiny_weights(cfg)
