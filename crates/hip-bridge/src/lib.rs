@@ -151,6 +151,8 @@ pub mod sys {
         pub fn hb_model_get_config(model: *const hb_model, out: *mut hb_model_config) -> c_int;
         pub fn hb_model_weight_bytes(model: *const hb_model, out: *mut u64) -> c_int;
         pub fn hb_model_set_softcap(model: *mut hb_model, softcap: f32) -> c_int;
+        pub fn hb_model_set_precise_layers(model: *mut hb_model, n: c_int) -> c_int;
+        pub fn hb_model_get_precise_layers(model: *const hb_model, out_n: *mut c_int) -> c_int;
         pub fn hb_model_upload_layer(
             model: *mut hb_model,
             layer: c_int,
@@ -610,6 +612,12 @@ impl<'c> Model<'c> {
         check(unsafe { sys::hb_model_set_softcap(self.raw, softcap) })?;
         self.cfg.softcap = softcap;
         Ok(())
+    }
+
+    /// hb_model_set_precise_layers: the first n layers of later forwards run
+    /// on two-term fp16 operands (~22-bit inputs to their products).
+    pub fn set_precise_layers(&mut self, n: usize) -> Result<()> {
+        check(unsafe { sys::hb_model_set_precise_layers(self.raw, n as c_int) })
     }
 
     pub fn upload_layer(&mut self, layer: usize, w: &LayerWeightsRef<'_>) -> Result<()> {

@@ -129,6 +129,22 @@ int hb_model_weight_bytes(const hb_model* model, uint64_t* out);
 /* Logit softcap for later forwards (0 = off). The reference passes it per call
  * (forward_ws(..., softcap, ..), full_model.rs:187-195). */
 int hb_model_set_softcap(hb_model* model, float softcap);
+/*
+ * Precision of the first layers (no counterpart in the reference, whose ANE
+ * graphs compute in fp16 throughout). The first n layers of later forwards
+ * (hb_forward*, hb_prefill, and the decode steps of KV caches created after
+ * the call) feed their products two-term fp16 operands, hi + lo with
+ * lo = fp16(x - fp16(x)): GEMM/GEMV inputs, Q, K, V and attention
+ * probabilities carry ~22 significant bits instead of 11, at twice the MFMA
+ * work of those layers (the weights are still read once). Rounding inside the
+ * first layer, where the residual stream is still the small embedding, sets
+ * most of a deep model's distance from fp32 arithmetic. Default 1; 0 <= n <=
+ * nlayers; with n = nlayers the final norm's rows feeding the logits are
+ * split too (fp32 arithmetic on the fp16 weights, to accumulation order). The
+ * training entry points and hb_op_* are not affected.
+ */
+int hb_model_set_precise_layers(hb_model* model, int n);
+int hb_model_get_precise_layers(const hb_model* model, int* out_n);
 
 /*
  * Upload one layer's weights from host fp32 arrays in the reference layouts

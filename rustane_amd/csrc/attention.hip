@@ -34,20 +34,25 @@ constexpr int PW = PQ * PK;
 
 HB_DEV int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
-template <int HD>
-__global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p) {
+// SPLIT: Q, K, V and the probabilities in two-term fp16 form (common.hpp):
+// each score and output product runs hi*hi + hi*lo + lo*hi MFMAs (the lo*lo
+// term is below fp32 rounding of the sum), and the output rows are split rows.
+template <int HD, bool SPLIT>
+__global__ __launch_bounds__(PW * 64, SPLIT ? 1 : 2) void attn_prefill_kernel(AttnPrefill p) {
   constexpr int KS = HD / 16;          // k-steps over head dim
   constexpr int MB = HD / 32;          // 32-row blocks of O^T
   constexpr int NCH = HD / 8;          // 16-byte chunks per K row
   constexpr int KT8 = 4 * HD;          // 16-byte chunks per K tile (= per V^T tile)
-  constexpr int NLD = 2 * PK * KT8 / (PW * 64);  // 16-byte loads per thread per iteration
-  static_assert(NLD * PW * 64 == 2 * PK * KT8, "loader coverage");
+  constexpr int NKIND = SPLIT ? 4 : 2;  // tile kinds: K, V^T (then their low parts)
+  constexpr int NLD = NKIND * PK * KT8 / (PW * 64);  // 16-byte loads per thread per iteration
+  static_assert(NLD * PW * 64 == NKIND * PK * KT8, "loader coverage");
   // K tiles (block kh: row r, chunk c at kh*KT8 + r*NCH + (c ^ (swap23(r) % NCH))), then
-  // V^T tiles (block kh: row e, chunk c at (PK+kh)*KT8 + e*4 + (c ^ ((e >> 2) & 3)));
-  // after the loop the region holds the key-half-1 waves' O for the merge
-  __shared__ f16x8 s_kv[2 * PK * KT8];
+  // V^T tiles (block kh: row e, chunk c at (PK+kh)*KT8 + e*4 + (c ^ ((e >> 2) & 3))),
+  // then (SPLIT) the same two for the low parts; after the loop the region
+  // holds the key-half-1 waves' O for the merge
+  __shared__ f16x8 s_kv[NKIND * PK * KT8];
   __shared__ float s_ml[PQ][2][64];
-  static_assert(2 * PK * KT8 * 16 >= PQ * MB * 16 * 64 * 4, "merge buffer fits in the tiles");
+  static_assert(NKIND * PK * KT8 * 16 >= PQ * MB * 16 * 64 * 4, "merge buffer fits in the tiles");
   const int tid = threadIdx.x, lane = tid & 63, h2 = lane >> 5, li = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int qs = wave % PQ, kh = wave / PQ;
@@ -62,28 +67,35 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
   const int q0 = qb * 32;
   const int qi = q0 + li;
 
-  f16x8 qf[KS];
+  f16x8 qf[KS], ql[SPLIT ? KS : 1];
   if (active) {
-    const f16* qp = p.q + (((size_t)b * p.H + h) * p.q_rows + q0 + li) * HD + 8 * h2;
+    const size_t qo = (((size_t)b * p.H + h) * p.q_rows + q0 + li) * HD + 8 * h2;
 #pragma unroll
-    for (int j = 0; j < KS; ++j) qf[j] = *(const f16x8*)(qp + 16 * j);
+    for (int j = 0; j < KS; ++j) qf[j] = *(const f16x8*)(p.q + qo + 16 * j);
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int j = 0; j < KS; ++j) ql[j] = *(const f16x8*)(p.q_lo + qo + 16 * j);
+    }
   }
 
-  const f16* kbase = p.k + b * p.k_bstride + kvh * p.k_hstride;
-  const f16* vbase = p.vt + ((size_t)b * p.KVH + kvh) * HD * p.vt_ld;
+  const size_t koff = b * p.k_bstride + kvh * p.k_hstride;
+  const size_t voff = ((size_t)b * p.KVH + kvh) * HD * p.vt_ld;
   const float sl2 = p.scale * HB_LOG2E;
 
   // thread tid, load i covers 16-byte chunk x = i*256 + tid of the iteration's
-  // 2*PK tiles (K blocks, then V^T blocks)
+  // NKIND*PK tiles (K blocks, then V^T blocks, then their low parts)
   f16x8 kvreg[NLD];
   auto gload = [&](int n) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int x = i * PW * 64 + tid, tile = x / KT8, y = x % KT8;
+      const int kind = tile / PK;  // 0 K, 1 V^T, 2 K low, 3 V^T low
       const int kb = min(n * PK + (tile % PK), nkb - 1);
-      if (tile < PK) {
+      if ((kind & 1) == 0) {
+        const f16* kbase = (kind ? p.k_lo : p.k) + koff;
         kvreg[i] = *(const f16x8*)(kbase + ((size_t)kb * 32 + y / NCH) * HD + (y % NCH) * 8);
       } else {
+        const f16* vbase = (kind > 1 ? p.vt_lo : p.vt) + voff;
         const int e = y >> 2, c = y & 3;
         kvreg[i] = *(const f16x8*)(vbase + (size_t)e * p.vt_ld + kb * 32 + c * 8);
       }
@@ -93,7 +105,7 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int x = i * PW * 64 + tid, tile = x / KT8, y = x % KT8;
-      if (tile < PK) {
+      if (((tile / PK) & 1) == 0) {
         const int r = y / NCH, c = y % NCH;
         s_kv[tile * KT8 + r * NCH + (c ^ (swap23(r) % NCH))] = kvreg[i];
       } else {
@@ -104,6 +116,8 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
   };
   const f16x8* sk = s_kv + kh * KT8;
   const f16x8* sv = s_kv + (PK + kh) * KT8;
+  const f16x8* skl = s_kv + (2 * PK + kh) * KT8;  // SPLIT only
+  const f16x8* svl = s_kv + (3 * PK + kh) * KT8;
 
   f32x16 o[MB];
 #pragma unroll
@@ -124,8 +138,13 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
     f32x16 s = {};
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      const f16x8 kf = sk[krow * NCH + ((2 * j + h2) ^ (li % NCH))];
+      const int ko = krow * NCH + ((2 * j + h2) ^ (li % NCH));
+      const f16x8 kf = sk[ko];
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[j], s, 0, 0, 0);
+      if constexpr (SPLIT) {
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[j], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(skl[ko], qf[j], s, 0, 0, 0);
+      }
     }
     float mloc = -INFINITY;
 #pragma unroll
@@ -161,14 +180,23 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
 
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      f16x8 pb;
+      f16x8 pb, pl;
 #pragma unroll
       for (int i = 0; i < 8; ++i) pb[i] = (f16)s[8 * j + i];
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pl[i] = (f16)(s[8 * j + i] - (float)pb[i]);
+      }
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
         const int e = m * 32 + li;
-        const f16x8 va = sv[e * 4 + ((2 * j + h2) ^ ((e >> 2) & 3))];
+        const int vo = e * 4 + ((2 * j + h2) ^ ((e >> 2) & 3));
+        const f16x8 va = sv[vo];
         o[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[m], 0, 0, 0);
+        if constexpr (SPLIT) {
+          o[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, o[m], 0, 0, 0);
+          o[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(svl[vo], pb, o[m], 0, 0, 0);
+        }
       }
     }
   }
@@ -202,17 +230,18 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
 
   if (qi < p.S) {
     const float inv = 1.0f / L;
-    f16* op = p.out + ((size_t)b * p.S + qi) * (p.H * HD) + h * HD;
+    f16* op = p.out + ((size_t)b * p.S + qi) * (SPLIT ? 2 * p.H * HD : p.H * HD) + h * HD;
+    const size_t lo = SPLIT ? (size_t)p.H * HD : 0;  // split rows: [hi | lo]
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        f16x4 w;
-        w.x = (f16)(o[m][4 * g + 0] * inv);
-        w.y = (f16)(o[m][4 * g + 1] * inv);
-        w.z = (f16)(o[m][4 * g + 2] * inv);
-        w.w = (f16)(o[m][4 * g + 3] * inv);
-        *(f16x4*)(op + m * 32 + 8 * g + 4 * h2) = w;
+        f32x4 w;
+        w.x = o[m][4 * g + 0] * inv;
+        w.y = o[m][4 * g + 1] * inv;
+        w.z = o[m][4 * g + 2] * inv;
+        w.w = o[m][4 * g + 3] * inv;
+        store_f16x4(op + m * 32 + 8 * g + 4 * h2, w, lo);
       }
   }
 }
@@ -220,10 +249,16 @@ __global__ __launch_bounds__(PW * 64, 2) void attn_prefill_kernel(AttnPrefill p)
 hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
   const int nqb = (p.S + 31) / 32;
   dim3 grid((nqb + PQ - 1) / PQ, p.H, p.B);
-  if (p.hd == 128)
-    hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(PW * 64), 0, st, p);
+  const bool split = p.q_lo != nullptr;
+  if (split && (!p.k_lo || !p.vt_lo)) return hipErrorInvalidValue;
+  if (p.hd == 128 && split)
+    hipLaunchKernelGGL((attn_prefill_kernel<128, true>), grid, dim3(PW * 64), 0, st, p);
+  else if (p.hd == 128)
+    hipLaunchKernelGGL((attn_prefill_kernel<128, false>), grid, dim3(PW * 64), 0, st, p);
+  else if (p.hd == 64 && split)
+    hipLaunchKernelGGL((attn_prefill_kernel<64, true>), grid, dim3(PW * 64), 0, st, p);
   else if (p.hd == 64)
-    hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(PW * 64), 0, st, p);
+    hipLaunchKernelGGL((attn_prefill_kernel<64, false>), grid, dim3(PW * 64), 0, st, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -251,7 +286,9 @@ constexpr int DWAVES = 16;
 int attn_decode_chunks(int ctx_max) { return (ctx_max + DCHUNK - 1) / DCHUNK; }
 int attn_decode_chunk_keys() { return DCHUNK; }
 
-template <int HD>
+// SPLIT: q, K and V come in two-term fp16 form (common.hpp) and are summed to
+// fp32 as they are loaded (the arithmetic is fp32 throughout).
+template <int HD, bool SPLIT>
 __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) {
   constexpr int NT = DWAVES * 64;
   constexpr int LPK = HD / 8;             // lanes per key row
@@ -269,37 +306,55 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane / LPK, j = lane % LPK;
 
-  const f16x8 qv = *(const f16x8*)(p.q + ((size_t)b * p.H + h) * HD + 8 * j);
+  const size_t qo = ((size_t)b * p.H + h) * HD + 8 * j;
+  const f16x8 qv = *(const f16x8*)(p.q + qo);
   float qf[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) qf[i] = (float)qv[i];
-  const f16* kb = p.k + b * p.bstride + kvh * p.hstride + 8 * j;
-  const f16* vb = p.v + b * p.bstride + kvh * p.hstride + 8 * j;
+  if constexpr (SPLIT) {
+    const f16x8 ql = *(const f16x8*)(p.q_lo + qo);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qf[i] += (float)ql[i];
+  }
+  const size_t kvo = b * p.bstride + kvh * p.hstride + 8 * j;
+  const f16* kb = p.k + kvo;
+  const f16* vb = p.v + kvo;
   const float sl2 = p.scale * HB_LOG2E;
 
   const int kbase = c0 + wave * WKEYS + g;
-  f16x8 kr[NIT], vr[NIT];
+  constexpr int NL = SPLIT ? NIT : 1;
+  f16x8 kr[NIT], vr[NIT], krl[NL], vrl[NL];
   const f16x8 zero8 = {};
 #pragma unroll
   for (int i = 0; i < NIT; ++i) {
     const int kk = kbase + i * KPW;
     kr[i] = kk <= pos ? *(const f16x8*)(kb + (size_t)kk * HD) : zero8;
+    if constexpr (SPLIT) krl[i] = kk <= pos ? *(const f16x8*)(p.k_lo + kvo + (size_t)kk * HD) : zero8;
   }
+  // V loads go out with K's, before the scores, except with low parts: then
+  // they follow the scores so that K's registers are free again
+  auto load_v = [&]() {
 #pragma unroll
-  for (int i = 0; i < NIT; ++i) {
-    const int kk = kbase + i * KPW;
-    vr[i] = kk <= pos ? *(const f16x8*)(vb + (size_t)kk * HD) : zero8;
-  }
+    for (int i = 0; i < NIT; ++i) {
+      const int kk = kbase + i * KPW;
+      vr[i] = kk <= pos ? *(const f16x8*)(vb + (size_t)kk * HD) : zero8;
+      if constexpr (SPLIT) vrl[i] = kk <= pos ? *(const f16x8*)(p.v_lo + kvo + (size_t)kk * HD) : zero8;
+    }
+  };
+  if constexpr (!SPLIT) load_v();
+  auto kval = [&](int i, int e) { return SPLIT ? (float)kr[i][e] + (float)krl[i % NL][e] : (float)kr[i][e]; };
+  auto vval = [&](int i, int e) { return SPLIT ? (float)vr[i][e] + (float)vrl[i % NL][e] : (float)vr[i][e]; };
   float sc[NIT];
 #pragma unroll
   for (int i = 0; i < NIT; ++i) {
     float d = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) d += qf[e] * (float)kr[i][e];
+    for (int e = 0; e < 8; ++e) d += qf[e] * kval(i, e);
 #pragma unroll
     for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
     sc[i] = (kbase + i * KPW <= pos) ? d * sl2 : -INFINITY;
   }
+  if constexpr (SPLIT) load_v();
   // wave-wide max over its keys (lanes of a group hold equal scores)
   float m = sc[0];
 #pragma unroll
@@ -313,7 +368,7 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
       const float pk = exp2f(sc[i] - m);
       l += pk;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += pk * (float)vr[i][e];
+      for (int e = 0; e < 8; ++e) acc[e] += pk * vval(i, e);
     }
   }
 #pragma unroll
@@ -378,6 +433,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecode p, int nch
     O1 += w * *(const f32x4*)(po + (size_t)c * HD + 4);
   }
   const float iL = 1.0f / L;
+  if (p.q_lo) {  // split rows [B][2*H*hd]: hi | lo
+    const int b = bh / p.H, h = bh - b * p.H;
+    f16* op = p.out + (size_t)b * 2 * p.H * HD + h * HD + e0;
+    store_f16x4(op, O0 * iL, (size_t)p.H * HD);
+    store_f16x4(op + 4, O1 * iL, (size_t)p.H * HD);
+    return;
+  }
   f16x8 o;
   o[0] = (f16)(O0.x * iL);
   o[1] = (f16)(O0.y * iL);
@@ -393,10 +455,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecode p, int nch
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
   const int nch = attn_decode_chunks(p.ctx_max);
   dim3 grid(nch, p.H, p.B), block(DWAVES * 64);
-  if (p.hd == 128)
-    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, block, 0, st, p);
+  const bool split = p.q_lo != nullptr;
+  if (split && (!p.k_lo || !p.v_lo)) return hipErrorInvalidValue;
+  if (p.hd == 128 && split)
+    hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, block, 0, st, p);
+  else if (p.hd == 128)
+    hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, block, 0, st, p);
+  else if (p.hd == 64 && split)
+    hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, block, 0, st, p);
   else if (p.hd == 64)
-    hipLaunchKernelGGL(attn_decode_kernel<64>, grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, block, 0, st, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -93,6 +93,10 @@ struct Workspace {
   float *x = nullptr, *x2 = nullptr, *logits = nullptr, *loss = nullptr, *mean = nullptr;
   f16 *xn = nullptr, *q = nullptr, *k = nullptr, *vt = nullptr, *attn = nullptr, *gate = nullptr;
   uint32_t *tok = nullptr, *tgt = nullptr;
+  // split-operand layers (hb_model::precise_layers): xn, attn and gate have
+  // room for split rows [T, 2K], and Q, K, V^T have low parts
+  bool split = false;
+  f16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
 };
 
 }  // namespace
@@ -132,6 +136,12 @@ struct hb_model {
   // weights out of date after any weight write.
   TrainState* train = nullptr;
   bool wt_stale = true;
+  // The first precise_layers layers of a prefill or decode forward run on
+  // two-term fp16 operands (common.hpp): their GEMM/GEMV inputs, Q, K, V and
+  // attention probabilities carry ~22 bits instead of fp16's 11. Rounding in
+  // the first layer, where the residual stream is still the small embedding,
+  // sets most of the deep models' distance from fp32 arithmetic.
+  int precise_layers = 1;
 };
 
 namespace hb {
@@ -199,6 +209,13 @@ struct hb_kv {
   float* amax_val = nullptr;  // greedy argmax partials [B][vocab/16]
   int* amax_idx = nullptr;
   f16 *xn = nullptr, *qd = nullptr, *attn = nullptr, *gate = nullptr;
+  // Layers l < np run on two-term fp16 operands (hb_model::precise_layers at
+  // creation): their K/V low parts live in lo_cache [np][B][K,V][KVH][ctx_cap][hd],
+  // the query's in qd_lo; xn, attn and gate have room for split rows.
+  int np = 0;
+  f16* lo_cache = nullptr;
+  size_t lo_bytes = 0;
+  f16* qd_lo = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   int graph_epoch = -1;
@@ -286,9 +303,10 @@ int ensure_staging(hb_model* m, size_t floats) {
   return HB_OK;
 }
 
-int ensure_workspace(hb_model* m, long T, long Tpad) {
+int ensure_workspace(hb_model* m, long T, long Tpad, bool need_split = false) {
   Workspace& w = m->ws;
-  if (T <= w.cap_T && Tpad <= w.cap_Tpad) return HB_OK;
+  const bool split = need_split || m->precise_layers > 0 || w.split;
+  if (T <= w.cap_T && Tpad <= w.cap_Tpad && w.split == split) return HB_OK;
   T = std::max(T, w.cap_T);
   Tpad = std::max(Tpad, w.cap_Tpad);
   const hb_model_config& c = m->cfg;
@@ -301,18 +319,27 @@ int ensure_workspace(hb_model* m, long T, long Tpad) {
     off += align256(bytes);
     return o;
   };
+  const size_t sf = split ? 2 : 1;  // split rows take twice the halves
   const size_t o_x = take(T * c.dim * 4), o_x2 = take(T * c.dim * 4);
   const size_t o_logits = take((size_t)T * c.vocab * 4), o_loss = take(T * 4), o_mean = take(4);
-  const size_t o_xn = take(T * c.dim * 2), o_attn = take(T * c.q_dim * 2);
-  const size_t o_gate = take((size_t)T * c.hidden * 2);
+  const size_t o_xn = take(sf * T * c.dim * 2), o_attn = take(sf * T * c.q_dim * 2);
+  const size_t o_gate = take(sf * (size_t)T * c.hidden * 2);
   const size_t o_q = take(Tpad * c.q_dim * 2), o_k = take(Tpad * c.kv_dim * 2);
   const size_t o_vt = take(Tpad * c.kv_dim * 2);
   const size_t o_tok = take(T * 4), o_tgt = take(T * 4);
+  const size_t o_qlo = split ? take(Tpad * c.q_dim * 2) : 0, o_klo = split ? take(Tpad * c.kv_dim * 2) : 0;
+  const size_t o_vtlo = split ? take(Tpad * c.kv_dim * 2) : 0;
   char* base = nullptr;
   HIP_TRY(hipMalloc(&base, off));
   w.base = base;
   w.cap_T = T;
   w.cap_Tpad = Tpad;
+  w.split = split;
+  if (split) {
+    w.q_lo = (f16*)(base + o_qlo);
+    w.k_lo = (f16*)(base + o_klo);
+    w.vt_lo = (f16*)(base + o_vtlo);
+  }
   w.x = (float*)(base + o_x);
   w.x2 = (float*)(base + o_x2);
   w.logits = (float*)(base + o_logits);
@@ -332,6 +359,11 @@ int ensure_workspace(hb_model* m, long T, long Tpad) {
   HIP_TRY(fill_f16_zero(w.q, (size_t)Tpad * c.q_dim, st));
   HIP_TRY(fill_f16_zero(w.k, (size_t)Tpad * c.kv_dim, st));
   HIP_TRY(fill_f16_zero(w.vt, (size_t)Tpad * c.kv_dim, st));
+  if (split) {
+    HIP_TRY(fill_f16_zero(w.q_lo, (size_t)Tpad * c.q_dim, st));
+    HIP_TRY(fill_f16_zero(w.k_lo, (size_t)Tpad * c.kv_dim, st));
+    HIP_TRY(fill_f16_zero(w.vt_lo, (size_t)Tpad * c.kv_dim, st));
+  }
   return HB_OK;
 }
 
@@ -430,24 +462,35 @@ struct KVTarget {
   size_t k_bstride, k_hstride;
   f16* v;  // nullable
   size_t v_bstride, v_hstride;
+  // low parts for split-operand layers, same strides (v_lo nullable)
+  f16 *k_lo = nullptr, *v_lo = nullptr;
 };
 
-int zero_vt_pad(hb_model* m, int B, int S, hipStream_t st);
+int zero_vt_pad(hb_model* m, f16* vt, int B, int S, hipStream_t st);
 
 // xn_ready: w.xn already holds RMSNorm1(x) (the previous layer's W2 produced
 // it). next_gamma != NULL: also leave RMSNorm(x_out, next_gamma) in w.xn for
 // the next layer (or the final norm); the norm is fused into the W2 split-K
 // reduction when that projection splits.
+// Layers l < np run on two-term fp16 operands (common.hpp): split rows for
+// xn, attn, x2n and gate (GEMM K doubled, weights read once per half), Q, K,
+// V with low parts, split attention; the norm that feeds layer l is written
+// split when l < np. kv.k_lo / kv.v_lo must be set for those layers.
 int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_tap, bool xn_ready,
-              const float* next_gamma) {
+              const float* next_gamma, int np) {
   const hb_model_config& c = m->cfg;
   Workspace& w = m->ws;
   const LayerW& L = m->layers[l];
   hipStream_t st = m->ctx->stream();
   const int T = B * S, Sp = S_pad_of(S);
   const float alpha = alpha_of(c);
+  // the norm after the last layer feeds the logits: split when every layer is
+  const bool sp = l < np, sp_next = l + 1 < np || (l + 1 == c.nlayers && np == c.nlayers);
+  if ((sp && (!w.split || !kv.k_lo)) || (sp_next && !w.split))
+    return fail(HB_E_STATE, "split-operand buffers missing");
+  const int f = sp ? 2 : 1;  // K multiplier of this layer's products
 
-  if (!xn_ready) HIP_TRY(rmsnorm(w.x, c.dim, L.g1, T, c.dim, c.norm_eps, w.xn, nullptr, st));
+  if (!xn_ready) HIP_TRY(rmsnorm(w.x, c.dim, L.g1, T, c.dim, c.norm_eps, w.xn, nullptr, st, sp));
   EpiQKV e{};
   e.q_dim = c.q_dim;
   e.kv_dim = c.kv_dim;
@@ -469,8 +512,15 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
   e.vt = w.vt;
   e.vt_ld = Sp;
   e.tap = qkv_tap;
-  HIP_TRY(gemm_qkv(L.wqkv, w.xn, c.q_dim + 2 * c.kv_dim, T, c.dim, e, st));
-  TRY(zero_vt_pad(m, B, S, st));
+  if (sp) {
+    e.q_lo = w.q_lo;
+    e.k_lo = kv.k_lo;
+    e.v_lo = kv.v_lo;
+    e.vt_lo = w.vt_lo;
+  }
+  HIP_TRY(gemm_qkv(L.wqkv, w.xn, c.q_dim + 2 * c.kv_dim, T, f * c.dim, e, st, c.dim));
+  TRY(zero_vt_pad(m, w.vt, B, S, st));
+  if (sp) TRY(zero_vt_pad(m, w.vt_lo, B, S, st));
   AttnPrefill a{};
   a.q = w.q;
   a.q_rows = Sp;
@@ -486,18 +536,25 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
   a.KVH = c.kv_heads;
   a.hd = c.hd;
   a.scale = 1.0f / sqrtf((float)c.hd);
+  if (sp) {
+    a.q_lo = w.q_lo;
+    a.k_lo = kv.k_lo;
+    a.vt_lo = w.vt_lo;
+  }
   HIP_TRY(attention_prefill(a, st));
   GemmScratch so, s2;
-  TRY(residual_scratch(m, c.dim, T, c.q_dim, so));
-  HIP_TRY(gemm_residual_norm(L.wo, w.attn, c.dim, T, c.q_dim, EpiResidual{w.x, w.x2, c.dim, alpha},
-                             NormOut{L.g2, c.norm_eps, w.xn}, &so, st));
-  HIP_TRY(gemm_swiglu(L.w13, w.xn, 2 * c.hidden, T, c.dim, EpiSwiGLU{w.gate, nullptr, c.hidden}, st));
-  TRY(residual_scratch(m, c.dim, T, c.hidden, s2));
+  TRY(residual_scratch(m, c.dim, T, f * c.q_dim, so));
+  HIP_TRY(gemm_residual_norm(L.wo, w.attn, c.dim, T, f * c.q_dim, EpiResidual{w.x, w.x2, c.dim, alpha},
+                             NormOut{L.g2, c.norm_eps, w.xn, sp}, &so, st, c.q_dim));
+  HIP_TRY(gemm_swiglu(L.w13, w.xn, 2 * c.hidden, T, f * c.dim, EpiSwiGLU{w.gate, nullptr, c.hidden, sp}, st,
+                      c.dim));
+  TRY(residual_scratch(m, c.dim, T, f * c.hidden, s2));
   const EpiResidual e2{w.x2, w.x, c.dim, alpha};
   if (next_gamma)
-    HIP_TRY(gemm_residual_norm(L.w2, w.gate, c.dim, T, c.hidden, e2, NormOut{next_gamma, c.norm_eps, w.xn}, &s2, st));
+    HIP_TRY(gemm_residual_norm(L.w2, w.gate, c.dim, T, f * c.hidden, e2,
+                               NormOut{next_gamma, c.norm_eps, w.xn, sp_next}, &s2, st, c.hidden));
   else
-    HIP_TRY(gemm_residual(L.w2, w.gate, c.dim, T, c.hidden, e2, &s2, st));
+    HIP_TRY(gemm_residual(L.w2, w.gate, c.dim, T, f * c.hidden, e2, &s2, st, c.hidden));
   return HB_OK;
 }
 
@@ -509,6 +566,7 @@ KVTarget scratch_kv(hb_model* m, int B, int S) {
   t.k_hstride = (size_t)Sp * c.hd;
   t.k_bstride = (size_t)c.kv_heads * t.k_hstride;
   t.v = nullptr;
+  t.k_lo = m->ws.k_lo;
   (void)B;
   return t;
 }
@@ -523,12 +581,11 @@ __global__ void zero_vt_pad_kernel(f16* vt, int rows, int ld, int S) {
 }
 
 namespace {
-int zero_vt_pad(hb_model* m, int B, int S, hipStream_t st) {
+int zero_vt_pad(hb_model* m, f16* vt, int B, int S, hipStream_t st) {
   const int Sp = S_pad_of(S);
   if (Sp == S) return HB_OK;
   const int rows = B * m->cfg.kv_heads * m->cfg.hd;
-  hipLaunchKernelGGL(zero_vt_pad_kernel, dim3((rows + 3) / 4), dim3(128), 0, st, m->ws.vt, rows, Sp,
-                     S);
+  hipLaunchKernelGGL(zero_vt_pad_kernel, dim3((rows + 3) / 4), dim3(128), 0, st, vt, rows, Sp, S);
   HIP_TRY(hipGetLastError());
   return HB_OK;
 }
@@ -705,6 +762,21 @@ extern "C" int hb_model_weight_bytes(const hb_model* m, uint64_t* out) {
   HB_INJECT_CHECK();
   if (!m || !out) return fail(HB_E_INVALID, "null argument");
   *out = m->wbytes;
+  return HB_OK;
+}
+
+extern "C" int hb_model_set_precise_layers(hb_model* m, int n) {
+  HB_INJECT_CHECK();
+  if (!m) return fail(HB_E_INVALID, "null model");
+  if (n < 0 || n > m->cfg.nlayers) return fail(HB_E_INVALID, "precise layers %d outside [0, %d]", n, m->cfg.nlayers);
+  m->precise_layers = n;
+  return HB_OK;
+}
+
+extern "C" int hb_model_get_precise_layers(const hb_model* m, int* out) {
+  HB_INJECT_CHECK();
+  if (!m || !out) return fail(HB_E_INVALID, "null argument");
+  *out = m->precise_layers;
   return HB_OK;
 }
 
@@ -1761,9 +1833,11 @@ static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint
   // Each layer leaves the next norm (the final one after the last layer) in xn.
   for (int l = 0; l < c.nlayers; ++l)
     TRY(run_layer(m, l, B, S, kv, nullptr, l > 0,
-                  l + 1 < c.nlayers ? m->layers[l + 1].g1 : m->gamma_f));
+                  l + 1 < c.nlayers ? m->layers[l + 1].g1 : m->gamma_f, m->precise_layers));
   float* logits = d_logits ? d_logits : w.logits;
-  HIP_TRY(gemm_logits(m->embed, w.xn, c.vocab, (int)T, c.dim, EpiLogits{logits, c.vocab, c.softcap}, st));
+  const int fl = m->precise_layers == c.nlayers ? 2 : 1;  // split final rows (run_layer)
+  HIP_TRY(gemm_logits(m->embed, w.xn, c.vocab, (int)T, fl * c.dim, EpiLogits{logits, c.vocab, c.softcap}, st,
+                      c.dim));
   if (d_targets) {
     float* loss = d_loss ? d_loss : w.loss;
     HIP_TRY(cross_entropy(logits, d_targets, (int)T, c.vocab, loss, nullptr, m->ctx->d_err, st));
@@ -1858,7 +1932,7 @@ extern "C" int hb_op_sdpa_fwd(hb_model* m, int layer, const void* xnorm, int B, 
   e.k = kv.k; e.k_bstride = kv.k_bstride; e.k_hstride = kv.k_hstride; e.v = nullptr;
   e.vt = w.vt; e.vt_ld = Sp; e.tap = qkv_tap;
   HIP_TRY(gemm_qkv(m->layers[layer].wqkv, (const f16*)xnorm, c.q_dim + 2 * c.kv_dim, T, c.dim, e, st));
-  TRY(zero_vt_pad(m, B, S, st));
+  TRY(zero_vt_pad(m, w.vt, B, S, st));
   AttnPrefill a{};
   a.q = w.q; a.q_rows = Sp; a.k = kv.k; a.k_bstride = kv.k_bstride; a.k_hstride = kv.k_hstride;
   a.vt = w.vt; a.vt_ld = Sp; a.out = (f16*)attn; a.B = B; a.S = S; a.H = c.heads;
@@ -1969,7 +2043,47 @@ KVTarget cache_target(hb_kv* kv, int l) {
   t.v = t.k + (size_t)c.kv_heads * t.k_hstride;
   t.v_bstride = t.k_bstride;
   t.v_hstride = t.k_hstride;
+  if (l < kv->np) {  // same layout, one layer block per split layer
+    t.k_lo = kv->lo_cache + (size_t)l * kv->B * 2 * c.kv_heads * kv->ctx_cap * c.hd;
+    t.v_lo = t.k_lo + (size_t)c.kv_heads * t.k_hstride;
+  }
   return t;
+}
+
+// Decode layer l < kv->np on two-term fp16 operands: separate norm, combine
+// and GEMV launches on split rows (the fused prologues stage fp16 rows only).
+int enqueue_decode_layer_split(hb_kv* kv, int l, const KVTarget& t, hipStream_t st) {
+  hb_model* m = kv->model;
+  const hb_model_config& c = m->cfg;
+  const LayerW& L = m->layers[l];
+  const int B = kv->B;
+  const float alpha = alpha_of(c);
+  HIP_TRY(rmsnorm(kv->x, c.dim, L.g1, B, c.dim, c.norm_eps, kv->xn, nullptr, st, true));
+  EpiQKV e{};
+  e.q_dim = c.q_dim; e.kv_dim = c.kv_dim; e.hd = c.hd; e.S = 1; e.heads = c.heads;
+  e.kv_heads = c.kv_heads; e.rope = m->rope; e.rope_ld = m->rope_len; e.d_pos = kv->d_pos;
+  e.q = kv->qd; e.q_rows = 1;
+  e.k = t.k; e.k_bstride = t.k_bstride; e.k_hstride = t.k_hstride;
+  e.v = t.v; e.v_bstride = t.v_bstride; e.v_hstride = t.v_hstride; e.vt = nullptr; e.vt_ld = 0;
+  e.tap = nullptr;
+  e.q_lo = kv->qd_lo; e.k_lo = t.k_lo; e.v_lo = t.v_lo;
+  HIP_TRY(gemv_qkv(L.t_wqkv, kv->xn, nullptr, c.q_dim + 2 * c.kv_dim, B, c.dim, e, st, true));
+  AttnDecode a{};
+  a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
+  a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
+  a.ctx_max = kv->ctx_cap; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
+  a.part_ml = kv->part_ml; a.out = kv->attn;
+  a.q_lo = kv->qd_lo; a.k_lo = t.k_lo; a.v_lo = t.v_lo;
+  HIP_TRY(attention_decode(a, st));
+  HIP_TRY(attention_combine(a, st));
+  HIP_TRY(gemv_residual(L.t_wo, kv->attn, nullptr, c.dim, B, c.q_dim, EpiResidual{kv->x, kv->x2, c.dim, alpha},
+                        st, true));
+  HIP_TRY(rmsnorm(kv->x2, c.dim, L.g2, B, c.dim, c.norm_eps, kv->xn, nullptr, st, true));
+  HIP_TRY(gemv_swiglu(L.t_w13, kv->xn, nullptr, 2 * c.hidden, B, c.dim,
+                      EpiSwiGLU{kv->gate, nullptr, c.hidden, true}, st, true));
+  HIP_TRY(gemv_residual(L.t_w2, kv->gate, nullptr, c.dim, B, c.hidden, EpiResidual{kv->x2, kv->x, c.dim, alpha},
+                        st, true));
+  return HB_OK;
 }
 
 // One decode step over the kv->B sequences at position *d_pos. Launch shapes
@@ -1991,6 +2105,10 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
   for (int l = 0; l < c.nlayers; ++l) {
     const LayerW& L = m->layers[l];
     const KVTarget t = cache_target(kv, l);
+    if (l < kv->np) {
+      TRY(enqueue_decode_layer_split(kv, l, t, st));
+      continue;
+    }
     NormIn n1, n2;
     HIP_TRY(prep_norm(kv->x, L.g1, n1));
     EpiQKV e{};
@@ -2016,12 +2134,17 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     HIP_TRY(gemv_residual(L.t_w2, kv->gate, nullptr, c.dim, B, c.hidden,
                           EpiResidual{kv->x2, kv->x, c.dim, alpha}, st));
   }
-  NormIn nf;
-  HIP_TRY(prep_norm(kv->x, m->gamma_f, nf));
   EpiLogits el{kv->logits, c.vocab, c.softcap};
   el.part_val = kv->amax_val;
   el.part_idx = kv->amax_idx;
-  HIP_TRY(gemv_logits(m->t_embed, kv->xn, fused ? &nf : nullptr, c.vocab, B, c.dim, el, st));
+  if (kv->np == c.nlayers) {  // every layer split: so are the final rows
+    HIP_TRY(rmsnorm(kv->x, c.dim, m->gamma_f, B, c.dim, c.norm_eps, kv->xn, nullptr, st, true));
+    HIP_TRY(gemv_logits(m->t_embed, kv->xn, nullptr, c.vocab, B, c.dim, el, st, true));
+  } else {
+    NormIn nf;
+    HIP_TRY(prep_norm(kv->x, m->gamma_f, nf));
+    HIP_TRY(gemv_logits(m->t_embed, kv->xn, fused ? &nf : nullptr, c.vocab, B, c.dim, el, st));
+  }
   HIP_TRY(argmax_reduce(kv->amax_val, kv->amax_idx, c.vocab / 16, B, kv->d_next, kv->d_tok,
                         kv->d_hist, kv->d_pos, kv->d_pos0, st));
   return HB_OK;
@@ -2091,6 +2214,17 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
     return fail(e == hipErrorOutOfMemory ? HB_E_OOM : HB_E_DEVICE, "KV cache of %zu bytes: %s",
                 kv->cache_bytes, hipGetErrorString(e));
   }
+  kv->np = std::min(m->precise_layers, c.nlayers);
+  if (kv->np > 0) {
+    kv->lo_bytes = kv->cache_bytes / c.nlayers * kv->np;
+    e = hipMalloc(&kv->lo_cache, kv->lo_bytes);
+    if (e != hipSuccess) {
+      (void)hipFree(kv->cache);
+      delete kv;
+      return fail(e == hipErrorOutOfMemory ? HB_E_OOM : HB_E_DEVICE, "KV low parts of %zu bytes: %s",
+                  kv->lo_bytes, hipGetErrorString(e));
+    }
+  }
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t o = off;
@@ -2104,12 +2238,14 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   const size_t o_logits = take(B * c.vocab * 4);
   const size_t o_po = take(B * c.heads * kv->nch * c.hd * 4), o_pml = take(B * c.heads * kv->nch * 8);
   const size_t o_aval = take(B * (c.vocab / 16) * 4), o_aidx = take(B * (c.vocab / 16) * 4);
-  const size_t o_xn = take(B * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(B * c.q_dim * 2);
-  const size_t o_gate = take(B * c.hidden * 2);
+  // xn, attn and gate hold split rows [B, 2K] in split layers
+  const size_t o_xn = take(2 * B * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(2 * B * c.q_dim * 2);
+  const size_t o_gate = take(2 * B * c.hidden * 2), o_qdlo = take(B * c.q_dim * 2);
   char* sb = nullptr;
   e = hipMalloc(&sb, off);
   if (e != hipSuccess) {
     (void)hipFree(kv->cache);
+    if (kv->lo_cache) (void)hipFree(kv->lo_cache);
     delete kv;
     return fail(HB_E_OOM, "decode buffers: %s", hipGetErrorString(e));
   }
@@ -2130,12 +2266,15 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   kv->qd = (f16*)(sb + o_qd);
   kv->attn = (f16*)(sb + o_attn);
   kv->gate = (f16*)(sb + o_gate);
+  kv->qd_lo = (f16*)(sb + o_qdlo);
   hipStream_t st = m->ctx->stream();
   e = hipMemsetAsync(sb, 0, off, st);
   if (e == hipSuccess) e = fill_f16_zero(kv->cache, kv->cache_bytes / 2, st);
+  if (e == hipSuccess && kv->lo_cache) e = fill_f16_zero(kv->lo_cache, kv->lo_bytes / 2, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   if (e != hipSuccess) {
     (void)hipFree(kv->cache);
+    if (kv->lo_cache) (void)hipFree(kv->lo_cache);
     (void)hipFree(sb);
     delete kv;
     return fail(HB_E_DEVICE, "KV init: %s", hipGetErrorString(e));
@@ -2151,6 +2290,7 @@ extern "C" int hb_kv_destroy(hb_kv* kv) {
   if (kv->exec) (void)hipGraphExecDestroy(kv->exec);
   if (kv->graph) (void)hipGraphDestroy(kv->graph);
   (void)hipFree(kv->cache);
+  if (kv->lo_cache) (void)hipFree(kv->lo_cache);
   (void)hipFree(kv->sbase);
   delete kv;
   return HB_OK;
@@ -2176,7 +2316,7 @@ extern "C" int hb_kv_length(hb_kv* kv, int* out) {
 extern "C" int hb_kv_bytes(hb_kv* kv, uint64_t* out) {
   HB_INJECT_CHECK();
   if (!kv || !out) return fail(HB_E_INVALID, "null argument");
-  *out = kv->cache_bytes;
+  *out = kv->cache_bytes + kv->lo_bytes;
   return HB_OK;
 }
 
@@ -2195,7 +2335,7 @@ extern "C" int hb_prefill(hb_model* m, hb_kv* kv, const uint32_t* tokens, int S,
   const long T = (long)B * S;
   TRY(check_ids(tokens, T, c.vocab, "tokens"));
   TRY(ensure_rope(m, kv->ctx_cap));
-  TRY(ensure_workspace(m, T, (long)B * S_pad_of(S)));
+  TRY(ensure_workspace(m, T, (long)B * S_pad_of(S), kv->np > 0));
   TRY(ensure_decode_weights(m));
   Workspace& w = m->ws;
   hipStream_t st = m->ctx->stream();
@@ -2203,14 +2343,15 @@ extern "C" int hb_prefill(hb_model* m, hb_kv* kv, const uint32_t* tokens, int S,
   HIP_TRY(embedding(m->embed, w.tok, (int)T, c.dim, c.vocab, w.x, m->ctx->d_err, st));
   for (int l = 0; l < c.nlayers; ++l)
     TRY(run_layer(m, l, B, S, cache_target(kv, l), nullptr, l > 0,
-                  l + 1 < c.nlayers ? m->layers[l + 1].g1 : nullptr));
+                  l + 1 < c.nlayers ? m->layers[l + 1].g1 : nullptr, kv->np));
   // Last position of each sequence -> logits and greedy token.
+  const bool sf = kv->np == c.nlayers;  // every layer split: so are the final rows
   HIP_TRY(rmsnorm(w.x + (size_t)(S - 1) * c.dim, (long)S * c.dim, m->gamma_f, B, c.dim, c.norm_eps,
-                  kv->xn, nullptr, st));
+                  kv->xn, nullptr, st, sf));
   EpiLogits el{kv->logits, c.vocab, c.softcap};
   el.part_val = kv->amax_val;
   el.part_idx = kv->amax_idx;
-  HIP_TRY(gemv_logits(m->t_embed, kv->xn, nullptr, c.vocab, B, c.dim, el, st));
+  HIP_TRY(gemv_logits(m->t_embed, kv->xn, nullptr, c.vocab, B, c.dim, el, st, sf));
   HIP_TRY(argmax_reduce(kv->amax_val, kv->amax_idx, c.vocab / 16, B, kv->d_next, nullptr, nullptr,
                         nullptr, nullptr, st));
   HIP_TRY(set_int(kv->d_pos, S, st));

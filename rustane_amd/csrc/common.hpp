@@ -87,3 +87,32 @@ HB_DEV int xcd_remap(int wg, int n) {
 }
 
 HB_DEV float silu_f(float x) { return x * (1.0f / (1.0f + __expf(-x))); }
+
+// Two-term fp16 form of fp32 values, for the operands that must carry more
+// than fp16's 11 significant bits into an MFMA: x ~ hi + lo with hi = fp16(x)
+// and lo = fp16(x - hi) (x - hi is exact in fp32), about 22 bits in all. An
+// activation row of K features is then stored as 2K halves, [hi | lo], and a
+// product with it runs the k-steps of hi and of lo against the same weights
+// into the same fp32 accumulator ("split" rows).
+HB_DEV f16x4 f16x4_hi(f32x4 v) {
+  f16x4 h;
+  h.x = (f16)v.x;
+  h.y = (f16)v.y;
+  h.z = (f16)v.z;
+  h.w = (f16)v.w;
+  return h;
+}
+HB_DEV f16x4 f16x4_lo(f32x4 v, f16x4 h) {
+  f16x4 l;
+  l.x = (f16)(v.x - (float)h.x);
+  l.y = (f16)(v.y - (float)h.y);
+  l.z = (f16)(v.z - (float)h.z);
+  l.w = (f16)(v.w - (float)h.w);
+  return l;
+}
+// Stores fp16(v) at p and, for split rows, its low part lo_off halves later.
+HB_DEV void store_f16x4(f16* p, f32x4 v, size_t lo_off) {
+  const f16x4 h = f16x4_hi(v);
+  *(f16x4*)p = h;
+  if (lo_off) *(f16x4*)(p + lo_off) = f16x4_lo(v, h);
+}

@@ -47,11 +47,12 @@ template <int NPT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, long row_stride,
                                                       const float* __restrict__ gamma, int dim,
                                                       float eps, f16* __restrict__ out,
-                                                      float* __restrict__ rms_inv) {
+                                                      float* __restrict__ rms_inv, int split) {
   __shared__ float red[4];
   const int t = blockIdx.x;
   const float* xr = x + (size_t)t * row_stride;
-  f16* orow = out + (size_t)t * dim;
+  f16* orow = out + (size_t)t * dim * (split ? 2 : 1);
+  const size_t lo = split ? (size_t)dim : 0;  // split rows: [hi | lo]
   float ss = 0.f;
   if constexpr (NPT > 0) {
     f32x4 v[NPT], g[NPT];
@@ -66,12 +67,12 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     if (rms_inv && threadIdx.x == 0) rms_inv[t] = r;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-      f16x4 o;
-      o.x = (f16)(v[i].x * r * g[i].x);
-      o.y = (f16)(v[i].y * r * g[i].y);
-      o.z = (f16)(v[i].z * r * g[i].z);
-      o.w = (f16)(v[i].w * r * g[i].w);
-      *(f16x4*)(orow + threadIdx.x * 4 + i * 1024) = o;
+      f32x4 o;
+      o.x = v[i].x * r * g[i].x;
+      o.y = v[i].y * r * g[i].y;
+      o.z = v[i].z * r * g[i].z;
+      o.w = v[i].w * r * g[i].w;
+      store_f16x4(orow + threadIdx.x * 4 + i * 1024, o, lo);
     }
   } else {
     for (int c = threadIdx.x * 4; c < dim; c += 1024) {
@@ -84,30 +85,31 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     for (int c = threadIdx.x * 4; c < dim; c += 1024) {
       const f32x4 v = *(const f32x4*)(xr + c);
       const f32x4 g = *(const f32x4*)(gamma + c);
-      f16x4 o;
-      o.x = (f16)(v.x * r * g.x);
-      o.y = (f16)(v.y * r * g.y);
-      o.z = (f16)(v.z * r * g.z);
-      o.w = (f16)(v.w * r * g.w);
-      *(f16x4*)(orow + c) = o;
+      f32x4 o;
+      o.x = v.x * r * g.x;
+      o.y = v.y * r * g.y;
+      o.z = v.z * r * g.z;
+      o.w = v.w * r * g.w;
+      store_f16x4(orow + c, o, lo);
     }
   }
 }
 
 hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
-                   f16* out, float* rms_inv, hipStream_t st) {
+                   f16* out, float* rms_inv, hipStream_t st, bool split) {
   if (T <= 0) return hipSuccess;
+  const int sp = split ? 1 : 0;
   switch (dim % 1024 == 0 ? dim / 1024 : 0) {
 #define HB_NORM(n)                                                                              \
   case n:                                                                                       \
     hipLaunchKernelGGL(rmsnorm_kernel<n>, dim3(T), dim3(256), 0, st, x, row_stride, gamma, dim, \
-                       eps, out, rms_inv);                                                      \
+                       eps, out, rms_inv, sp);                                                  \
     break;
     HB_NORM(1) HB_NORM(2) HB_NORM(3) HB_NORM(4) HB_NORM(5) HB_NORM(6) HB_NORM(7) HB_NORM(8)
 #undef HB_NORM
     default:
       hipLaunchKernelGGL(rmsnorm_kernel<0>, dim3(T), dim3(256), 0, st, x, row_stride, gamma, dim,
-                         eps, out, rms_inv);
+                         eps, out, rms_inv, sp);
   }
   return hipGetLastError();
 }

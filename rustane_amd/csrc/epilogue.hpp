@@ -62,16 +62,26 @@ struct EpiResidual {
 // 4 consecutive features are therefore (h1[u], h1[u+1], h3[u], h3[u+1]) with
 // u = f0/2, and the SwiGLU gate (kernels/ffn_fused.rs:60-62) is formed in
 // registers: gate = silu(h1) * h3.
+// With split set, gate rows are split rows [T, 2*hidden] (hi | lo, common.hpp).
 struct EpiSwiGLU {
-  f16* gate;   // [T, hidden]
+  f16* gate;   // [T, hidden], or [T, 2*hidden] split
   float* tap;  // nullable [T, 2*hidden] = h1 | h3
   int hidden;
+  bool split = false;
   HB_DEV void operator()(int t, int f0, f32x4 v) const {
     const int u = f0 >> 1;
+    const float g0 = silu_f(v.x) * v.z, g1 = silu_f(v.y) * v.w;
     f16x2 g;
-    g.x = (f16)(silu_f(v.x) * v.z);
-    g.y = (f16)(silu_f(v.y) * v.w);
-    *(f16x2*)(gate + (size_t)t * hidden + u) = g;
+    g.x = (f16)g0;
+    g.y = (f16)g1;
+    f16* row = gate + (size_t)t * (split ? 2 * hidden : hidden) + u;
+    *(f16x2*)row = g;
+    if (split) {
+      f16x2 lo;
+      lo.x = (f16)(g0 - (float)g.x);
+      lo.y = (f16)(g1 - (float)g.y);
+      *(f16x2*)(row + hidden) = lo;
+    }
     if (tap) {
       float* r = tap + (size_t)t * 2 * hidden;
       r[u] = v.x;
@@ -131,6 +141,9 @@ struct EpiQKV {
   f16* vt;
   int vt_ld;
   float* tap;  // nullable [T, q+2kv] fp32 = Q_rope | K_rope | V
+  // Low parts of the two-term fp16 form (common.hpp) in the same layouts as
+  // q, k, v and vt; all NULL for plain fp16 outputs.
+  f16 *q_lo = nullptr, *k_lo = nullptr, *v_lo = nullptr, *vt_lo = nullptr;
   FastDiv div_S, div_hd;  // by S and hd; set by prepare() on the host
 
   __host__ void prepare() {
@@ -183,36 +196,47 @@ struct EpiQKV {
       o.z = v4.z * a.c1.x - v4.w * a.c1.y;
       o.w = v4.w * a.c1.x + v4.z * a.c1.y;
     }
-    f16x4 oh;
-    oh.x = (f16)o.x;
-    oh.y = (f16)o.y;
-    oh.z = (f16)o.z;
-    oh.w = (f16)o.w;
+    const f16x4 oh = f16x4_hi(o);
     // Q, K and V rows share one addressing form: base + b*bstride + h*hstride + s*hd + e
-    f16* base;
+    f16 *base, *base_lo;
     size_t bs, hs;
     int srow = s;
     if (r0 == 0) {
       base = q;
+      base_lo = q_lo;
       hs = (size_t)q_rows * hd;
       bs = (size_t)heads * hs;
       if (d_pos) srow = 0;  // decode keeps one Q row per sequence
     } else if (r0 == q_dim) {
       base = k;
+      base_lo = k_lo;
       bs = k_bstride;
       hs = k_hstride;
     } else {
       base = v;
+      base_lo = v_lo;
       bs = v_bstride;
       hs = v_hstride;
     }
-    if (base) *(f16x4*)(base + b * bs + h * hs + (size_t)srow * hd + e) = oh;
+    const size_t off = b * bs + h * hs + (size_t)srow * hd + e;
+    if (base) *(f16x4*)(base + off) = oh;
+    const bool lo = base_lo || (r0 == q_dim + kv_dim && vt_lo);
+    const f16x4 ol = lo ? f16x4_lo(o, oh) : f16x4{};
+    if (base_lo) *(f16x4*)(base_lo + off) = ol;
     if (r0 == q_dim + kv_dim && vt) {
-      f16* p = vt + ((size_t)b * kv_heads + h) * hd * vt_ld + (size_t)e * vt_ld + s;
+      const size_t vo = ((size_t)b * kv_heads + h) * hd * vt_ld + (size_t)e * vt_ld + s;
+      f16* p = vt + vo;
       p[0] = oh.x;
       p[vt_ld] = oh.y;
       p[2 * vt_ld] = oh.z;
       p[3 * vt_ld] = oh.w;
+      if (vt_lo) {
+        f16* pl = vt_lo + vo;
+        pl[0] = ol.x;
+        pl[vt_ld] = ol.y;
+        pl[2 * vt_ld] = ol.z;
+        pl[3 * vt_ld] = ol.w;
+      }
     }
     if (tap) *(f32x4*)(tap + (size_t)t * (q_dim + 2 * kv_dim) + f0) = o;
   }

@@ -4,15 +4,19 @@
 
 namespace hb {
 
+// kw: W's row length; K (the X row length and the reduction length) is kw,
+// or 2 * kw for split X rows (gemm_kernel.hpp). 0 means K.
 template <int FT, int TT, int WF, int WT, class Epi>
 static hipError_t launch_tile(const f16* W, const f16* X, int N, int T, int K, const Epi& epi,
-                              hipStream_t st, int splits = 1, GemmBatch bt = {}) {
+                              hipStream_t st, int splits = 1, GemmBatch bt = {}, int kw = 0) {
   const int tiles = ((N + FT - 1) / FT) * ((T + TT - 1) / TT);
   const int nk = K / 64, kq = (nk + splits - 1) / splits;
+  if (kw == 0) kw = K;
   if (nk < 1 || K % 64 || splits < 1 || (splits - 1) * kq >= nk) return hipErrorInvalidValue;
+  if ((kw != K && 2 * kw != K) || kw % 64) return hipErrorInvalidValue;
   if (bt.n < 1 || bt.n > 65535) return hipErrorInvalidValue;
   hipLaunchKernelGGL((gemm_nt_kernel<FT, TT, WF, WT, Epi>), dim3(tiles, splits, bt.n),
-                     dim3(WF * WT * 64), 0, st, W, X, N, T, K, kq, epi, bt.wbs, bt.xbs);
+                     dim3(WF * WT * 64), 0, st, W, X, N, T, K, kw, kq, epi, bt.wbs, bt.xbs);
   return hipGetLastError();
 }
 
@@ -51,7 +55,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
   __shared__ float red[4];
   const int t = blockIdx.x;
   const size_t row = (size_t)t * N;
-  f16* orow = no.xn + row;
+  f16* orow = no.xn + (no.split ? 2 * row : row);
+  const size_t lo = no.split ? (size_t)N : 0;  // split xn rows: [hi | lo]
   float ss = 0.f;
   if constexpr (NPT > 0) {
     f32x4 y[NPT], g[NPT];
@@ -85,12 +90,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
     const float rinv = 1.0f / sqrtf(ss * (1.0f / (float)N) + no.eps);
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-      f16x4 o;
-      o.x = (f16)(y[i].x * rinv * g[i].x);
-      o.y = (f16)(y[i].y * rinv * g[i].y);
-      o.z = (f16)(y[i].z * rinv * g[i].z);
-      o.w = (f16)(y[i].w * rinv * g[i].w);
-      *(f16x4*)(orow + threadIdx.x * 4 + i * 1024) = o;
+      f32x4 o;
+      o.x = y[i].x * rinv * g[i].x;
+      o.y = y[i].y * rinv * g[i].y;
+      o.z = y[i].z * rinv * g[i].z;
+      o.w = y[i].w * rinv * g[i].w;
+      store_f16x4(orow + threadIdx.x * 4 + i * 1024, o, lo);
     }
   } else {
     for (int c = threadIdx.x * 4; c < N; c += 1024) {
@@ -116,12 +121,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
     for (int c = threadIdx.x * 4; c < N; c += 1024) {
       const f32x4 y = *(const f32x4*)(e.out + row + c);  // this thread's own stores
       const f32x4 g = *(const f32x4*)(no.gamma + c);
-      f16x4 o;
-      o.x = (f16)(y.x * rinv * g.x);
-      o.y = (f16)(y.y * rinv * g.y);
-      o.z = (f16)(y.z * rinv * g.z);
-      o.w = (f16)(y.w * rinv * g.w);
-      *(f16x4*)(orow + c) = o;
+      f32x4 o;
+      o.x = y.x * rinv * g.x;
+      o.y = y.y * rinv * g.y;
+      o.z = y.z * rinv * g.z;
+      o.w = y.w * rinv * g.w;
+      store_f16x4(orow + c, o, lo);
     }
   }
 }
@@ -166,14 +171,14 @@ struct EpiMaxFT<E, std::void_t<decltype(E::kMaxFT)>> {
 
 template <class Epi>
 static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, const Epi& epi,
-                              const GemmScratch* scr, hipStream_t st, GemmBatch bt = {}) {
+                              const GemmScratch* scr, hipStream_t st, GemmBatch bt = {}, int kw = 0) {
   if ((long)N * K >= (1L << 31) || (long)T * K >= (1L << 31)) return hipErrorInvalidValue;
   if (bt.n != 1 && scr) return hipErrorInvalidValue;
   const int S = scr ? gemm_splits(N, T, K, scr->wgs) : 1;
   if (S > 1) {
     const size_t stride = (size_t)T * N;
     if (!scr->p || (size_t)S * stride > scr->floats) return hipErrorInvalidValue;
-    const hipError_t e = launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
+    const hipError_t e = launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S, {}, kw);
     if (e != hipSuccess) return e;
     const size_t n4 = stride / 4;
     const int grid = (int)std::min<size_t>((n4 + 255) / 256, 4096);
@@ -210,33 +215,33 @@ static hipError_t launch_gemm(const f16* W, const f16* X, int N, int T, int K, c
     }
   }
   if constexpr (max_ft >= 256) {
-    if (best == 0) return launch_tile<256, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
-    if (best == 4) return launch_tile<256, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
+    if (best == 0) return launch_tile<256, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt, kw);
+    if (best == 4) return launch_tile<256, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt, kw);
   }
   if constexpr (max_ft >= 192) {
-    if (best == 1) return launch_tile<192, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
-    if (best == 3) return launch_tile<192, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
+    if (best == 1) return launch_tile<192, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt, kw);
+    if (best == 3) return launch_tile<192, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt, kw);
   }
-  if (best == 2) return launch_tile<128, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
-  if (best == 5) return launch_tile<128, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
-  return launch_tile<64, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt);
+  if (best == 2) return launch_tile<128, 256, 2, 2>(W, X, N, T, K, epi, st, 1, bt, kw);
+  if (best == 5) return launch_tile<128, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt, kw);
+  return launch_tile<64, 128, 2, 2>(W, X, N, T, K, epi, st, 1, bt, kw);
 }
 
 hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st) {
   return launch_gemm(W, X, N, T, K, EpiStore{C, N}, nullptr, st);
 }
 hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
-                         const GemmScratch* scr, hipStream_t st) {
-  return launch_gemm(W, X, N, T, K, e, scr, st);
+                         const GemmScratch* scr, hipStream_t st, int kw) {
+  return launch_gemm(W, X, N, T, K, e, scr, st, {}, kw);
 }
 hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
-                              const NormOut& no, const GemmScratch* scr, hipStream_t st) {
+                              const NormOut& no, const GemmScratch* scr, hipStream_t st, int kw) {
   if (e.ld != N) return hipErrorInvalidValue;
   const int S = scr ? gemm_splits(N, T, K, scr->wgs) : 1;
   if (S > 1) {
     const size_t stride = (size_t)T * N;
     if (!scr->p || (size_t)S * stride > scr->floats || (long)N * K >= (1L << 31)) return hipErrorInvalidValue;
-    const hipError_t err = launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S);
+    const hipError_t err = launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S, {}, kw);
     if (err != hipSuccess) return err;
     switch (N % 1024 == 0 ? N / 1024 : 0) {
 #define HB_RN(n)                                                                                \
@@ -252,24 +257,24 @@ hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, c
     }
     return hipGetLastError();
   }
-  const hipError_t err = launch_gemm(W, X, N, T, K, e, nullptr, st);
+  const hipError_t err = launch_gemm(W, X, N, T, K, e, nullptr, st, {}, kw);
   if (err != hipSuccess) return err;
-  return rmsnorm(e.out, N, no.gamma, T, N, no.eps, no.xn, nullptr, st);
+  return rmsnorm(e.out, N, no.gamma, T, N, no.eps, no.xn, nullptr, st, no.split);
 }
 hipError_t gemm_swiglu(const f16* W, const f16* X, int N, int T, int K, const EpiSwiGLU& e,
-                       hipStream_t st) {
-  return launch_gemm(W, X, N, T, K, e, nullptr, st);
+                       hipStream_t st, int kw) {
+  return launch_gemm(W, X, N, T, K, e, nullptr, st, {}, kw);
 }
 hipError_t gemm_logits(const f16* W, const f16* X, int N, int T, int K, const EpiLogits& e,
-                       hipStream_t st) {
-  return launch_gemm(W, X, N, T, K, e, nullptr, st);
+                       hipStream_t st, int kw) {
+  return launch_gemm(W, X, N, T, K, e, nullptr, st, {}, kw);
 }
 hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQKV& e,
-                    hipStream_t st) {
+                    hipStream_t st, int kw) {
   if (e.S < 1 || e.hd < 1) return hipErrorInvalidValue;
   EpiQKV ep = e;
   ep.prepare();
-  return launch_gemm(W, X, N, T, K, ep, nullptr, st);
+  return launch_gemm(W, X, N, T, K, ep, nullptr, st, {}, kw);
 }
 
 

@@ -80,11 +80,15 @@ struct EpiSumSq<E, std::void_t<decltype(E::kSumSq)>> : std::bool_constant<E::kSu
 // Batches: blockIdx.z selects one of gridDim.z independent products whose
 // operands start wbs and xbs halfs apart (attention backward: one per
 // sequence and KV head); epilogues that care read blockIdx.z themselves.
+//
+// Split X rows (common.hpp): X rows hold K = 2*kw halves [hi | lo] while W
+// rows hold kw; k-slice k0 reads W columns k0 mod kw, so the hi and the lo
+// halves of each row meet the same weights. kw = K otherwise.
 template <int FT, int TT, int WF, int WT, class Epi>
 __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __restrict__ W,
                                                                  const f16* __restrict__ X, int N,
-                                                                 int T, int K, int kq, Epi epi,
-                                                                 size_t wbs, size_t xbs) {
+                                                                 int T, int K, int kw, int kq,
+                                                                 Epi epi, size_t wbs, size_t xbs) {
   W += blockIdx.z * wbs;
   X += blockIdx.z * xbs;
   constexpr int NT = WF * WT * 64;
@@ -125,7 +129,7 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   const f16* xb = X + c0 * 8;
   int woff[WL], xoff[XL];
 #pragma unroll
-  for (int i = 0; i < WL; ++i) woff[i] = min(f_base + r0 + RSTEP * i, N - 1) * K;
+  for (int i = 0; i < WL; ++i) woff[i] = min(f_base + r0 + RSTEP * i, N - 1) * kw;
 #pragma unroll
   for (int i = 0; i < XL; ++i) xoff[i] = min(t_base + r0 + RSTEP * i, T - 1) * K;
 
@@ -134,8 +138,9 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   f16x8 wreg[2][WL], xreg[2][XL];
   auto gload = [&](auto rs, int k0) {
     constexpr int R = decltype(rs)::value;
+    const int kw0 = k0 < kw ? k0 : k0 - kw;  // wave-uniform
 #pragma unroll
-    for (int i = 0; i < WL; ++i) wreg[R][i] = *(const f16x8*)(wb + woff[i] + k0);
+    for (int i = 0; i < WL; ++i) wreg[R][i] = *(const f16x8*)(wb + woff[i] + kw0);
 #pragma unroll
     for (int i = 0; i < XL; ++i) xreg[R][i] = *(const f16x8*)(xb + xoff[i] + k0);
   };

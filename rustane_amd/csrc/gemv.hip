@@ -206,10 +206,14 @@ HB_DEV void argmax_partial(const EpiLogits& e, f32x4 v, int f0, int col, int B) 
 // in LDS by stage_norm (PRO_NORM) or stage_attn (PRO_ATTN).
 enum { PRO_NONE = 0, PRO_NORM = 1, PRO_ATTN = 2 };
 
-template <int KS, int U, class Epi, int PRO>
+// SPLIT (PRO_NONE only): X rows are split rows [B][2K] (common.hpp); every
+// weight fragment meets the hi and the lo half of the B operand, two MFMAs
+// into the same accumulator, so the weight stream is read once.
+template <int KS, int U, class Epi, int PRO, bool SPLIT>
 __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__ Wt,
                                                        const f16* __restrict__ X, int N, int B,
                                                        int K, Epi epi, NormIn nin, AttnIn ain) {
+  static_assert(!SPLIT || PRO == PRO_NONE, "split rows come from memory");
   extern __shared__ f16x8 s_dyn[];  // staged B-operand rows [B][xn_ld(K)]
   __shared__ f32x4 red[KS][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -221,10 +225,14 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
   const bool xok = col < B;
   const f16* s_x = (const f16*)s_dyn;
   const f16* xrow = PRO != PRO_NONE ? s_x + (xok ? col : 0) * xn_ld(K) + kq
-                                     : X + (size_t)(xok ? col : 0) * K + kq;
+                                     : X + (size_t)(xok ? col : 0) * (SPLIT ? 2 * K : K) + kq;
   auto bop = [&](int s) -> f16x8 {
     const f16x8 zero8 = {};
     return xok ? *(const f16x8*)(xrow + (size_t)s * 32) : zero8;
+  };
+  auto bopl = [&](int s) -> f16x8 {  // low half of a split row
+    const f16x8 zero8 = {};
+    return xok ? *(const f16x8*)(xrow + K + (size_t)s * 32) : zero8;
   };
 
   f32x4 acc = {};
@@ -249,18 +257,23 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
     s += npf;
   }
   for (; s + U <= s_end; s += U) {
-    f16x8 a[U], bx[U];
+    f16x8 a[U], bx[U], bl[SPLIT ? U : 1];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       a[u] = __builtin_nontemporal_load(wp + (size_t)(s + u) * 64);
       bx[u] = bop(s + u);
+      if constexpr (SPLIT) bl[u] = bopl(s + u);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bx[u], acc, 0, 0, 0);
+    for (int u = 0; u < U; ++u) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bx[u], acc, 0, 0, 0);
+      if constexpr (SPLIT) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bl[u], acc, 0, 0, 0);
+    }
   }
   for (; s < s_end; ++s) {
     const f16x8 a = __builtin_nontemporal_load(wp + (size_t)s * 64);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop(s), acc, 0, 0, 0);
+    if constexpr (SPLIT) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bopl(s), acc, 0, 0, 0);
   }
 
   red[wave][lane] = acc;
@@ -284,8 +297,15 @@ constexpr int GEMV_U = 4;   // 1 KB weight loads in flight per wave
 
 template <class Epi>
 hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, const AttnIn* ain, int N,
-                       int B, int K, const Epi& epi, hipStream_t st) {
+                       int B, int K, const Epi& epi, hipStream_t st, bool split = false) {
   if (B < 1 || B > 16 || N % 16 || K % 32) return hipErrorInvalidValue;
+  if (split) {
+    if (nin || ain) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE, true>), dim3(N / 16),
+                       dim3(GEMV_KS * 64), 0, st, (const f16x8*)Wt, X, N, B, K, epi, NormIn{},
+                       AttnIn{});
+    return hipGetLastError();
+  }
   const dim3 grid(N / 16), block(GEMV_KS * 64);
   const size_t lds = (size_t)B * (K + 8) * 2;
   // Only the projections fed by a norm (QKV, W1|W3, logits) have a norm
@@ -295,7 +315,7 @@ hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, const Att
   if (nin) {
     if constexpr (kNorm) {
       if (!gemv_norm_fits(B, K)) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NORM>), grid, block, lds, st,
+      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NORM, false>), grid, block, lds, st,
                          (const f16x8*)Wt, nullptr, N, B, K, epi, *nin, AttnIn{});
     } else {
       return hipErrorInvalidValue;
@@ -303,13 +323,13 @@ hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, const Att
   } else if (ain) {
     if constexpr (kAttn) {
       if (!gemv_attn_fits(B, K, ain->nch) || ain->H * ain->hd != K || ain->hd % 8) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_ATTN>), grid, block, lds, st,
+      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_ATTN, false>), grid, block, lds, st,
                          (const f16x8*)Wt, nullptr, N, B, K, epi, NormIn{}, *ain);
     } else {
       return hipErrorInvalidValue;
     }
   } else {
-    hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE>), grid, block, 0, st,
+    hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE, false>), grid, block, 0, st,
                        (const f16x8*)Wt, X, N, B, K, epi, NormIn{}, AttnIn{});
   }
   return hipGetLastError();
@@ -325,23 +345,23 @@ bool gemv_attn_fits(int B, int K, int nch) {
 }
 
 hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, int B, int K,
-                         const EpiResidual& e, hipStream_t st) {
-  return launch_gemv(Wt, X, nullptr, ain, N, B, K, e, st);
+                         const EpiResidual& e, hipStream_t st, bool split) {
+  return launch_gemv(Wt, X, nullptr, ain, N, B, K, e, st, split);
 }
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const EpiSwiGLU& e, hipStream_t st) {
-  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st);
+                       const EpiSwiGLU& e, hipStream_t st, bool split) {
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st, split);
 }
 hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const EpiLogits& e, hipStream_t st) {
-  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st);
+                       const EpiLogits& e, hipStream_t st, bool split) {
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st, split);
 }
 hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                    const EpiQKV& e, hipStream_t st) {
+                    const EpiQKV& e, hipStream_t st, bool split) {
   if (e.S < 1 || e.hd < 1) return hipErrorInvalidValue;
   EpiQKV ep = e;
   ep.prepare();
-  return launch_gemv(Wt, X, nin, nullptr, N, B, K, ep, st);
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, ep, st, split);
 }
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st) {
   return launch_gemv(Wt, X, nullptr, nullptr, N, B, K, EpiStore{C, N}, st);

@@ -22,23 +22,27 @@ struct GemmBatch {
 // (1 = none), aiming at wgs workgroups; it needs splits * T * N floats.
 int gemm_splits(int N, int T, int K, int wgs = 256);
 hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st);
+// kw (the residual, SwiGLU and QKV projections): 0 for plain X rows of K
+// halves; for split X rows (common.hpp) K = 2 * kw with kw the weights' row
+// length.
 hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
-                         const GemmScratch* scr, hipStream_t st);
+                         const GemmScratch* scr, hipStream_t st, int kw = 0);
 // Residual projection followed by the RMSNorm of its output rows into xn
 // (fused into the split-K reduction when the shape splits).
 struct NormOut {
   const float* gamma;
   float eps;
-  f16* xn;  // [T, N]
+  f16* xn;             // [T, N], or split rows [T, 2N]
+  bool split = false;
 };
 hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
-                              const NormOut& no, const GemmScratch* scr, hipStream_t st);
+                              const NormOut& no, const GemmScratch* scr, hipStream_t st, int kw = 0);
 hipError_t gemm_swiglu(const f16* W, const f16* X, int N, int T, int K, const EpiSwiGLU& e,
-                       hipStream_t st);
+                       hipStream_t st, int kw = 0);
 hipError_t gemm_logits(const f16* W, const f16* X, int N, int T, int K, const EpiLogits& e,
-                       hipStream_t st);
+                       hipStream_t st, int kw = 0);
 hipError_t gemm_qkv(const f16* W, const f16* X, int N, int T, int K, const EpiQKV& e,
-                    hipStream_t st);
+                    hipStream_t st, int kw = 0);
 
 // Training products (the epilogues are documented in epilogue.hpp). All take
 // K % 64 == 0; token-dimension (K = tokens) operands are zero-padded to it.
@@ -90,14 +94,16 @@ struct AttnIn {
 };
 constexpr int GEMV_ATTN_MAXCH = 8;  // B * nch limit of the in-GEMV combine
 bool gemv_attn_fits(int B, int K, int nch);
+// split: X rows are split rows [B, 2K] (common.hpp), read from memory (no
+// prologue); the weights are still [N, K].
 hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, int B, int K,
-                         const EpiResidual& e, hipStream_t st);
+                         const EpiResidual& e, hipStream_t st, bool split = false);
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const EpiSwiGLU& e, hipStream_t st);
+                       const EpiSwiGLU& e, hipStream_t st, bool split = false);
 hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const EpiLogits& e, hipStream_t st);
+                       const EpiLogits& e, hipStream_t st, bool split = false);
 hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                    const EpiQKV& e, hipStream_t st);
+                    const EpiQKV& e, hipStream_t st, bool split = false);
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st);
 // Greedy token from the logits GEMV's argmax partials ([B][nblk] each). With
 // tok != NULL it also feeds the token back (tok, hist row pos - *d_pos0) and
@@ -114,9 +120,12 @@ struct AttnPrefill {
   size_t k_bstride, k_hstride;
   const f16* vt;  // [B][KVH][hd][vt_ld]
   int vt_ld;
-  f16* out;  // [B*S][H*hd]
+  f16* out;  // [B*S][H*hd], or split rows [B*S][2*H*hd] when q_lo is set
   int B, S, H, KVH, hd;
   float scale;  // 1/sqrt(hd)
+  // Two-term fp16 inputs (common.hpp): low parts of q, k and vt in the same
+  // layouts, all set or all NULL.
+  const f16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
 };
 hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st);
 
@@ -131,6 +140,10 @@ struct AttnDecode {
   float* part_o;   // [B][H][nchunks][hd] unnormalised chunk outputs
   float* part_ml;  // [B][H][nchunks][2] chunk (max, sum) in log2 units
   f16* out;        // [B][H*hd], written by attention_combine
+  // Two-term fp16 inputs (common.hpp): low parts of q, k and v in the same
+  // layouts, all set or all NULL; attention_combine then writes split rows
+  // [B][2*H*hd].
+  const f16 *q_lo = nullptr, *k_lo = nullptr, *v_lo = nullptr;
 };
 int attn_decode_chunks(int ctx_max);
 int attn_decode_chunk_keys();
@@ -142,9 +155,10 @@ hipError_t attention_combine(const AttnDecode& p, hipStream_t st);
 // ---- elementwise / reductions (elementwise.hip) ----
 hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int vocab, float* x,
                      int* err, hipStream_t st);
-// Rows r < T of x at x + r*row_stride (floats), dim contiguous.
+// Rows r < T of x at x + r*row_stride (floats), dim contiguous; out rows are
+// [T, dim], or split rows [T, 2*dim] (common.hpp).
 hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
-                   f16* out, float* rms_inv, hipStream_t st);
+                   f16* out, float* rms_inv, hipStream_t st, bool split = false);
 // Per-row cross-entropy (targets nullable) and argmax (nullable).
 hipError_t cross_entropy(const float* logits, const uint32_t* targets, int T, int vocab,
                          float* loss, uint32_t* argmax, int* err, hipStream_t st);

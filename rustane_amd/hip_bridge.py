@@ -122,6 +122,8 @@ SIGNATURES = {
     "hb_model_get_config": [_P, C.POINTER(hb_model_config)],
     "hb_model_weight_bytes": [_P, C.POINTER(C.c_uint64)],
     "hb_model_set_softcap": [_P, _F],
+    "hb_model_set_precise_layers": [_P, _I],
+    "hb_model_get_precise_layers": [_P, C.POINTER(C.c_int)],
     "hb_model_upload_layer": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "hb_model_upload_embed": [_P, _P, _P],
     "hb_model_init_synthetic": [_P, _U64, _F],
@@ -339,6 +341,15 @@ class Model:
 
     def reserve(self, B: int, S: int) -> None:
         call("hb_model_reserve", self.handle, B, S)
+
+    def set_precise_layers(self, n: int) -> None:
+        """hb_model_set_precise_layers: the first n layers run on two-term fp16 operands."""
+        call("hb_model_set_precise_layers", self.handle, n)
+
+    def precise_layers(self) -> int:
+        n = C.c_int()
+        call("hb_model_get_precise_layers", self.handle, C.byref(n))
+        return n.value
 
     def train_forward(self, tokens, targets, batch: int, seq: int, views=()):
         """hb_train_forward: the training forward of `batch` sequences of `seq`

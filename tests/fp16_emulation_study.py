@@ -179,6 +179,9 @@ def main():
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--seq", type=int, default=512)
     ap.add_argument("--variants", default=None, help="';'-separated variant specs")
+    ap.add_argument("--vs-unrounded", action="store_true",
+                    help="compare with fp32 arithmetic on the unrounded fp32 weights instead "
+                         "(adds the weights' own fp16 rounding to every variant)")
     a = ap.parse_args()
     seed = a.seed if a.seed is not None else {"7b": 46, "5b": 44}.get(a.shape, 42)
     cfg = {"7b": ModelConfig.llama_7b(), "5b": ModelConfig.llama_5b(),
@@ -192,11 +195,16 @@ def main():
     t0 = time.time()
     res = dict(zip(specs, run(cfg, ow, tok, S, specs)))
     L0, l0 = res["fp32"]
-    print(f"{a.shape} seq {S} seed {seed}: each variant vs all-fp32 operands on the device's weights "
-          f"({time.time() - t0:.0f} s)")
+    against = "all-fp32 operands on the device's weights"
+    if a.vs_unrounded:
+        ow32 = synthetic_oracle_weights(cfg, 1234, round16=False, cache=False)
+        (L0, l0), = run(cfg, ow32, tok, S, ["fp32"])
+        against = "fp32 arithmetic on the unrounded fp32 weights"
+        specs = specs + ["fp32"] if "fp32" in specs else specs
+    print(f"{a.shape} seq {S} seed {seed}: each variant vs {against} ({time.time() - t0:.0f} s)")
     print(f"{'variant':<24} {'max|dlogit|':>11} {'rms dlogit':>10} {'max rel dloss':>13} {'top-1':>7}")
-    for s in specs:
-        if s == "fp32":
+    for s in dict.fromkeys(specs):
+        if s == "fp32" and not a.vs_unrounded:
             continue
         L1, l1 = res[s]
         dl = L1 - L0

@@ -67,10 +67,10 @@ pytestmark = pytest.mark.gpu
 
 LOSS_RTOL = 1e-3
 LOGIT_ATOL = 2e-2
-TOP1_PREFILL_MIN = 0.98   # prefill positions, per sequence (see above)
-BAR_5B, BAR_7B = 2.0, 3.0  # bar multipliers of the deep shapes (see above)
+TOP1_PREFILL_MIN = 0.995   # prefill positions, per sequence
+BAR_5B, BAR_7B = 1.0, 1.0  # the contract's bars at every shape
 BAR_7B_UNROUNDED = 4.0
-TOP1_7B = 0.975
+TOP1_7B = 0.995
 SEED = 1234
 STD = 0.02
 
@@ -304,7 +304,7 @@ def test_7b_decode_b1_teacher_forced_matches_oracle(m7b, tok7, orc7, orc7_steps)
         # and 41 positions measure the rate coarsely (2 flips measured); the
         # seq-2048 prefill of the same sequence measures it over 2048 (98.5%).
         assert max(errs) <= LOGIT_ATOL * BAR_7B
-        assert len(agree) - sum(agree) <= 4
+        assert np.mean(agree) >= TOP1_7B
         assert dec.length() == P7 + DEC_STEPS
     finally:
         dec.kv.close()

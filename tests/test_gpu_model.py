@@ -307,3 +307,86 @@ def test_oversize_token_counts_are_rejected_before_any_allocation(gpu):
     # the largest accepted count is reserved normally
     S_ok = (1 << 31) // 32000 // 64 * 64 - 64
     hb.call("hb_model_reserve", k.model.handle, 1, S_ok)
+
+
+def _emulated_logits(cfg, ow16, tok, S, np_layers):
+    """The oracle's arithmetic with fp16 rounding where the device rounds, and
+    two-term fp16 operands in the first np_layers layers (the device's
+    hb_model_set_precise_layers); tests/fp16_emulation_study.py."""
+    from tests.fp16_emulation_study import run
+    spec = "all" + (f",*@0:{np_layers}=2" if np_layers else "")
+    if np_layers == cfg.nlayers:  # then the final norm's rows are split too
+        spec += ",xf=2"
+    (lg, _), = run(cfg, ow16, tok, S, [spec], log_every=10 ** 9)
+    return lg
+
+
+@pytest.mark.parametrize("shape", ["tiny", "48m"])
+def test_precise_layers_track_their_emulation(gpu, shape):
+    """Two-term fp16 operands in the first n layers (n = 0, 1, all): the
+    device's distance from the fp32 oracle on its own fp16 weights follows the
+    CPU emulation of exactly those roundings (within 2.5x of its max |dlogit|,
+    a maximum over S x vocab entries, plus 2e-4 for fp32 summation order and
+    exp2-based softmax; measured 48M: 1.378e-3 / 1.361e-3 all-fp16, 1.104e-3 /
+    1.009e-3 one split layer, 6.4e-5 / 2.2e-6 all split). With every layer
+    split (the final norm's rows too) the forward is fp32 arithmetic on fp16
+    weights to fp32 accumulation order, 20x below the fp16-operand distance: a
+    lost or misplaced low half anywhere would show at the fp16 level."""
+    from tests._util import f16_round
+    cfg = tiny_config() if shape == "tiny" else ModelConfig.llama_48m()
+    S = cfg.seq if shape == "tiny" else 128
+    w = ModelWeights.synthetic(cfg, seed=61, std=0.02)
+    ow = oracle_weights(w)
+    ow16 = O.ModelW(embed=f16_round(ow.embed), gamma_final=ow.gamma_final,
+                    layers=[O.LayerW(**{n: (f16_round(getattr(l, n)) if n.startswith("w") else getattr(l, n))
+                                        for n in O.LayerW.__dataclass_fields__}) for l in ow.layers])
+    tok = tokens_for(cfg, S + 1, seed=62)
+    from tests.fp16_emulation_study import run
+    (ref, _), = run(cfg, ow16, tok, S, ["fp32"], log_every=10 ** 9)
+    k = CompiledKernels.compile(cfg)
+    errs = {}
+    for n in (0, 1, cfg.nlayers):
+        k.model.set_precise_layers(n)
+        assert k.model.precise_layers() == n
+        dev = E.forward_logits(cfg, k, w, tok[:-1], tok[1:]).logits.reshape(S, cfg.vocab)
+        emu = _emulated_logits(cfg, ow16, tok, S, n)
+        errs[n] = (np.abs(dev - ref).max(), np.abs(emu - ref).max())
+        print(f"{shape} precise layers {n}: max|dlogit| device {errs[n][0]:.3e} emulated {errs[n][1]:.3e}",
+              flush=True)
+        assert errs[n][0] <= 2.5 * errs[n][1] + 2e-4, (n, errs[n])
+    assert errs[cfg.nlayers][0] < errs[0][0] / 10
+    with pytest.raises(hb.HipBridgeError) as e:
+        k.model.set_precise_layers(cfg.nlayers + 1)
+    assert e.value.code == hb.HB_E_INVALID
+
+
+@pytest.mark.parametrize("n", [0, 2])
+def test_decode_equals_prefill_rows_with_precise_layers(gpu, n):
+    """Decode with 0 and 2 split-operand layers (low parts of K/V in their own
+    cache, separate norm/combine launches) reproduces the device's prefill
+    rows, for two sequences at once."""
+    cfg = ModelConfig.llama_48m()
+    w = ModelWeights.synthetic(cfg, seed=63, std=0.02)
+    k = CompiledKernels.compile(cfg)
+    k.model.set_precise_layers(n)
+    B, S, P = 2, 48, 30
+    tok = tokens_for(cfg, B * S, seed=64).reshape(B, S)
+    full = E.forward_logits(cfg, k, w, tok, None, batch=B).logits.reshape(B, S, cfg.vocab)
+    dec = E.Decoder(k, batch=B, ctx_max=S)
+    gl, _ = dec.prefill(tok[:, :P])
+    assert np.abs(gl - full[:, P - 1]).max() < 2e-3
+    worst = 0.0
+    for p in range(P, S):
+        gl, _ = dec.step(tok[:, p])
+        worst = max(worst, float(np.abs(gl - full[:, p]).max()))
+    print(f"precise layers {n}: decode vs prefill rows max |dlogit| {worst:.2e}", flush=True)
+    assert worst < 2e-3
+    # the greedy graph replays the same split layers
+    d2 = E.Decoder(k, batch=B, ctx_max=S)
+    _, nxt = d2.prefill(tok[:, :P])
+    out = d2.greedy(nxt, 4)
+    d3 = E.Decoder(k, batch=B, ctx_max=S)
+    _, cur = d3.prefill(tok[:, :P])
+    for i in range(4):
+        _, cur = d3.step(cur)
+        np.testing.assert_array_equal(out[i], cur)
