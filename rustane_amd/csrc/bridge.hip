@@ -136,6 +136,23 @@ struct hb_model {
   // weights out of date after any weight write.
   TrainState* train = nullptr;
   bool wt_stale = true;
+  // Forward of one launch sequence replayed from a HIP graph: after a first
+  // eager run of a call shape (fwd_seen), the next identical call captures
+  // it (fwd_exec); later identical calls replay it with one launch.
+  struct FwdKey {
+    int B = 0, S = 0, np = -1, epoch = -1;
+    float softcap = 0.f;
+    const void *tok = nullptr, *tgt = nullptr, *loss = nullptr, *logits = nullptr, *mean = nullptr;
+    const void *ws = nullptr, *splitk = nullptr;
+    bool operator==(const FwdKey& o) const {
+      return B == o.B && S == o.S && np == o.np && epoch == o.epoch && softcap == o.softcap &&
+             tok == o.tok && tgt == o.tgt && loss == o.loss && logits == o.logits && mean == o.mean &&
+             ws == o.ws && splitk == o.splitk;
+    }
+  };
+  FwdKey fwd_seen, fwd_key;
+  hipGraph_t fwd_graph = nullptr;
+  hipGraphExec_t fwd_exec = nullptr;
   // The first precise_layers layers of a prefill or decode forward run on
   // two-term fp16 operands (common.hpp): their GEMM/GEMV inputs, Q, K, V and
   // attention probabilities carry ~22 bits instead of fp16's 11. Rounding in
@@ -746,6 +763,8 @@ extern "C" int hb_model_destroy(hb_model* m) {
   if (m->rope) (void)hipFree(m->rope);
   if (m->staging) (void)hipFree(m->staging);
   if (m->ws.base) (void)hipFree(m->ws.base);
+  if (m->fwd_exec) (void)hipGraphExecDestroy(m->fwd_exec);
+  if (m->fwd_graph) (void)hipGraphDestroy(m->fwd_graph);
   train_free(m->train);
   delete m;
   return HB_OK;
@@ -1817,6 +1836,21 @@ extern "C" int hb_model_reserve(hb_model* m, int B, int S) {
   return ensure_workspace(m, (long)B * S, (long)B * S_pad_of(S));
 }
 
+static int forward_enqueue(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets, int B, int S,
+                           float* d_loss, float* d_logits, float* d_mean);
+
+// HB_NO_GRAPH=1 runs the forward and decode launches eagerly (for profiling
+// individual launches).
+static bool graphs_enabled() {
+  const char* s = getenv("HB_NO_GRAPH");
+  return !(s && s[0] == '1');
+}
+
+// The forward's launches depend only on the call's shape, pointers, softcap
+// and split layers (and the addresses of the workspace, split-K scratch and
+// RoPE table); the weights are read at run time. Repeated identical calls --
+// a serving or benchmark loop -- replay one captured graph instead of ~7
+// launches per layer, which is what bounds shallow or narrow models.
 static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets,
                                int B, int S, float* d_loss, float* d_logits, float* d_mean) {
   const hb_model_config& c = m->cfg;
@@ -1824,8 +1858,56 @@ static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint
   TRY(check_token_count(c, B, S));
   if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
   if (!d_tokens) return fail(HB_E_INVALID, "null tokens");
-  const long T = (long)B * S, Tp = (long)B * S_pad_of(S);
-  TRY(ensure_workspace(m, T, Tp));
+  TRY(ensure_workspace(m, (long)B * S, (long)B * S_pad_of(S)));
+  if (!graphs_enabled()) return forward_enqueue(m, d_tokens, d_targets, B, S, d_loss, d_logits, d_mean);
+  auto key = [&]() {
+    hb_model::FwdKey k;
+    k.B = B; k.S = S; k.np = m->precise_layers; k.epoch = m->graph_epoch; k.softcap = c.softcap;
+    k.tok = d_tokens; k.tgt = d_targets; k.loss = d_loss; k.logits = d_logits; k.mean = d_mean;
+    k.ws = m->ws.base; k.splitk = m->splitk;
+    return k;
+  };
+  hb_ctx* ctx = m->ctx;
+  const hb_model::FwdKey k = key();
+  if (m->fwd_exec && k == m->fwd_key) {
+    HIP_TRY(hipGraphLaunch(m->fwd_exec, ctx->stream()));
+    return HB_OK;
+  }
+  if (!(k == m->fwd_seen)) {  // first call of this shape: eager (it may allocate)
+    TRY(forward_enqueue(m, d_tokens, d_targets, B, S, d_loss, d_logits, d_mean));
+    m->fwd_seen = key();
+    return HB_OK;
+  }
+  if (m->fwd_exec) (void)hipGraphExecDestroy(m->fwd_exec);
+  if (m->fwd_graph) (void)hipGraphDestroy(m->fwd_graph);
+  m->fwd_exec = nullptr;
+  m->fwd_graph = nullptr;
+  m->fwd_key = hb_model::FwdKey{};
+  // the capture stream starts after the work already queued on the context stream
+  HIP_TRY(hipStreamSynchronize(ctx->stream()));
+  hipStream_t saved = ctx->user;
+  ctx->user = ctx->capture;
+  HIP_TRY(hipStreamBeginCapture(ctx->capture, hipStreamCaptureModeThreadLocal));
+  const int r = forward_enqueue(m, d_tokens, d_targets, B, S, d_loss, d_logits, d_mean);
+  hipGraph_t gr = nullptr;
+  const hipError_t e = hipStreamEndCapture(ctx->capture, &gr);
+  ctx->user = saved;
+  if (r != HB_OK || e != hipSuccess) {
+    if (gr) (void)hipGraphDestroy(gr);
+    if (r != HB_OK) return r;
+    return fail(HB_E_DEVICE, "forward graph capture failed: %s", hipGetErrorString(e));
+  }
+  m->fwd_graph = gr;
+  HIP_TRY(hipGraphInstantiate(&m->fwd_exec, gr, nullptr, nullptr, 0));
+  m->fwd_key = k;
+  HIP_TRY(hipGraphLaunch(m->fwd_exec, ctx->stream()));
+  return HB_OK;
+}
+
+static int forward_enqueue(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets, int B, int S,
+                           float* d_loss, float* d_logits, float* d_mean) {
+  const hb_model_config& c = m->cfg;
+  const long T = (long)B * S;
   Workspace& w = m->ws;
   hipStream_t st = m->ctx->stream();
   HIP_TRY(embedding(m->embed, d_tokens, (int)T, c.dim, c.vocab, w.x, m->ctx->d_err, st));
@@ -2150,10 +2232,6 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
   return HB_OK;
 }
 
-bool graphs_enabled() {
-  const char* s = getenv("HB_NO_GRAPH");
-  return !(s && s[0] == '1');
-}
 
 int launch_decode_step(hb_kv* kv) {
   hb_ctx* ctx = kv->model->ctx;

@@ -33,7 +33,11 @@ that covers a (point, layer) wins; "all" / "fp32" set every point to 16 / 32,
 "<point>=<16|2|32>" sets one point, "<point>@a:b=<mode>" sets it in layers
 a..b-1 only, "*" stands for every point; xf counts as layer nlayers. Points
 no token covers stay fp32. Default: fp32, all, each point alone, all but each
-point.
+point. With --vs-unrounded the weights may differ too: "w@a:b=32" keeps the
+unrounded fp32 weights of layers a..b-1, "e=32" the embedding rows the input
+gathers, "elog=32" the embedding in the logits product (fp16 otherwise, as
+the device holds them); every variant is then compared with fp32 arithmetic
+on the unrounded weights.
 
 Inputs: the first sequence of tokens_for(cfg, S + 1, seed) (the same draw as
 the full-size tests), seq 512, synthetic N(0, 0.02) weights of seed 1234.
@@ -68,9 +72,14 @@ def r2x16(a):
 ROUND = {"32": lambda a: a, "16": r16, "2": r2x16}
 
 
+WEIGHT_POINTS = ("w", "e", "elog")  # layer weights, embedding rows gathered, embedding in the logits
+
+
 def parse_variant(spec):
-    """-> {point: [(first layer, end layer, mode), ...]}; the last matching rule wins."""
-    rules = {p: [] for p in POINTS}
+    """-> {point: [(first layer, end layer, mode), ...]}; the last matching rule wins.
+    Weight points (w, e, elog) default to 16 (the device's fp16 weights); "=32"
+    uses the unrounded fp32 values (run() then needs unrounded weights)."""
+    rules = {p: [] for p in POINTS + WEIGHT_POINTS}
     inf = 1 << 30
     for tok in filter(None, (t.strip() for t in spec.split(","))):
         if tok in ("all", "fp32"):
@@ -81,10 +90,12 @@ def parse_variant(spec):
         pt, _, rng = lhs.partition("@")
         a, _, b = rng.partition(":")
         lo, hi = (int(a or 0), int(b) if b else inf) if rng else (0, inf)
-        if pt not in POINTS + ("*",) or mode not in ROUND:
+        if pt not in POINTS + WEIGHT_POINTS + ("*",) or mode not in ROUND:
             raise SystemExit(f"bad variant token {tok!r}")
         for p in (POINTS if pt == "*" else (pt,)):
             rules[p].append((lo, hi, mode))
+    for p in WEIGHT_POINTS:
+        rules[p] = [(0, inf, "16")] + rules[p]
     return rules
 
 
@@ -107,6 +118,9 @@ class Stream:
         """{point: rounding function} in this layer (the final norm counts as layer nlayers)."""
         out = {}
         for p, rl in self.rules.items():
+            if p in WEIGHT_POINTS:
+                out[p] = [m for lo, hi, m in rl if lo <= layer < hi][-1]
+                continue
             mode = "32"
             for lo, hi, m in rl:
                 if lo <= layer < hi:
@@ -115,7 +129,9 @@ class Stream:
         return out
 
 
-def run(cfg, ow, tok, S, specs, log_every=8):
+def run(cfg, ow, tok, S, specs, log_every=8, unrounded=False):
+    """Logits and per-position losses of each variant. unrounded: ow holds the
+    unrounded fp32 weights (the weight points then choose per variant)."""
     d, H, hd, q, hid = cfg.dim, cfg.heads, cfg.hd, cfg.q_dim, cfg.hidden
     KVH, kv = cfg.kv_heads, cfg.kv_dim
     rep = H // KVH
@@ -135,17 +151,22 @@ def run(cfg, ow, tok, S, specs, log_every=8):
         rot[..., 1::2] = a[..., 0::2]
         return (a * cos[:, None] + rot * sin[:, None]).reshape(S, -1)
 
-    E = ow.embed.reshape(-1, d)
+    # ow holds the device's fp16-rounded weights, or the unrounded ones when a
+    # variant asks for fp32 weights somewhere (then each variant rounds itself)
+    E32 = ow.embed.reshape(-1, d)
+    E16 = r16(E32) if unrounded else E32
     streams = [Stream(s) for s in specs]
     for st in streams:
-        st.x = E[tok[:-1]].astype(F32)
+        st.x = (E32 if st.at(0)["e"] == "32" else E16)[tok[:-1]].astype(F32)
     t0 = time.time()
     for l in range(cfg.nlayers):
         lw = ow.layers[l]
-        wq, wk, wv = lw.wq.reshape(d, q), lw.wk.reshape(d, kv), lw.wv.reshape(d, kv)
-        wo, w1, w3, w2t = lw.wo.reshape(q, d), lw.w1.reshape(d, hid), lw.w3.reshape(d, hid), lw.w2.reshape(d, hid).T
+        w32 = (lw.wq.reshape(d, q), lw.wk.reshape(d, kv), lw.wv.reshape(d, kv), lw.wo.reshape(q, d),
+               lw.w1.reshape(d, hid), lw.w3.reshape(d, hid), lw.w2.reshape(d, hid).T)
+        w16 = tuple(r16(a) for a in w32) if unrounded else w32
         for st in streams:
             R, x = st.at(l), st.x
+            wq, wk, wv, wo, w1, w3, w2t = w32 if R["w"] == "32" else w16
             xn = R["xn"](norm(x, lw.gamma1))
             Q = R["q"](rope(xn @ wq))
             K = R["k"](rope(xn @ wk))
@@ -166,7 +187,8 @@ def run(cfg, ow, tok, S, specs, log_every=8):
             print(f"  layer {l + 1}/{cfg.nlayers} ({time.time() - t0:.0f} s)", flush=True)
     out = []
     for st in streams:
-        lg = st.at(cfg.nlayers)["xf"](norm(st.x, ow.gamma_final)) @ E.T
+        R = st.at(cfg.nlayers)
+        lg = R["xf"](norm(st.x, ow.gamma_final)) @ (E32 if R["elog"] == "32" else E16).T
         m = lg.max(1, keepdims=True)
         lse = np.log(np.exp(lg - m).sum(1)) + m[:, 0]
         out.append((lg, lse - lg[np.arange(S), tok[1:]]))
@@ -189,18 +211,20 @@ def main():
     specs = a.variants.split(";") if a.variants else default_variants()
     if "fp32" not in specs:
         specs = ["fp32"] + specs
-    ow = synthetic_oracle_weights(cfg, 1234, round16=True, cache=False)
     S = a.seq
     tok = tokens_for(cfg, S + 1, seed=seed)
     t0 = time.time()
-    res = dict(zip(specs, run(cfg, ow, tok, S, specs)))
-    L0, l0 = res["fp32"]
-    against = "all-fp32 operands on the device's weights"
     if a.vs_unrounded:
-        ow32 = synthetic_oracle_weights(cfg, 1234, round16=False, cache=False)
-        (L0, l0), = run(cfg, ow32, tok, S, ["fp32"])
+        ow = synthetic_oracle_weights(cfg, 1234, round16=False, cache=False)
+        ref = "fp32,w=32,e=32,elog=32"
+        res = dict(zip(specs + [ref], run(cfg, ow, tok, S, specs + [ref], unrounded=True)))
+        L0, l0 = res[ref]
         against = "fp32 arithmetic on the unrounded fp32 weights"
-        specs = specs + ["fp32"] if "fp32" in specs else specs
+    else:
+        ow = synthetic_oracle_weights(cfg, 1234, round16=True, cache=False)
+        res = dict(zip(specs, run(cfg, ow, tok, S, specs)))
+        L0, l0 = res["fp32"]
+        against = "all-fp32 operands on the device's weights"
     print(f"{a.shape} seq {S} seed {seed}: each variant vs {against} ({time.time() - t0:.0f} s)")
     print(f"{'variant':<24} {'max|dlogit|':>11} {'rms dlogit':>10} {'max rel dloss':>13} {'top-1':>7}")
     for s in dict.fromkeys(specs):

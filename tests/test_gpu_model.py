@@ -390,3 +390,53 @@ def test_decode_equals_prefill_rows_with_precise_layers(gpu, n):
     for i in range(4):
         _, cur = d3.step(cur)
         np.testing.assert_array_equal(out[i], cur)
+
+
+def test_forward_graph_replays_match_eager(gpu):
+    """Repeated identical hb_forward_device calls replay one captured HIP graph
+    (first call eager, second captured). Every replay -- with eager forwards
+    of another shape, host synchronisations and a weight upload in between --
+    equals the eager result bit for bit, and a replay after new weights equals
+    an eager forward on them (the graph reads the weights at run time)."""
+    import os
+    import torch
+    cfg = ModelConfig.llama_48m()
+    k = CompiledKernels.compile(cfg)
+    k.init_synthetic(71)
+    B, S = 2, 96
+    tok = tokens_for(cfg, B * (S + 1), seed=72).reshape(B, S + 1)
+    dt = torch.from_numpy(tok[:, :-1].astype(np.int32).copy()).cuda()
+    dg = torch.from_numpy(tok[:, 1:].astype(np.int32).copy()).cuda()
+    loss = torch.empty(B * S, device="cuda")
+    logits = torch.empty(B * S, cfg.vocab, device="cuda")
+    mean = torch.empty(1, device="cuda")
+    other = torch.from_numpy(tokens_for(cfg, 40, seed=73).astype(np.int32)).cuda()
+
+    def fwd():
+        hb.call("hb_forward_device", k.model.handle, dt.data_ptr(), dg.data_ptr(), B, S, loss.data_ptr(),
+                logits.data_ptr(), mean.data_ptr())
+        k.ctx.synchronize()
+        torch.cuda.synchronize()
+        return loss.clone(), logits.clone(), mean.clone()
+
+    def eager_other():
+        hb.call("hb_forward_device", k.model.handle, other.data_ptr(), None, 1, 40, None, None, None)
+        k.ctx.synchronize()
+
+    ref = fwd()  # eager
+    for i in range(4):  # capture, then replays
+        got = fwd()
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b), i
+        eager_other()
+    # new weights: a replay equals an eager forward on them
+    k.init_synthetic(74)
+    replay = fwd()
+    os.environ["HB_NO_GRAPH"] = "1"
+    try:
+        eager = fwd()
+    finally:
+        del os.environ["HB_NO_GRAPH"]
+    for a, b in zip(replay, eager):
+        assert torch.equal(a, b)
+    assert not torch.equal(replay[1], ref[1])
