@@ -225,6 +225,14 @@ pub mod sys {
             t: c_int,
             d_x2: *mut f32,
         ) -> c_int;
+        pub fn hb_op_wo_fwd_noalloc(
+            model: *mut hb_model,
+            layer: c_int,
+            d_attn_f16: *const c_void,
+            d_x: *const f32,
+            t: c_int,
+            d_x2: *mut f32,
+        ) -> c_int;
         pub fn hb_op_ffn_fused(
             model: *mut hb_model,
             layer: c_int,

@@ -222,6 +222,15 @@ int hb_op_sdpa_fwd(hb_model* model, int layer, const void* d_xnorm_f16, int B, i
  * x2 = x + alpha * attn @ Wo, x and x2 fp32 [T, dim]. */
 int hb_op_wo_fwd(hb_model* model, int layer, const void* d_attn_f16, const float* d_x, int T,
                  float* d_x2);
+/* hb_op_wo_fwd without any allocation. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The split-K
+ * partial sums live in a fixed 16 MiB device array inside the library (one per
+ * GPU, held until the process ends), which covers every shape; results equal
+ * hb_op_wo_fwd's bit for bit. Calls that overlap on one GPU share that array
+ * and race: keep them ordered on one stream. */
+int hb_op_wo_fwd_noalloc(hb_model* model, int layer, const void* d_attn_f16, const float* d_x, int T,
+                         float* d_x2);
 /*
  * ffnFused (kernels/ffn_fused.rs:22-83): h1 = xn@W1, h3 = xn@W3,
  * gate = silu(h1)*h3, x_next = x2 + alpha * gate @ W2^T. xn fp16 [T, dim], x2

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -628,6 +629,39 @@ extern "C" int hb_device_count(int* out) {
   return HB_OK;
 }
 
+// ---- scratch of the allocation-free entry point (hb_op_wo_fwd_noalloc) ----
+// The split-K partial sums of hb_op_wo_fwd_noalloc live in this file-scope
+// device array -- one copy on every GPU the library runs on, held until the
+// process ends -- instead of memory the library allocates. 16 MiB suffices
+// for every shape: gemm_splits aims the split count S at 256 workgroups of
+// 128x128 tiles (S <= 256 / tiles), so S * T * N <= 256 * 128 * 128 floats.
+constexpr size_t NOALLOC_SCRATCH_FLOATS = (size_t)256 * 128 * 128;
+static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_FLOATS];
+
+// Device address of `scratch` on each device, looked up once per device (with
+// that device current) when the first context on it is created. Host code
+// uses these addresses, never the array's name (a host-side stand-in).
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static float* g_scratch_dev[NOALLOC_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+static int scratch_setup(int device) {
+  if (device < 0 || device >= NOALLOC_MAX_DEVICES) return fail(HB_E_DEVICE, "device %d beyond the scratch table", device);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_dev[device]) return HB_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) return fail(HB_E_DEVICE, "scratch address on device %d: %s", device, hipGetErrorString(e));
+  g_scratch_dev[device] = (float*)p;
+  return HB_OK;
+}
+
+static float* scratch_of(int device) {
+  if (device < 0 || device >= NOALLOC_MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return g_scratch_dev[device];
+}
+
 extern "C" int hb_ctx_create(int device, hb_ctx** out) {
   HB_INJECT_CHECK();
   if (!out) return fail(HB_E_INVALID, "null out");
@@ -650,6 +684,14 @@ extern "C" int hb_ctx_create(int device, hb_ctx** out) {
     if (c->capture) (void)hipStreamDestroy(c->capture);
     delete c;
     return fail(HB_E_DEVICE, "context setup failed: %s", hipGetErrorString(e));
+  }
+  const int r = scratch_setup(device);
+  if (r != HB_OK) {
+    (void)hipFree(c->d_err);
+    (void)hipStreamDestroy(c->own);
+    (void)hipStreamDestroy(c->capture);
+    delete c;
+    return r;
   }
   *out = c;
   return HB_OK;
@@ -2034,6 +2076,28 @@ extern "C" int hb_op_wo_fwd(hb_model* m, int layer, const void* attn, const floa
   const hb_model_config& c = m->cfg;
   GemmScratch so;
   TRY(residual_scratch(m, c.dim, T, c.q_dim, so));
+  HIP_TRY(gemm_residual(m->layers[layer].wo, (const f16*)attn, c.dim, T, c.q_dim,
+                        EpiResidual{x, x2, c.dim, alpha_of(c)}, &so, m->ctx->stream()));
+  return HB_OK;
+}
+
+extern "C" int hb_op_wo_fwd_noalloc(hb_model* m, int layer, const void* attn, const float* x, int T,
+                                    float* x2) {
+  HB_INJECT_CHECK();
+  if (!m || !attn || !x || !x2) return fail(HB_E_INVALID, "null argument");
+  if (layer < 0 || layer >= m->cfg.nlayers || !m->layers[layer].uploaded)
+    return fail(HB_E_STATE, "layer %d not available", layer);
+  if (T <= 0) return fail(HB_E_INVALID, "T must be positive");
+  TRY(check_token_count(m->cfg, 1, T));
+  const hb_model_config& c = m->cfg;
+  const int splits = gemm_splits(c.dim, T, c.q_dim);
+  if (splits > 1 && (size_t)splits * T * c.dim > NOALLOC_SCRATCH_FLOATS)
+    return fail(HB_E_INVALID, "T=%d: %d K splits x %d x %d partial sums exceed the %zu-float no-alloc scratch", T,
+                splits, T, c.dim, NOALLOC_SCRATCH_FLOATS);
+  float* sp = scratch_of(m->ctx->device);
+  if (!sp) return fail(HB_E_STATE, "no-alloc scratch not set up on device %d", m->ctx->device);
+  DeviceGuard g(m->ctx->device);
+  const GemmScratch so{sp, NOALLOC_SCRATCH_FLOATS, 256};
   HIP_TRY(gemm_residual(m->layers[layer].wo, (const f16*)attn, c.dim, T, c.q_dim,
                         EpiResidual{x, x2, c.dim, alpha_of(c)}, &so, m->ctx->stream()));
   return HB_OK;

@@ -136,6 +136,7 @@ SIGNATURES = {
     "hb_op_embedding": [_P, _P, _I, _P],
     "hb_op_sdpa_fwd": [_P, _I, _P, _I, _I, _P, _P],
     "hb_op_wo_fwd": [_P, _I, _P, _P, _I, _P],
+    "hb_op_wo_fwd_noalloc": [_P, _I, _P, _P, _I, _P],
     "hb_op_ffn_fused": [_P, _I, _P, _P, _I, _P, _P, _P],
     "hb_op_ffn_up": [_P, _I, _P, _I, _P, _P],
     "hb_op_logits_ce": [_P, _P, _P, _I, _P, _P],
