@@ -46,11 +46,15 @@ shapes and K splits, so their fp32 sums differ in order; each lies within the
 bars of the oracle and their difference is held to twice the bars.
 
 The unrounded-weight comparisons add the weights' own fp16 rounding, which the
-workloads define (fp16 weights): fp32 arithmetic on the fp16-rounded weights
-against fp32 on the unrounded ones differs by about as much as the device does
-(see the measured table in the design notes), so those rows are held to
-BAR_UNROUNDED times the bars as a check that nothing beyond the weight
-rounding is added.
+workloads define (fp16 weights). The study's --vs-unrounded mode measures
+that floor on the 7B sequence above: exact fp32 arithmetic on the fp16
+weights is already 3.55e-2 / 2.03e-3 / 98.44% from fp32 arithmetic on the
+unrounded weights (the device: 3.75e-2 / 2.09e-3 / 98.05%). Most of it is
+again the first layer: keeping the embedding rows and layer 0's weights
+unrounded as well would give 1.82e-2 / 8.3e-4 / 98.83% (the other layers'
+fp16 weights keep top-1 below 99.5% even with fp32 arithmetic: 1.20e-2 /
+7.6e-4 / 99.22%). Those rows are held to BAR_UNROUNDED times the bars, which
+checks that the device adds nothing beyond the weights' rounding.
 """
 import time
 
@@ -69,7 +73,7 @@ LOGIT_ATOL = 2e-2
 TOP1_MIN = 0.995           # greedy top-1 agreement over the positions a test compares
 TOP1_ROW_MIN = 0.99        # and per 512-position sequence (a 2-flip margin is noise there)
 BAR_DEVICE_PAIR = 2.0      # two device runs of one sequence (see _check_batch)
-BAR_UNROUNDED = 4.0        # the weights' own fp16 rounding (see the module docstring)
+BAR_UNROUNDED = 2.5        # the weights' own fp16 rounding (module docstring)
 UNROUNDED_TOP1 = 0.975
 SEED = 1234
 STD = 0.02
@@ -224,12 +228,14 @@ def test_5b_b4_matches_oracle(m5b):
 # ---------------------------------------------------------------------------
 P7 = 2048          # decode prompt = the seq-2048 prefill's tokens
 DEC_STEPS = 40     # teacher-forced decode steps checked against the oracle
+DEC_LONG = 256     # free-running greedy steps checked against the device's own prefill
 
 
 @pytest.fixture(scope="module")
 def m7b(gpu, m5b):
     m5b.close()
-    m = _Full(ModelConfig.llama_7b(seq=P7), cache_f32=False)  # unrounded weights used once
+    # seq covers the prompt and the 256 greedy steps (a forward over the whole history)
+    m = _Full(ModelConfig.llama_7b(seq=P7 + DEC_LONG), cache_f32=False)  # unrounded weights used once
     yield m
     m.close()
 
@@ -360,3 +366,61 @@ def test_7b_decode_b16_rows_match_oracle_and_batch_one(m7b, tok7, orc7, orc7_ste
     finally:
         db.kv.close()
         d1.kv.close()
+
+
+def _greedy_against_prefill(m7b, B, rows, seed):
+    """The benchmark's decode workload: B sequences, a 2048-token seeded
+    prompt, then 256 free-running greedy steps, each feeding back its own
+    argmax (the step's logits are kept). A forward over each checked row's
+    whole history (prompt + the fed-back tokens) must give the same logits at
+    every decoded position, within the contract's 2e-2, and the same greedy
+    token at >= 99% of them: decode (GEMV, one position) and prefill (GEMM,
+    all positions) are two device computations in different summation orders,
+    each at its own distance from the oracle (both checked against it above),
+    so near-tied logits can flip between them (measured: 254/256 at batch 1,
+    511/512 at batch 16). The captured greedy graph must produce the same
+    tokens as the step-by-step decode."""
+    cfg = m7b.cfg
+    prompt = np.stack([tokens_for(cfg, P7, seed=seed, stream=b) for b in range(B)])
+    dec = E.Decoder(m7b.k, batch=B, ctx_max=P7 + DEC_LONG)
+    dg = E.Decoder(m7b.k, batch=B, ctx_max=P7 + DEC_LONG)
+    try:
+        t0 = time.time()
+        gl, nxt = dec.prefill(prompt)
+        hist, logits = [nxt.copy()], {b: [gl[b].copy()] for b in rows}
+        for i in range(DEC_LONG - 1):
+            gl, nxt = dec.step(hist[-1])
+            hist.append(nxt.copy())
+            for b in rows:
+                logits[b].append(gl[b].copy())
+        hist = np.stack(hist, axis=1)  # [B, DEC_LONG]: tokens at positions P7 .. P7+DEC_LONG-1
+        print(f"7B decode B={B}: prefill + {DEC_LONG - 1} steps in {time.time() - t0:.1f} s", flush=True)
+        _, n0 = dg.prefill(prompt)
+        graph_tokens = dg.greedy(n0, DEC_LONG - 1)  # [steps, B]
+        np.testing.assert_array_equal(graph_tokens.T, hist[:, 1:])
+    finally:
+        dec.kv.close()
+        dg.kv.close()
+    tally = []
+    for b in rows:
+        seq = np.concatenate([prompt[b], hist[b, :-1]])  # positions 0 .. P7+DEC_LONG-2
+        full = m7b.forward(seq, None, 1).logits.reshape(-1, cfg.vocab)
+        rows_ref = full[P7 - 1:]  # logits at positions P7-1 .. P7+DEC_LONG-2
+        got = np.stack(logits[b])
+        err = float(np.abs(got - rows_ref).max())
+        same = int((got.argmax(-1) == rows_ref.argmax(-1)).sum())
+        tally.append((same, got.shape[0]))
+        print(f"7B decode B={B} row {b}: {got.shape[0]} decoded positions vs device prefill rows: "
+              f"max|dlogit|={err:.3e} top1 {same}/{got.shape[0]}", flush=True)
+        assert err <= LOGIT_ATOL
+    _check_tally(f"7B decode B={B} vs prefill rows", tally, top1_min=TOP1_ROW_MIN)
+
+
+@pytest.mark.timeout(600)
+def test_7b_greedy_256_steps_b1_equal_prefill_rows(m7b):
+    _greedy_against_prefill(m7b, 1, [0], seed=50)
+
+
+@pytest.mark.timeout(600)
+def test_7b_greedy_256_steps_b16_equal_prefill_rows(m7b):
+    _greedy_against_prefill(m7b, 16, [0, 15], seed=51)
