@@ -34,9 +34,8 @@
 // merges them into the fp16 attention rows it needs (all of them) in the same
 // way. With B * chunks <= GEMV_ATTN_MAXCH that is at most 8 x 130 floats per
 // (sequence, head) -- 133 KB per workgroup on the 7B shape at 4096 context --
-// fetched in one round trip while the first weight loads are in flight,
-// instead of a separate combine launch (attention_combine, used when B *
-// chunks is larger).
+// fetched while the first weight loads are in flight, instead of a separate
+// combine launch (attention_combine, used when B * chunks is larger).
 #include <type_traits>
 
 #include "internal.hpp"
@@ -119,11 +118,13 @@ HB_DEV void stage_norm(const NormIn& nin, int B, int K, f16* s_x) {
 // attn[b][h*hd + e] = fp16(sum_c w_c o_c[e] / sum_c w_c l_c), w_c = exp2(m_c - M),
 // M = max_c m_c over the chunks c <= *d_pos / chunk of attention_decode -- the
 // arithmetic and chunk order of attention_combine. One 8-dim group of one
-// (sequence, head) per thread and pass, every chunk load of a group issued
-// before any is used (one memory round trip).
+// (sequence, head) per thread and pass: the chunk maxima first, then the
+// chunk outputs in batches of 8 with every load of a batch issued before any
+// is used.
 template <int NT>
 HB_DEV void stage_attn(const AttnIn& ai, int B, int K, f16* s_x) {
   constexpr int MAXCH = GEMV_ATTN_MAXCH;
+  constexpr int CB = 8;  // chunk outputs in flight per batch
   const int nvalid = min(*ai.d_pos / ai.chunk + 1, ai.nch);
   const int gph = ai.hd / 8;
   const int ngroups = B * ai.H * gph;
@@ -134,17 +135,10 @@ HB_DEV void stage_attn(const AttnIn& ai, int B, int K, f16* s_x) {
     const int b = bh / ai.H, h = bh - b * ai.H;
     const float* pml = ai.part_ml + (size_t)bh * ai.nch * 2;
     const float* po = ai.part_o + (size_t)bh * ai.nch * ai.hd + e0;
-    float m[MAXCH], l[MAXCH];
-    f32x4 u[MAXCH], v[MAXCH];
+    float m[MAXCH];
 #pragma unroll
-    for (int c = 0; c < MAXCH; ++c) {
-      if (c < nvalid) {
-        m[c] = pml[2 * c];
-        l[c] = pml[2 * c + 1];
-        u[c] = *(const f32x4*)(po + (size_t)c * ai.hd);
-        v[c] = *(const f32x4*)(po + (size_t)c * ai.hd + 4);
-      }
-    }
+    for (int c = 0; c < MAXCH; ++c)
+      if (c < nvalid) m[c] = pml[2 * c];
     float M = -INFINITY;
 #pragma unroll
     for (int c = 0; c < MAXCH; ++c)
@@ -152,12 +146,27 @@ HB_DEV void stage_attn(const AttnIn& ai, int B, int K, f16* s_x) {
     float L = 0.f;
     f32x4 O0 = {}, O1 = {};
 #pragma unroll
-    for (int c = 0; c < MAXCH; ++c) {
-      if (c < nvalid) {
-        const float w = exp2f(m[c] - M);
-        L += w * l[c];
-        O0 += w * u[c];
-        O1 += w * v[c];
+    for (int cb = 0; cb < MAXCH; cb += CB) {
+      float l[CB];
+      f32x4 u[CB], v[CB];
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const int c = cb + j;
+        if (c < nvalid) {
+          l[j] = pml[2 * c + 1];
+          u[j] = *(const f32x4*)(po + (size_t)c * ai.hd);
+          v[j] = *(const f32x4*)(po + (size_t)c * ai.hd + 4);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const int c = cb + j;
+        if (c < nvalid) {
+          const float w = exp2f(m[c] - M);
+          L += w * l[j];
+          O0 += w * u[j];
+          O1 += w * v[j];
+        }
       }
     }
     const float iL = 1.0f / L;

@@ -222,15 +222,15 @@ def test_decode_separate_norm_path_matches_fused(m48):
 
 def test_decode_long_context_both_chunk_combines(m48):
     """A 1030-token prompt spans three 512-key attention chunks. At batch 1 the
-    Wo GEMV combines the chunk partials (checked against the oracle); at batch 3
-    (3 x 3 chunks is past that path's limit of 8) a separate combine kernel
+    Wo GEMV combines the chunk partials (checked against the oracle); at batch 4
+    (4 x 3 chunks is past that path's limit of 8) a separate combine kernel
     does, and its rows must agree with the batch-1 decoder."""
     cfg, w, k = m48
     P, steps = 1030, 3
-    tok = tokens_for(cfg, 3 * (P + steps), seed=71).reshape(3, P + steps)
+    tok = tokens_for(cfg, 4 * (P + steps), seed=71).reshape(4, P + steps)
     d1 = E.Decoder(k, batch=1, ctx_max=P + steps)
     orc = O.DecodeOracle(oracle_cfg(cfg), oracle_weights(w), ctx_max=P + steps)
-    d3 = E.Decoder(k, batch=3, ctx_max=P + steps)
+    d3 = E.Decoder(k, batch=4, ctx_max=P + steps)
     g1, _ = d1.prefill(tok[0, :P])
     r1 = orc.prefill(tok[0, :P])
     g3, _ = d3.prefill(tok[:, :P])
@@ -240,10 +240,12 @@ def test_decode_long_context_both_chunk_combines(m48):
         r1 = orc.step(int(tok[0, P + i]))
         g3, n3 = d3.step(tok[:, P + i])
         err = np.abs(g1[0] - r1).max()
-        print(f"step {i}: max|dlogit| vs oracle {err:.2e}, batch-3 row 0 vs batch 1 "
+        print(f"step {i}: max|dlogit| vs oracle {err:.2e}, batch-4 row 0 vs batch 1 "
               f"{np.abs(g3[0] - g1[0]).max():.2e}", flush=True)
         assert err < LOGIT_ATOL
-        assert np.abs(g3[0] - g1[0]).max() < 1e-3
+        # two device paths (separate norm and combine launches vs the fused
+        # prologues), each ~1e-3 from the oracle on this model
+        assert np.abs(g3[0] - g1[0]).max() < 2e-3
         assert int(n3[0]) == int(n1[0])
 
 
