@@ -264,27 +264,37 @@ hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-// ---- decode: split the context into 512-key chunks ------------------------------
-// Grid (chunk, head, sequence), 16 waves per chunk, 32 keys per wave. hd/8
-// lanes share one key row (16-byte loads; one wave instruction reads 1 KB of
-// consecutive key rows). Each lane issues all of its K and V loads before
-// using any (V does not depend on the scores), each wave keeps its own online
-// softmax state, and the 16 waves merge through LDS into one partial
-// (max, sum, unnormalised output) per chunk. Chunks past the current position
-// exit at once, so the launch shape does not depend on the position (one HIP
-// graph replays every step). Measured on MI355X, 512-key chunks on 16 waves
-// stream the cache as fast as 128- or 256-key chunks on 4 or 8 waves while
-// leaving fewer partials to combine.
+// ---- decode: split the context into chunks of 512-key blocks ----------------
+// Grid (chunk, head, sequence), 16 waves per chunk, 32 keys of each 512-key
+// block per wave. hd/8 lanes share one key row (16-byte loads; one wave
+// instruction reads 1 KB of consecutive key rows). Per block each lane issues
+// all of its K and V loads before using any (V does not depend on the
+// scores); each wave keeps its own online softmax state across the chunk's
+// blocks, and the 16 waves merge through LDS into one partial (max, sum,
+// unnormalised output) per chunk -- or, when one chunk spans the whole
+// context, straight into the normalised fp16 attention row. Chunks past the
+// current position exit at once, so the launch shape does not depend on the
+// position (one HIP graph replays every step).
 //
-// The chunk partials are combined by the consumer -- the Wo GEMV prologue
-// (gemv.hip) when B * chunks is small -- or by attn_combine_kernel below,
-// which folds them in the same order with the same arithmetic, so both give
-// the same attention output.
-constexpr int DCHUNK = 512;
+// Chunk length: enough chunks for about 256 workgroups over the B x H
+// (sequence, head) pairs, at most one per 512-key block. On the 7B shape
+// (32 heads) that is 5 one-block chunks at B = 1 and a single chunk at
+// B >= 8 (no partials, no combine). Measured on MI355X, 512-key blocks on 16
+// waves stream the cache as fast as 128- or 256-key blocks on 4 or 8 waves.
+//
+// With several chunks the partials are combined by the consumer -- the Wo
+// GEMV prologue (gemv.hip) when B * chunks is small -- or by
+// attn_combine_kernel below, which folds them in the same order with the
+// same arithmetic, so both give the same attention output.
+constexpr int DBLOCK = 512;
 constexpr int DWAVES = 16;
 
-int attn_decode_chunks(int ctx_max) { return (ctx_max + DCHUNK - 1) / DCHUNK; }
-int attn_decode_chunk_keys() { return DCHUNK; }
+AttnChunking attn_decode_chunking(int ctx_max, int B, int H) {
+  const int nblk = (ctx_max + DBLOCK - 1) / DBLOCK;
+  const int want = std::max(1, std::min(nblk, 256 / std::max(1, B * H)));
+  const int per = (nblk + want - 1) / want;  // blocks per chunk
+  return AttnChunking{(nblk + per - 1) / per, per * DBLOCK};
+}
 
 // SPLIT: q, K and V come in two-term fp16 form (common.hpp) and are summed to
 // fp32 as they are loaded (the arithmetic is fp32 throughout).
@@ -293,14 +303,15 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
   constexpr int NT = DWAVES * 64;
   constexpr int LPK = HD / 8;             // lanes per key row
   constexpr int KPW = 64 / LPK;           // keys per wave instruction
-  constexpr int WKEYS = DCHUNK / DWAVES;  // keys per wave
+  constexpr int WKEYS = DBLOCK / DWAVES;  // keys per wave and block
   constexpr int NIT = WKEYS / KPW;
   __shared__ float s_m[DWAVES], s_l[DWAVES];
   __shared__ float s_o[DWAVES][HD];
 
   const int pos = *p.d_pos;
-  const int c0 = blockIdx.x * DCHUNK;
+  const int c0 = blockIdx.x * p.chunk;
   if (c0 > pos) return;
+  const int cend = min(c0 + p.chunk, pos + 1);  // keys c0 .. cend-1
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (p.H / p.KVH);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -321,54 +332,71 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
   const f16* vb = p.v + kvo;
   const float sl2 = p.scale * HB_LOG2E;
 
-  const int kbase = c0 + wave * WKEYS + g;
-  constexpr int NL = SPLIT ? NIT : 1;
-  f16x8 kr[NIT], vr[NIT], krl[NL], vrl[NL];
-  const f16x8 zero8 = {};
-#pragma unroll
-  for (int i = 0; i < NIT; ++i) {
-    const int kk = kbase + i * KPW;
-    kr[i] = kk <= pos ? *(const f16x8*)(kb + (size_t)kk * HD) : zero8;
-    if constexpr (SPLIT) krl[i] = kk <= pos ? *(const f16x8*)(p.k_lo + kvo + (size_t)kk * HD) : zero8;
-  }
-  // V loads go out with K's, before the scores, except with low parts: then
-  // they follow the scores so that K's registers are free again
-  auto load_v = [&]() {
+  // Online softmax state of this lane's keys (m is wave-uniform).
+  float m = -INFINITY, l = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int b0 = c0; b0 < cend; b0 += DBLOCK) {
+    const int kbase = b0 + wave * WKEYS + g;
+    constexpr int NL = SPLIT ? NIT : 1;
+    f16x8 kr[NIT], krl[NL];
+    const f16x8 zero8 = {};
 #pragma unroll
     for (int i = 0; i < NIT; ++i) {
       const int kk = kbase + i * KPW;
-      vr[i] = kk <= pos ? *(const f16x8*)(vb + (size_t)kk * HD) : zero8;
-      if constexpr (SPLIT) vrl[i] = kk <= pos ? *(const f16x8*)(p.v_lo + kvo + (size_t)kk * HD) : zero8;
+      kr[i] = kk <= pos ? *(const f16x8*)(kb + (size_t)kk * HD) : zero8;
+      if constexpr (SPLIT) krl[i] = kk <= pos ? *(const f16x8*)(p.k_lo + kvo + (size_t)kk * HD) : zero8;
     }
-  };
-  if constexpr (!SPLIT) load_v();
-  auto kval = [&](int i, int e) { return SPLIT ? (float)kr[i][e] + (float)krl[i % NL][e] : (float)kr[i][e]; };
-  auto vval = [&](int i, int e) { return SPLIT ? (float)vr[i][e] + (float)vrl[i % NL][e] : (float)vr[i][e]; };
-  float sc[NIT];
+    // Without low parts the V loads go out with K's, before the scores. With
+    // them they follow the scores, in two halves, so that K's registers are
+    // free again and one half of V (hi and lo) is live at a time.
+    constexpr int NV = SPLIT ? NIT / 2 : NIT;
+    f16x8 vr[NV], vrl[SPLIT ? NV : 1];
+    auto load_v = [&](int i0) {
 #pragma unroll
-  for (int i = 0; i < NIT; ++i) {
-    float d = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) d += qf[e] * kval(i, e);
-#pragma unroll
-    for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-    sc[i] = (kbase + i * KPW <= pos) ? d * sl2 : -INFINITY;
-  }
-  if constexpr (SPLIT) load_v();
-  // wave-wide max over its keys (lanes of a group hold equal scores)
-  float m = sc[0];
-#pragma unroll
-  for (int i = 1; i < NIT; ++i) m = fmaxf(m, sc[i]);
-#pragma unroll
-  for (int o = LPK; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  float l = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (m != -INFINITY) {
+      for (int i = 0; i < NV; ++i) {
+        const int kk = kbase + (i0 + i) * KPW;
+        vr[i] = kk <= pos ? *(const f16x8*)(vb + (size_t)kk * HD) : zero8;
+        if constexpr (SPLIT) vrl[i] = kk <= pos ? *(const f16x8*)(p.v_lo + kvo + (size_t)kk * HD) : zero8;
+      }
+    };
+    if constexpr (!SPLIT) load_v(0);
+    auto kval = [&](int i, int e) { return SPLIT ? (float)kr[i][e] + (float)krl[i % NL][e] : (float)kr[i][e]; };
+    float sc[NIT];
 #pragma unroll
     for (int i = 0; i < NIT; ++i) {
-      const float pk = exp2f(sc[i] - m);
-      l += pk;
+      float d = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += pk * vval(i, e);
+      for (int e = 0; e < 8; ++e) d += qf[e] * kval(i, e);
+#pragma unroll
+      for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+      sc[i] = (kbase + i * KPW <= pos) ? d * sl2 : -INFINITY;
+    }
+    // wave-wide max over this block's keys (lanes of a group hold equal scores)
+    float mb = sc[0];
+#pragma unroll
+    for (int i = 1; i < NIT; ++i) mb = fmaxf(mb, sc[i]);
+#pragma unroll
+    for (int o = LPK; o < 64; o <<= 1) mb = fmaxf(mb, __shfl_xor(mb, o, 64));
+    const float mn = fmaxf(m, mb);
+    if (mn != -INFINITY) {
+      if (m != mn) {  // rescale what earlier blocks left (nothing on the first)
+        const float r = exp2f(m - mn);
+        l *= r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= r;
+        m = mn;
+      }
+#pragma unroll
+      for (int i0 = 0; i0 < NIT; i0 += NV) {
+        if constexpr (SPLIT) load_v(i0);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const float pk = exp2f(sc[i0 + i] - m);
+          l += pk;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            acc[e] += pk * (SPLIT ? (float)vr[i][e] + (float)vrl[i % (SPLIT ? NV : 1)][e] : (float)vr[i][e]);
+        }
+      }
     }
   }
 #pragma unroll
@@ -389,12 +417,34 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
   float M = s_m[0];
 #pragma unroll
   for (int v = 1; v < DWAVES; ++v) M = fmaxf(M, s_m[v]);
-  const int nch = gridDim.x;
-  const size_t head = (size_t)b * p.H + h;
-  const size_t slot = head * nch + blockIdx.x;
   // Wave weights exp2(m_w - M); a wave whose keys are all past pos has
   // m_w = -inf and weight 0.
   auto wt = [&](int v) { return s_m[v] == -INFINITY ? 0.f : exp2f(s_m[v] - M); };
+  float L = 0.f;
+#pragma unroll
+  for (int v = 0; v < DWAVES; ++v) L += wt(v) * s_l[v];
+  const size_t head = (size_t)b * p.H + h;
+  if (gridDim.x == 1) {
+    // One chunk: the normalised attention row, fp16 (split rows [B][2*H*hd]
+    // hi | lo with two-term inputs), as attention_combine would write it.
+    const float iL = 1.0f / L;
+    for (int e = tid; e < HD; e += NT) {
+      float o = 0.f;
+#pragma unroll
+      for (int v = 0; v < DWAVES; ++v) o += wt(v) * s_o[v][e];
+      o *= iL;
+      const f16 hi = (f16)o;
+      if (p.q_lo) {
+        f16* op = p.out + (size_t)b * 2 * p.H * HD + h * HD + e;
+        op[0] = hi;
+        op[(size_t)p.H * HD] = (f16)(o - (float)hi);
+      } else {
+        p.out[head * HD + e] = hi;
+      }
+    }
+    return;
+  }
+  const size_t slot = head * gridDim.x + blockIdx.x;
   for (int e = tid; e < HD; e += NT) {
     float o = 0.f;
 #pragma unroll
@@ -402,9 +452,6 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
     p.part_o[slot * HD + e] = o;
   }
   if (tid == 0) {
-    float L = 0.f;
-#pragma unroll
-    for (int v = 0; v < DWAVES; ++v) L += wt(v) * s_l[v];
     p.part_ml[slot * 2] = M;
     p.part_ml[slot * 2 + 1] = L;
   }
@@ -418,7 +465,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecode p, int nch
   constexpr int GPH = HD / 8;
   const int gid = blockIdx.x * 256 + threadIdx.x;
   if (gid >= p.B * p.H * GPH) return;
-  const int nvalid = min(*p.d_pos / DCHUNK + 1, nch);
+  const int nvalid = min(*p.d_pos / p.chunk + 1, nch);
   const int bh = gid / GPH, e0 = (gid % GPH) * 8;
   const float* pml = p.part_ml + (size_t)bh * nch * 2;
   const float* po = p.part_o + (size_t)bh * nch * HD + e0;
@@ -453,8 +500,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecode p, int nch
 }
 
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
-  const int nch = attn_decode_chunks(p.ctx_max);
-  dim3 grid(nch, p.H, p.B), block(DWAVES * 64);
+  const AttnChunking ch = attn_decode_chunking(p.ctx_max, p.B, p.H);
+  if (p.chunk != ch.keys) return hipErrorInvalidValue;
+  dim3 grid(ch.n, p.H, p.B), block(DWAVES * 64);
   const bool split = p.q_lo != nullptr;
   if (split && (!p.k_lo || !p.v_lo)) return hipErrorInvalidValue;
   if (p.hd == 128 && split)
@@ -471,7 +519,9 @@ hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
 }
 
 hipError_t attention_combine(const AttnDecode& p, hipStream_t st) {
-  const int nch = attn_decode_chunks(p.ctx_max);
+  const AttnChunking ch = attn_decode_chunking(p.ctx_max, p.B, p.H);
+  if (p.chunk != ch.keys || ch.n < 2) return hipErrorInvalidValue;
+  const int nch = ch.n;
   const int n = p.B * p.H * (p.hd / 8);
   if (p.hd == 128)
     hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((n + 255) / 256), dim3(256), 0, st, p, nch);

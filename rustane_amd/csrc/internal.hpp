@@ -136,19 +136,26 @@ struct AttnDecode {
   size_t bstride, hstride;
   const int* d_pos;  // keys 0..*d_pos are attended
   int B, H, KVH, hd, ctx_max;
+  int chunk;  // keys per chunk: attn_decode_chunking(ctx_max, B, H).keys
   float scale;
   float* part_o;   // [B][H][nchunks][hd] unnormalised chunk outputs
   float* part_ml;  // [B][H][nchunks][2] chunk (max, sum) in log2 units
-  f16* out;        // [B][H*hd], written by attention_combine
+  f16* out;        // [B][H*hd], written by attention_combine, or by
+                   // attention_decode itself when there is one chunk
   // Two-term fp16 inputs (common.hpp): low parts of q, k and v in the same
-  // layouts, all set or all NULL; attention_combine then writes split rows
+  // layouts, all set or all NULL; the attention rows are then split rows
   // [B][2*H*hd].
   const f16 *q_lo = nullptr, *k_lo = nullptr, *v_lo = nullptr;
 };
-int attn_decode_chunks(int ctx_max);
-int attn_decode_chunk_keys();
-// Partials of chunks 0..*d_pos/chunk_keys; the Wo GEMV prologue or
-// attention_combine turns them into the attention output.
+// Chunks of the decode context for B sequences of H heads: n chunks of `keys`
+// keys each (a multiple of 512), n * keys >= ctx_max.
+struct AttnChunking {
+  int n, keys;
+};
+AttnChunking attn_decode_chunking(int ctx_max, int B, int H);
+// Partials of chunks 0..*d_pos/chunk; the Wo GEMV prologue or
+// attention_combine turns them into the attention output. With one chunk
+// the kernel writes the attention rows (out) itself.
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st);
 hipError_t attention_combine(const AttnDecode& p, hipStream_t st);
 
