@@ -187,7 +187,7 @@ HB_DEV void stage_attn(const AttnIn& ai, int B, int K, f16* s_x) {
 // Greedy-decode argmax partials of the logits epilogue: the first index of
 // the maximum of each sequence's 16 logits of this row block, with the
 // cross-entropy kernel's rules (NaN never wins, ties go to the lower index).
-HB_DEV void argmax_partial(const EpiLogits& e, f32x4 v, int f0, int col, int B) {
+HB_DEV void argmax_partial(const EpiLogits& e, f32x4 v, int f0, int col, int B, int rb, int nrb) {
   const f32x4 y = e.capped(v);
   float best = -INFINITY;
   int idx = 0x7fffffff;
@@ -205,7 +205,7 @@ HB_DEV void argmax_partial(const EpiLogits& e, f32x4 v, int f0, int col, int B) 
     }
   }
   if ((threadIdx.x & 63) < 16 && col < B) {
-    const size_t slot = (size_t)col * gridDim.x + blockIdx.x;
+    const size_t slot = (size_t)col * nrb + rb;
     e.part_val[slot] = best;
     e.part_idx[slot] = idx;
   }
@@ -295,13 +295,76 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
     const int f0 = rb * 16 + 4 * (lane >> 4);
     if (col < B) epi(col, f0, v);
     if constexpr (std::is_same_v<Epi, EpiLogits>) {
-      if (epi.part_val) argmax_partial(epi, v, f0, col, B);
+      if (epi.part_val) argmax_partial(epi, v, f0, col, B, rb, gridDim.x);
     }
+  }
+}
+
+// Wide batches (B > 3, no norm prologue): every lane of a wave reads the B
+// operand, as many bytes per k-step as the weight fragment, and the plain
+// kernel re-reads all B rows for each 16-row block. Here a workgroup walks R
+// row blocks (blockIdx.x, + gridDim.x, ...) and each wave keeps its K range of
+// the B rows in registers (XS fragments, K <= 32 * XS * KS), so the rows are
+// read once per workgroup. Same per-block arithmetic as gemv_kernel (one
+// MFMA chain per wave over its K range, waves summed in order).
+template <int KS, int XS, int U, class Epi>
+__global__ __launch_bounds__(KS * 64) void gemv_xreg_kernel(const f16x8* __restrict__ Wt,
+                                                            const f16* __restrict__ X, int N, int B,
+                                                            int K, Epi epi) {
+  __shared__ f32x4 red[KS][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, kq = 8 * (lane >> 4);
+  const int nsteps = K >> 5;
+  const int s_begin = (nsteps * wave) / KS, ns = (nsteps * (wave + 1)) / KS - s_begin;  // ns <= XS
+  const bool xok = col < B;
+  const f16* xrow = X + (size_t)(xok ? col : 0) * K + kq + (size_t)s_begin * 32;
+  const f16x8 zero8 = {};
+  f16x8 xr[XS];
+#pragma unroll
+  for (int j = 0; j < XS; ++j) {
+    const f16x8 v = j < ns ? *(const f16x8*)(xrow + (size_t)j * 32) : zero8;
+    xr[j] = xok ? v : zero8;
+  }
+  const int nrb = N >> 4;
+  for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
+    const f16x8* wp = Wt + ((size_t)rb * nsteps + s_begin) * 64 + lane;
+    f32x4 acc = {};
+#pragma unroll
+    for (int j0 = 0; j0 < XS; j0 += U) {
+      f16x8 a[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (j0 + u < ns) a[u] = __builtin_nontemporal_load(wp + (size_t)(j0 + u) * 64);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (j0 + u < ns) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], xr[j0 + u], acc, 0, 0, 0);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+      f32x4 v = red[0][lane];
+#pragma unroll
+      for (int w = 1; w < KS; ++w) v += red[w][lane];
+      const int f0 = rb * 16 + 4 * (lane >> 4);
+      if (col < B) epi(col, f0, v);
+      if constexpr (std::is_same_v<Epi, EpiLogits>) {
+        if (epi.part_val) argmax_partial(epi, v, f0, col, B, rb, nrb);
+      }
+    }
+    __syncthreads();  // red is reused by the next row block
   }
 }
 
 namespace {
 constexpr int GEMV_KS = 8;  // waves per workgroup (K split)
+// gemv_xreg_kernel: B-operand fragments per wave (K <= 4096), batches from
+// which it is used, workgroups (one per CU: 7B at B = 16, 6.78 -> 6.56 ms per
+// decode step; two per CU and half the row blocks each: 6.76) and weight
+// loads in flight per wave (4: 6.60 ms, 16: 7.18)
+constexpr int GEMV_XS = 16;
+constexpr int GEMV_XREG_MINB = 4;
+constexpr int GEMV_XREG_WGS = 256;
+constexpr int GEMV_XREG_U = 8;
 constexpr int GEMV_U = 4;   // 1 KB weight loads in flight per wave
 
 template <class Epi>
@@ -337,6 +400,11 @@ hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, const Att
     } else {
       return hipErrorInvalidValue;
     }
+  } else if (B >= GEMV_XREG_MINB && K <= 32 * GEMV_XS * GEMV_KS && N / 16 > GEMV_XREG_WGS) {
+    // several row blocks per workgroup: at most GEMV_XREG_WGS workgroups
+    const int nrb = N / 16, per = (nrb + GEMV_XREG_WGS - 1) / GEMV_XREG_WGS;
+    hipLaunchKernelGGL((gemv_xreg_kernel<GEMV_KS, GEMV_XS, GEMV_XREG_U, Epi>), dim3((nrb + per - 1) / per), block, 0,
+                       st, (const f16x8*)Wt, X, N, B, K, epi);
   } else {
     hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE, false>), grid, block, 0, st,
                        (const f16x8*)Wt, X, N, B, K, epi, NormIn{}, AttnIn{});
