@@ -35,7 +35,6 @@ namespace hb {
 // single sequences keep PQ = 2 (7B S = 512, B = 1: 256 workgroups).
 constexpr int PK = 2;  // key blocks per iteration (key halves)
 
-HB_DEV int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
 // SPLIT: Q, K, V and the probabilities in two-term fp16 form (common.hpp):
 // each score and output product runs hi*hi + hi*lo + lo*hi MFMAs (the lo*lo
@@ -232,6 +231,7 @@ __global__ __launch_bounds__(PQ * PK * 64, SPLIT ? 1 : 2) void attn_prefill_kern
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[m][r] = o[m][r] * c0 + cw * s_o[(m * 16 + r) * 64 + lane];
 
+  if (p.lse && qi < p.S && h2 == 0) p.lse[((size_t)b * p.H + h) * p.q_rows + qi] = M + log2f(L);
   if (qi < p.S) {
     const float inv = 1.0f / L;
     f16* op = p.out + ((size_t)b * p.S + qi) * (SPLIT ? 2 * p.H * HD : p.H * HD) + h * HD;

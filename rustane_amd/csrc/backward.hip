@@ -309,64 +309,6 @@ hipError_t rmsnorm_backward(const float* dy, const float* x, const float* gamma,
 }
 size_t rmsnorm_backward_part_floats(int dim) { return (size_t)NORM_PARTS * dim; }
 
-// ---- attention softmax backward -------------------------------------------------
-// One wave per score row (kernels/sdpa_bwd.rs:46-161 restated row-wise): row
-// g of nrows holds query position s = g % Sp of one head; sc and dp are the
-// raw scores Q K^T and dP = dO V^T of that row over Sp keys. With
-// p = softmax(sc * scale) over keys j <= s (causal):
-//   dS_j = p_j (dP_j - sum_k p_k dP_k) * scale
-// P and dS are written as fp16 rows; masked keys and padding rows (s >= S)
-// are written as zero.
-__global__ __launch_bounds__(256) void attn_softmax_bwd_kernel(const float* __restrict__ sc,
-                                                               const float* __restrict__ dp,
-                                                               long nrows, int Sp, int S,
-                                                               float scale, f16* __restrict__ P,
-                                                               f16* __restrict__ dS) {
-  const long g = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (g >= nrows) return;
-  const int s = (int)(g % Sp);
-  const float* a = sc + g * Sp;
-  const float* b = dp + g * Sp;
-  f16* po = P + g * Sp;
-  f16* so = dS + g * Sp;
-  if (s >= S) {
-    for (int j = lane; j < Sp; j += 64) {
-      po[j] = (f16)0.f;
-      so[j] = (f16)0.f;
-    }
-    return;
-  }
-  float m = -INFINITY;
-  for (int j = lane; j <= s; j += 64) m = fmaxf(m, a[j] * scale);
-  m = wave_max(m);
-  float se = 0.f;
-  for (int j = lane; j <= s; j += 64) se += expf(a[j] * scale - m);
-  se = wave_sum(se);
-  const float inv = 1.0f / se;
-  float rs = 0.f;
-  for (int j = lane; j <= s; j += 64) rs += expf(a[j] * scale - m) * inv * b[j];
-  rs = wave_sum(rs);
-  for (int j = lane; j < Sp; j += 64) {
-    float p = 0.f, d = 0.f;
-    if (j <= s) {
-      p = expf(a[j] * scale - m) * inv;
-      d = p * (b[j] - rs) * scale;
-    }
-    po[j] = (f16)p;
-    so[j] = (f16)d;
-  }
-}
-
-hipError_t attn_softmax_backward(const float* sc, const float* dp, long nrows, int Sp, int S,
-                                 float scale, f16* P, f16* dS, hipStream_t st) {
-  if (nrows < 0 || Sp < S || S < 1) return hipErrorInvalidValue;
-  if (nrows == 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_softmax_bwd_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, st, sc,
-                     dp, nrows, Sp, S, scale, P, dS);
-  return hipGetLastError();
-}
-
 // ---- embedding backward -----------------------------------------------------------
 // dE[tok[t]] += dx[t] (cpu/embedding.rs:34-44 scatter-add) without atomics:
 // the workgroup of position t returns unless t is the first occurrence of its

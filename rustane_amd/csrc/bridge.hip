@@ -173,6 +173,7 @@ inline long round64(long v) { return (v + 63) & ~63L; }
 struct LayerAct {
   float *x, *x2, *h13;  // layer input, attention residual, FFN pre-activations h1|h3
   f16 *xn, *x2n, *q, *k, *v, *attn, *gate;
+  float* lse;  // [B][heads][Sp] attention log-sum-exp (log2 units) for the fused backward
 };
 
 struct TrainState {
@@ -189,11 +190,10 @@ struct TrainState {
   f16* xf = nullptr;
   uint32_t *tok = nullptr, *tgt = nullptr;
   float *dy = nullptr, *dx2 = nullptr, *dtmp = nullptr, *rinv = nullptr, *part = nullptr;
-  float *sc = nullptr, *dp = nullptr;
+  float* Drow = nullptr;  // [B][heads][Sp] rowsum(P * dP) of the attention backward
   f16 *d16 = nullptr, *d16T = nullptr, *dh = nullptr, *dhT = nullptr, *actT = nullptr;
   f16 *dqkv = nullptr, *dqkvT = nullptr, *dl = nullptr, *dlT = nullptr;
   f16 *dA = nullptr, *dAT = nullptr, *qT = nullptr, *kT = nullptr, *vt = nullptr;
-  f16 *P = nullptr, *PT = nullptr, *dS = nullptr, *dST = nullptr;
   // hb_train_forward left its activations for hb_train_backward (the
   // reference's ForwardResult.caches); any other training call clears it.
   bool kept = false;
@@ -2608,7 +2608,7 @@ int train_buffers(hb_model* m, int B, int S) {
   const long T = (long)B * S, Sp = round64(S), Tp = round64(T), Vp = round64(c.vocab);
   const long d = c.dim, h = c.hidden, q = c.q_dim, kv = c.kv_dim, qkv = q + 2 * kv, V = c.vocab;
   const long qh = (long)B * c.heads * Sp * c.hd, kvh = (long)B * c.kv_heads * Sp * c.hd;
-  const long scores = (long)B * c.heads * Sp * Sp;
+  const long qrows = (long)B * c.heads * Sp;  // per-query attention statistics
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t o = off;
@@ -2616,27 +2616,25 @@ int train_buffers(hb_model* m, int B, int S) {
     return o;
   };
   struct ActOff {
-    size_t x, x2, h13, xn, x2n, q, k, v, attn, gate;
+    size_t x, x2, h13, xn, x2n, q, k, v, attn, gate, lse;
   };
   std::vector<ActOff> ao(c.nlayers);
   for (auto& a : ao) {
     a.x = take(T * d * 4); a.x2 = take(T * d * 4); a.h13 = take(T * 2 * h * 4);
     a.xn = take(T * d * 2); a.x2n = take(T * d * 2); a.q = take(qh * 2); a.k = take(kvh * 2);
-    a.v = take(kvh * 2); a.attn = take(T * q * 2); a.gate = take(T * h * 2);
+    a.v = take(kvh * 2); a.attn = take(T * q * 2); a.gate = take(T * h * 2); a.lse = take(qrows * 4);
   }
   const size_t o_xL = take(T * d * 4), o_logits = take(T * V * 4), o_loss = take(T * 4),
                o_mean = take(4), o_xf = take(T * d * 2), o_tok = take(T * 4), o_tgt = take(T * 4);
   const size_t o_dy = take(T * d * 4), o_dx2 = take(T * d * 4), o_dtmp = take(T * d * 4),
                o_rinv = take(T * 4), o_part = take(rmsnorm_backward_part_floats(c.dim) * 4);
-  const size_t o_sc = take(scores * 4), o_dp = take(scores * 4);
+  const size_t o_D = take(qrows * 4);
   const long actw = std::max(std::max(h, d), q);
   const size_t o_d16 = take(T * d * 2), o_d16T = take(d * Tp * 2), o_dh = take(T * 2 * h * 2),
                o_dhT = take(2 * h * Tp * 2), o_actT = take(actw * Tp * 2), o_dqkv = take(T * qkv * 2),
                o_dqkvT = take(qkv * Tp * 2), o_dl = take(T * Vp * 2), o_dlT = take(V * Tp * 2);
   const size_t o_dA = take(qh * 2), o_dAT = take(qh * 2), o_qT = take(qh * 2), o_kT = take(kvh * 2),
                o_vt = take(kvh * 2);
-  const size_t o_P = take(scores * 2), o_PT = take(scores * 2), o_dS = take(scores * 2),
-               o_dST = take(scores * 2);
   hipStream_t st = m->ctx->stream();
   if (off > ts->abytes) {
     HIP_TRY(hipStreamSynchronize(st));
@@ -2654,20 +2652,19 @@ int train_buffers(hb_model* m, int B, int S) {
     A.x = (float*)(b + a.x); A.x2 = (float*)(b + a.x2); A.h13 = (float*)(b + a.h13);
     A.xn = (f16*)(b + a.xn); A.x2n = (f16*)(b + a.x2n); A.q = (f16*)(b + a.q); A.k = (f16*)(b + a.k);
     A.v = (f16*)(b + a.v); A.attn = (f16*)(b + a.attn); A.gate = (f16*)(b + a.gate);
+    A.lse = (float*)(b + a.lse);
   }
   ts->xL = (float*)(b + o_xL); ts->logits = (float*)(b + o_logits); ts->loss = (float*)(b + o_loss);
   ts->mean = (float*)(b + o_mean); ts->xf = (f16*)(b + o_xf); ts->tok = (uint32_t*)(b + o_tok);
   ts->tgt = (uint32_t*)(b + o_tgt);
   ts->dy = (float*)(b + o_dy); ts->dx2 = (float*)(b + o_dx2); ts->dtmp = (float*)(b + o_dtmp);
   ts->rinv = (float*)(b + o_rinv); ts->part = (float*)(b + o_part);
-  ts->sc = (float*)(b + o_sc); ts->dp = (float*)(b + o_dp);
+  ts->Drow = (float*)(b + o_D);
   ts->d16 = (f16*)(b + o_d16); ts->d16T = (f16*)(b + o_d16T); ts->dh = (f16*)(b + o_dh);
   ts->dhT = (f16*)(b + o_dhT); ts->actT = (f16*)(b + o_actT); ts->dqkv = (f16*)(b + o_dqkv);
   ts->dqkvT = (f16*)(b + o_dqkvT); ts->dl = (f16*)(b + o_dl); ts->dlT = (f16*)(b + o_dlT);
   ts->dA = (f16*)(b + o_dA); ts->dAT = (f16*)(b + o_dAT); ts->qT = (f16*)(b + o_qT);
   ts->kT = (f16*)(b + o_kT); ts->vt = (f16*)(b + o_vt);
-  ts->P = (f16*)(b + o_P); ts->PT = (f16*)(b + o_PT); ts->dS = (f16*)(b + o_dS);
-  ts->dST = (f16*)(b + o_dST);
   HIP_TRY(fill_f16_zero((f16*)b, off / 2, st));
   ts->B = B;
   ts->S = S;
@@ -2700,7 +2697,7 @@ int train_forward(hb_model* m, int B, int S) {
     AttnPrefill a{};
     a.q = A.q; a.q_rows = Sp; a.k = A.k; a.k_bstride = kbs; a.k_hstride = khs;
     a.vt = ts->vt; a.vt_ld = Sp; a.out = A.attn; a.B = B; a.S = S; a.H = c.heads;
-    a.KVH = c.kv_heads; a.hd = c.hd; a.scale = 1.0f / sqrtf((float)c.hd);
+    a.KVH = c.kv_heads; a.hd = c.hd; a.scale = 1.0f / sqrtf((float)c.hd); a.lse = A.lse;
     HIP_TRY(attention_prefill(a, st));
     GemmScratch so, s2;
     TRY(residual_scratch(m, c.dim, T, c.q_dim, so));
@@ -2717,43 +2714,31 @@ int train_forward(hb_model* m, int B, int S) {
   return HB_OK;
 }
 
-// Attention backward of one layer (kernels/sdpa_bwd.rs:46-161) on the MFMA
-// GEMM, batched over z = b*kv_heads + g with the rep = heads/kv_heads query
-// heads of a group stacked as rows r*Sp + s:
-//   scores = Q K^T, dP = dO V^T            [rep*Sp, Sp] fp32 per z
-//   P, dS = causal softmax backward          fp16, then transposed
-//   dQ = dS K        (W = K^T)               -> RoPE^-1 -> dQKV columns of Q
-//   dK = dS^T Q      (K-dim rep*Sp)          -> RoPE^-1 -> dQKV columns of K
-//   dV = P^T dO      (K-dim rep*Sp)          -> dQKV columns of V
-// The stacked K-dimension of dK and dV is the sum over the group's heads.
+// Attention backward of one layer (kernels/sdpa_bwd.rs:46-161): the fused
+// kernels (attention_bwd.hip) recompute P from Q, K and the forward's
+// log-sum-exp, with the operands they read as MFMA A fragments transposed
+// first (K^T, and the rep = heads/kv_heads query heads of a group stacked as
+// [hd][rep*Sp] for Q^T and dO^T), and write dQ, dK, dV with RoPE^-1 into the
+// dQKV rows and their transpose.
 int attention_backward(hb_model* m, const LayerAct& A, int B, int S) {
   const hb_model_config& c = m->cfg;
   TrainState* ts = m->train;
   hipStream_t st = m->ctx->stream();
   const int Sp = (int)round64(S), T = B * S, Tp = (int)round64(T);
   const int Z = B * c.kv_heads, rep = c.heads / c.kv_heads, Rq = rep * Sp, hd = c.hd;
-  const int qkv = c.q_dim + 2 * c.kv_dim;
-  const size_t khs = (size_t)Sp * hd, qzs = (size_t)Rq * hd, szs = (size_t)Rq * Sp;
-  const float scale = 1.0f / sqrtf((float)hd);
-  HIP_TRY(gemm_store_batched(A.k, A.q, Sp, Rq, hd, EpiStoreBatched{ts->sc, Sp, szs},
-                             GemmBatch{Z, khs, qzs}, st));
-  HIP_TRY(gemm_store_batched(A.v, ts->dA, Sp, Rq, hd, EpiStoreBatched{ts->dp, Sp, szs},
-                             GemmBatch{Z, khs, qzs}, st));
-  HIP_TRY(attn_softmax_backward(ts->sc, ts->dp, (long)Z * Rq, Sp, S, scale, ts->P, ts->dS, st));
-  HIP_TRY(transpose_f16(ts->dS, Rq, Sp, Sp, szs, ts->dST, Rq, szs, Z, st));
-  HIP_TRY(transpose_f16(ts->P, Rq, Sp, Sp, szs, ts->PT, Rq, szs, Z, st));
+  const size_t khs = (size_t)Sp * hd, qzs = (size_t)Rq * hd;
   HIP_TRY(transpose_f16(A.k, Sp, hd, hd, khs, ts->kT, Sp, khs, Z, st));
   HIP_TRY(transpose_f16(A.q, Rq, hd, hd, qzs, ts->qT, Rq, qzs, Z, st));
   HIP_TRY(transpose_f16(ts->dA, Rq, hd, hd, qzs, ts->dAT, Rq, qzs, Z, st));
-  EpiAttnGrad e{};
-  e.d = ts->dqkv; e.dt = ts->dqkvT; e.ld = qkv; e.tld = Tp; e.rows = Sp; e.kv_heads = c.kv_heads;
-  e.S = S; e.hd = hd; e.rope_ld = m->rope_len;
-  e.col0 = 0; e.hpz = rep; e.rope = m->rope;
-  HIP_TRY(gemm_attn_grad(ts->kT, ts->dS, hd, Rq, Sp, e, GemmBatch{Z, khs, szs}, st));
-  e.col0 = c.q_dim; e.hpz = 1;
-  HIP_TRY(gemm_attn_grad(ts->qT, ts->dST, hd, Sp, Rq, e, GemmBatch{Z, qzs, szs}, st));
-  e.col0 = c.q_dim + c.kv_dim; e.rope = nullptr;
-  HIP_TRY(gemm_attn_grad(ts->dAT, ts->PT, hd, Sp, Rq, e, GemmBatch{Z, qzs, szs}, st));
+  AttnBwd p{};
+  p.q = A.q; p.dO = ts->dA; p.k = A.k; p.v = A.v; p.qT = ts->qT; p.dOT = ts->dAT; p.kT = ts->kT;
+  p.lse = A.lse; p.D = ts->Drow;
+  p.B = B; p.S = S; p.Sp = Sp; p.H = c.heads; p.KVH = c.kv_heads; p.hd = hd;
+  p.scale = 1.0f / sqrtf((float)hd);
+  p.dqkv = ts->dqkv; p.dqkvT = ts->dqkvT; p.ld = c.q_dim + 2 * c.kv_dim; p.tld = Tp;
+  p.q_dim = c.q_dim; p.kv_dim = c.kv_dim; p.rope = m->rope; p.rope_ld = m->rope_len;
+  (void)T;
+  HIP_TRY(attention_backward_fused(p, st));
   return HB_OK;
 }
 

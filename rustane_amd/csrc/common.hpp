@@ -30,6 +30,12 @@ struct FastDiv {
   HB_DEV int div(int n) const { return (int)((__umulhi((uint32_t)n, m) + (uint32_t)n) >> s); }
 };
 
+// x with bits 2 and 3 swapped: the key (or query) held in row slot x of a
+// 32x32 MFMA tile whose A rows were loaded in that order, so that the 8
+// accumulator registers 8j..8j+7 of lane half h hold the consecutive
+// entries 16j+8h .. 16j+8h+7 (attention kernels).
+HB_DEV int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+
 // LDS-only workgroup barrier: orders LDS accesses of the workgroup without
 // draining outstanding global loads (a full __syncthreads would wait for the
 // prefetches that are meant to stay in flight across it).

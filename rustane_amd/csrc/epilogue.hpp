@@ -248,18 +248,6 @@ struct EpiQKV {
 
 // ---- training (backward) epilogues ----
 
-// c[blockIdx.z * bstride + t * ldc + f0 ..] = v: batched fp32 store (attention
-// scores and their gradient, one batch entry per sequence and KV head).
-struct EpiStoreBatched {
-  float* c;
-  int ldc;
-  size_t bstride;
-  HB_DEV void operator()(int t, int f0, f32x4 v) const {
-    float* p = c + blockIdx.z * bstride + (size_t)t * ldc + f0;
-    *(f32x4*)p = v;
-  }
-};
-
 // g[t * ld + f0 ..] += v: weight-gradient accumulation into the fp32 gradient
 // arena (layer.rs:1864-1867 accumulate_dw: dW += A B^T). Each element belongs
 // to exactly one lane of one tile, so the read-modify-write needs no atomics.
@@ -370,47 +358,6 @@ struct EpiHeads {
     o.z = (f16)v.z;
     o.w = (f16)v.w;
     *(f16x4*)(out + (((size_t)b * H + h) * rows + s) * hd + e) = o;
-  }
-};
-
-// dQ, dK or dV of one batch entry z = b*kv_heads + g of the attention backward
-// (rows r*rows + s: head g*hpz + r, position s) into the packed QKV gradient,
-// token-major d [T][ld] and feature-major dt [ld][tld], at columns
-// col0 + head*hd + e. Q and K gradients go through the inverse of the forward
-// RoPE rotation (layer.rs:1880-1897 rope_backward_inplace):
-//   dx[2i] = d[2i] c + d[2i+1] s,   dx[2i+1] = d[2i+1] c - d[2i] s.
-// Padding positions s >= S are dropped.
-struct EpiAttnGrad {
-  static constexpr int kMaxFT = 128;  // N = hd
-  f16* d;
-  f16* dt;
-  int ld, tld, col0, rows, hpz, kv_heads, S, hd;
-  const float2* rope;  // [hd/2][rope_ld], NULL for V
-  int rope_ld;
-  HB_DEV void operator()(int t, int f0, f32x4 v) const {
-    const int z = blockIdx.z, b = z / kv_heads, g = z - b * kv_heads;
-    const int r = t / rows, s = t - r * rows;
-    if (s >= S) return;
-    f32x4 o = v;
-    if (rope) {
-      const float2* rp = rope + (size_t)(f0 >> 1) * rope_ld + s;
-      const float2 c0 = rp[0], c1 = rp[rope_ld];
-      o.x = v.x * c0.x + v.y * c0.y;
-      o.y = v.y * c0.x - v.x * c0.y;
-      o.z = v.z * c1.x + v.w * c1.y;
-      o.w = v.w * c1.x - v.z * c1.y;
-    }
-    f16x4 h;
-    h.x = (f16)o.x;
-    h.y = (f16)o.y;
-    h.z = (f16)o.z;
-    h.w = (f16)o.w;
-    const int tok = b * S + s, col = col0 + (g * hpz + r) * hd + f0;
-    *(f16x4*)(d + (size_t)tok * ld + col) = h;
-    dt[(size_t)col * tld + tok] = h.x;
-    dt[(size_t)(col + 1) * tld + tok] = h.y;
-    dt[(size_t)(col + 2) * tld + tok] = h.z;
-    dt[(size_t)(col + 3) * tld + tok] = h.w;
   }
 };
 

@@ -321,15 +321,5 @@ hipError_t gemm_heads(const f16* W, const f16* X, int N, int T, int K, const Epi
   if (N != e.H * e.hd || e.hd % 4 || e.rows < e.S) return hipErrorInvalidValue;
   return launch_gemm(W, X, N, T, K, e, nullptr, st);
 }
-hipError_t gemm_store_batched(const f16* W, const f16* X, int N, int T, int K,
-                              const EpiStoreBatched& e, GemmBatch bt, hipStream_t st) {
-  if (N % 4 || e.ldc < N) return hipErrorInvalidValue;
-  return launch_gemm(W, X, N, T, K, e, nullptr, st, bt);
-}
-hipError_t gemm_attn_grad(const f16* W, const f16* X, int N, int T, int K, const EpiAttnGrad& e,
-                          GemmBatch bt, hipStream_t st) {
-  if (N != e.hd || e.hd % 4 || T != e.rows * e.hpz || e.rows < e.S) return hipErrorInvalidValue;
-  return launch_gemm(W, X, N, T, K, e, nullptr, st, bt);
-}
 
 }  // namespace hb

@@ -64,10 +64,6 @@ hipError_t gemm_silu_bwd(const f16* W, const f16* X, int N, int T, int K, const 
                          hipStream_t st);
 hipError_t gemm_heads(const f16* W, const f16* X, int N, int T, int K, const EpiHeads& e,
                       hipStream_t st);
-hipError_t gemm_store_batched(const f16* W, const f16* X, int N, int T, int K,
-                              const EpiStoreBatched& e, GemmBatch bt, hipStream_t st);
-hipError_t gemm_attn_grad(const f16* W, const f16* X, int N, int T, int K, const EpiAttnGrad& e,
-                          GemmBatch bt, hipStream_t st);
 
 // ---- decode GEMV (gemv.hip): rows of X are the B <= 16 sequences ----
 // W arguments are decode copies in fragment-tiled order (tile_decode); N is a
@@ -126,8 +122,37 @@ struct AttnPrefill {
   // Two-term fp16 inputs (common.hpp): low parts of q, k and vt in the same
   // layouts, all set or all NULL.
   const f16 *q_lo = nullptr, *k_lo = nullptr, *vt_lo = nullptr;
+  // Training: per-query log-sum-exp of the scaled scores in log2 units,
+  // lse[(b*H + h)*q_rows + s] = log2(sum_t exp2(sc[s,t] * scale * log2 e)),
+  // for the fused backward. NULL: not written.
+  float* lse = nullptr;
 };
 hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st);
+
+// Fused attention backward (kernels/sdpa_bwd.rs:46-161) for one layer of the
+// training forward: P is recomputed from Q, K and the forward's log-sum-exp,
+// so no score matrix is stored. Two launches:
+//   dQ:     per (2 query blocks, head, sequence): D = rowsum(P * dP), then
+//           dS = P (dP - D) scale and dQ = dS K, RoPE^-1
+//   dK, dV: per (2 key blocks, sequence and KV head), over the group's heads
+//           and the causal query blocks: dV = P^T dO, dK = dS^T Q, RoPE^-1
+// Outputs go to the dQKV rows (token-major, ld columns) and their transpose
+// (feature-major, tld tokens), as the unfused path writes them.
+struct AttnBwd {
+  const f16 *q, *dO;      // [B][H][Sp][hd]
+  const f16 *k, *v;       // [B][KVH][Sp][hd]
+  const f16 *qT, *dOT;    // per z = b*KVH + g: [hd][rep*Sp] (head r of the group at r*Sp)
+  const f16* kT;          // per z: [hd][Sp]
+  const float* lse;       // [B][H][Sp], from attention_prefill
+  float* D;               // [B][H][Sp] scratch, written by the dQ launch
+  int B, S, Sp, H, KVH, hd;
+  float scale;
+  f16 *dqkv, *dqkvT;
+  int ld, tld, q_dim, kv_dim;
+  const float2* rope;  // [hd/2][rope_ld]
+  int rope_ld;
+};
+hipError_t attention_backward_fused(const AttnBwd& p, hipStream_t st);
 
 struct AttnDecode {
   const f16* q;  // [B][H][hd]
@@ -255,9 +280,6 @@ hipError_t rmsnorm_backward(const float* dy, const float* x, const float* gamma,
                             int T, int dim, float eps, float* out, float* rinv, float* part,
                             float* dgamma, bool accumulate, hipStream_t st, float* sq = nullptr);
 size_t rmsnorm_backward_part_floats(int dim);
-// Causal softmax backward of nrows score rows of Sp keys (row g: position g % Sp).
-hipError_t attn_softmax_backward(const float* sc, const float* dp, long nrows, int Sp, int S,
-                                 float scale, f16* P, f16* dS, hipStream_t st);
 // dE[tok[t]] += dx[t], deterministic; tokens >= vocab are skipped.
 hipError_t embedding_backward(const float* dx, const uint32_t* tok, int T, int dim, int vocab,
                               float* dE, hipStream_t st);
