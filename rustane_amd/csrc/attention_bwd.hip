@@ -148,10 +148,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(sk[ko], qf[j], s, 0, 0, 0);
       dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv[ko], df[j], dp, 0, 0, 0);
     }
+    // masked entries get exp2(-inf) = 0: a select on the argument, no branch
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = kb * 32 + swap23(8 * (r >> 2) + 4 * h2 + (r & 3));
-      s[r] = (qok && key <= qi) ? exp2f(s[r] * sl2 - L2) : 0.f;
+      s[r] = exp2f((qok && key <= qi) ? s[r] * sl2 - L2 : -INFINITY);
     }
   };
 
@@ -345,14 +346,22 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(sq[qo], kf[j], s, 0, 0, 0);
       dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(sd[qo], vf[j], dp, 0, 0, 0);
     }
-    // rows are the queries qb*32 + swap23(slot), columns this lane's key ki
+    // rows are the queries qb*32 + swap23(slot), columns this lane's key ki;
+    // their log-sum-exp and D are read from LDS together, then masked
+    // entries get exp2(-inf) = 0 (a select on the argument, no branch)
+    float lq[16], dq[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int qq = swap23(8 * (e >> 2) + 4 * h2 + (e & 3));
-      const int qpos = qb * 32 + qq;
-      const float pe = (ki <= qpos && qpos < p.S) ? exp2f(s[e] * sl2 - s_ld[qh][0][qq]) : 0.f;
+      lq[e] = s_ld[qh][0][qq];
+      dq[e] = s_ld[qh][1][qq];
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int qpos = qb * 32 + swap23(8 * (e >> 2) + 4 * h2 + (e & 3));
+      const float pe = exp2f((ki <= qpos && qpos < p.S) ? s[e] * sl2 - lq[e] : -INFINITY);
       s[e] = pe;
-      dp[e] = pe * (dp[e] - s_ld[qh][1][qq]) * p.scale;
+      dp[e] = pe * (dp[e] - dq[e]) * p.scale;
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
