@@ -101,3 +101,17 @@ def test_layer0_gamma1_directional_derivative(trained_7b):
     finally:
         upload(base)
     _check(f"layer 0 {which}", g, u, lp, lm, eps)
+
+
+def test_gradient_norm_from_tile_sums_matches_full_pass(trained_7b):
+    """The norm hb_opt_grad_norm assembles from the backward's per-tile sums of
+    squares (fp32 per weight-gradient tile, thousands of slots at 7B) against
+    the full fp64 pass over the arena, which it takes once the raw arena
+    pointer has been handed out."""
+    cfg, k, opt, tok = trained_7b
+    from_tiles = opt.grad_norm()
+    opt.grad_arena()  # the next norm reads the whole arena
+    full = opt.grad_norm()
+    print(f"7B gradient norm: per-tile sums {from_tiles:.9e}, full pass {full:.9e}", flush=True)
+    assert np.isfinite(full) and full > 0
+    assert abs(from_tiles - full) <= 1e-5 * full, (from_tiles, full)
