@@ -15,16 +15,17 @@
 // at e*4 + (c ^ ((e >> 2) & 3))) gives A fragments of one hd row and 8
 // consecutive keys or queries.
 //
-// attn_bwd_dq_kernel, per (2 query blocks, head, sequence), 4 waves = 2 query
-// blocks x 2 key halves (as the forward): S^T = K Q^T and dP^T = V dO^T per
-// key block, two passes over the keys (D first, then dQ^T += K^T dS^T); the
-// key halves add their D and dQ through LDS.
+// attn_bwd_dq_kernel, per (PQ query blocks, head, sequence), 4 waves = PQ
+// query blocks x 4/PQ key parts: S^T = K Q^T and dP^T = V dO^T per key block,
+// two passes over the keys (D first, then dQ^T += K^T dS^T); with two key
+// halves (PQ = 2, as the forward) the halves add their D and dQ through LDS.
 //
-// attn_bwd_dkv_kernel, per (2 key blocks, sequence and KV head), 4 waves = 2
-// key blocks x 2 query halves: the wave's K and V rows stay in registers as B
-// operands, S = Q K^T and dP = dO V^T per query block of every head of the
-// group (the GQA sum over heads is the loop), dV^T += dO^T P and
-// dK^T += Q^T dS; the query halves add their partials through LDS.
+// attn_bwd_dkv_kernel, per (PB key blocks, sequence and KV head), 4 waves =
+// PB key blocks x 4/PB query parts: the wave's K and V rows stay in registers
+// as B operands, S = Q K^T and dP = dO V^T per query block of every head of
+// the group (the GQA sum over heads is the loop), dV^T += dO^T P and
+// dK^T += Q^T dS; with two query halves (PB = 2) the halves add their
+// partials through LDS.
 #include "internal.hpp"
 
 namespace hb {
@@ -68,14 +69,14 @@ HB_DEV int col_chunk(int e, int c) { return e * 4 + (c ^ ((e >> 2) & 3)); }  // 
 
 }  // namespace
 
-template <int HD>
+template <int HD, int PQ>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
-  constexpr int PQ = 2, PK = 2, PW = PQ * PK;
+  constexpr int PK = 4 / PQ, PW = PQ * PK;  // query blocks x key parts = 4 waves
   constexpr int KS = HD / 16, MB = HD / 32, NCH = HD / 8, KT8 = 4 * HD;
   constexpr int NKIND = 3;  // K rows, V rows, K^T columns
   constexpr int NLD = NKIND * PK * KT8 / (PW * 64);
   static_assert(NLD * PW * 64 == NKIND * PK * KT8, "loader coverage");
-  constexpr int NTILE = NKIND * PK * KT8, NMERGE = PQ * MB * 16 * 64 * 4 / 16;
+  constexpr int NTILE = NKIND * PK * KT8, NMERGE = PK == 2 ? PQ * MB * 16 * 64 * 4 / 16 : 0;
   __shared__ f16x8 s_t[NTILE > NMERGE ? NTILE : NMERGE];
   __shared__ float s_d[PQ][64];
 
@@ -172,13 +173,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
     for (int r = 0; r < 16; ++r) dsum += s[r] * dp[r];
   }
   dsum += __shfl_xor(dsum, 32, 64);  // both lanes of a query pair
-  if (kh == 1) s_d[qs][lane] = dsum;
-  lds_barrier();
-  const float Dq = kh == 0 ? dsum + s_d[qs][lane] : 0.f;
-  lds_barrier();
-  if (kh == 0) s_d[qs][lane] = Dq;
-  lds_barrier();
-  const float D = s_d[qs][lane];
+  float D = dsum;
+  if constexpr (PK == 2) {
+    if (kh == 1) s_d[qs][lane] = dsum;
+    lds_barrier();
+    const float Dq = kh == 0 ? dsum + s_d[qs][lane] : 0.f;
+    lds_barrier();
+    if (kh == 0) s_d[qs][lane] = Dq;
+    lds_barrier();
+    D = s_d[qs][lane];
+  }
   if (kh == 0 && qok && h2 == 0) p.D[qrow + qi] = D;
 
   // pass 2: dS^T = P (dP - D) scale, dQ^T += K^T dS^T
@@ -211,39 +215,46 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
     }
   }
 
-  // key half 1 hands its dQ^T to key half 0 (same lane, same slots)
-  float* s_o = (float*)s_t + qs * (MB * 16 * 64);
-  lds_barrier();
-  if (kh == 1) {
+  // with two key halves, half 1 hands its dQ^T to half 0 (same lane, same slots)
+  if constexpr (PK == 2) {
+    float* s_o = (float*)s_t + qs * (MB * 16 * 64);
+    lds_barrier();
+    if (kh == 1) {
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s_o[(m * 16 + r) * 64 + lane] = o[m][r];
+    }
+    lds_barrier();
+    if (kh == 1) return;
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s_o[(m * 16 + r) * 64 + lane] = o[m][r];
+      for (int r = 0; r < 16; ++r) o[m][r] += s_o[(m * 16 + r) * 64 + lane];
   }
-  lds_barrier();
-  if (kh == 1 || !qok) return;
+  if (!qok) return;
 #pragma unroll
   for (int m = 0; m < MB; ++m)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int f0 = m * 32 + 8 * g + 4 * h2;
       f32x4 v;
-      v.x = o[m][4 * g + 0] + s_o[(m * 16 + 4 * g + 0) * 64 + lane];
-      v.y = o[m][4 * g + 1] + s_o[(m * 16 + 4 * g + 1) * 64 + lane];
-      v.z = o[m][4 * g + 2] + s_o[(m * 16 + 4 * g + 2) * 64 + lane];
-      v.w = o[m][4 * g + 3] + s_o[(m * 16 + 4 * g + 3) * 64 + lane];
+      v.x = o[m][4 * g + 0];
+      v.y = o[m][4 * g + 1];
+      v.z = o[m][4 * g + 2];
+      v.w = o[m][4 * g + 3];
       store_grad4(p, b, qi, h * HD + f0, f0, v, true);
     }
 }
 
-template <int HD>
+template <int HD, int PB>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
-  constexpr int PB = 2, PH = 2, PW = PB * PH;  // key blocks x query halves
+  constexpr int PH = 4 / PB, PW = PB * PH;  // key blocks x query parts = 4 waves
   constexpr int KS = HD / 16, MB = HD / 32, NCH = HD / 8, KT8 = 4 * HD;
   constexpr int NKIND = 4;  // Q rows, dO rows, Q^T columns, dO^T columns
   constexpr int NLD = NKIND * PH * KT8 / (PW * 64);
   static_assert(NLD * PW * 64 == NKIND * PH * KT8, "loader coverage");
-  constexpr int NTILE = NKIND * PH * KT8, NMERGE = PB * 2 * MB * 16 * 64 * 4 / 16;
+  constexpr int NTILE = NKIND * PH * KT8, NMERGE = PH == 2 ? PB * 2 * MB * 16 * 64 * 4 / 16 : 0;
   __shared__ f16x8 s_t[NTILE > NMERGE ? NTILE : NMERGE];
   __shared__ float s_ld[PH][2][32];  // log-sum-exp and D of the iteration's query blocks
 
@@ -380,20 +391,31 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
     }
   }
 
-  // query half 1 hands its dK^T and dV^T to query half 0 of the same key block
-  float* s_o = (float*)s_t + kbi * (2 * MB * 16 * 64);
-  lds_barrier();
-  if (qh == 1) {
+  // with two query halves, half 1 hands its dK^T and dV^T to half 0 of the
+  // same key block
+  if constexpr (PH == 2) {
+    float* s_o = (float*)s_t + kbi * (2 * MB * 16 * 64);
+    lds_barrier();
+    if (qh == 1) {
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          s_o[(m * 16 + e) * 64 + lane] = dk[m][e];
+          s_o[((MB + m) * 16 + e) * 64 + lane] = dv[m][e];
+        }
+    }
+    lds_barrier();
+    if (qh == 1) return;
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        s_o[(m * 16 + e) * 64 + lane] = dk[m][e];
-        s_o[((MB + m) * 16 + e) * 64 + lane] = dv[m][e];
+        dk[m][e] += s_o[(m * 16 + e) * 64 + lane];
+        dv[m][e] += s_o[((MB + m) * 16 + e) * 64 + lane];
       }
   }
-  lds_barrier();
-  if (qh == 1 || !active || ki >= p.S) return;
+  if (!active || ki >= p.S) return;
   const int colk = p.q_dim + g * HD, colv = p.q_dim + p.kv_dim + g * HD;
 #pragma unroll
   for (int m = 0; m < MB; ++m)
@@ -401,31 +423,47 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
     for (int q4 = 0; q4 < 4; ++q4) {
       const int f0 = m * 32 + 8 * q4 + 4 * h2;
       f32x4 a, c;
-      a.x = dk[m][4 * q4 + 0] + s_o[(m * 16 + 4 * q4 + 0) * 64 + lane];
-      a.y = dk[m][4 * q4 + 1] + s_o[(m * 16 + 4 * q4 + 1) * 64 + lane];
-      a.z = dk[m][4 * q4 + 2] + s_o[(m * 16 + 4 * q4 + 2) * 64 + lane];
-      a.w = dk[m][4 * q4 + 3] + s_o[(m * 16 + 4 * q4 + 3) * 64 + lane];
-      c.x = dv[m][4 * q4 + 0] + s_o[((MB + m) * 16 + 4 * q4 + 0) * 64 + lane];
-      c.y = dv[m][4 * q4 + 1] + s_o[((MB + m) * 16 + 4 * q4 + 1) * 64 + lane];
-      c.z = dv[m][4 * q4 + 2] + s_o[((MB + m) * 16 + 4 * q4 + 2) * 64 + lane];
-      c.w = dv[m][4 * q4 + 3] + s_o[((MB + m) * 16 + 4 * q4 + 3) * 64 + lane];
+      a.x = dk[m][4 * q4 + 0];
+      a.y = dk[m][4 * q4 + 1];
+      a.z = dk[m][4 * q4 + 2];
+      a.w = dk[m][4 * q4 + 3];
+      c.x = dv[m][4 * q4 + 0];
+      c.y = dv[m][4 * q4 + 1];
+      c.z = dv[m][4 * q4 + 2];
+      c.w = dv[m][4 * q4 + 3];
       store_grad4(p, b, ki, colk + f0, f0, a, true);
       store_grad4(p, b, ki, colv + f0, f0, c, false);
     }
 }
 
+namespace {
+// Four query blocks (dQ) or four key blocks (dK/dV) per workgroup share each
+// staged tile once that still leaves two workgroups per CU (7B, one sequence
+// of 2048: forward + backward 136.1 -> 129.5 ms); otherwise two blocks, with
+// the key or query range split in halves.
+constexpr long HB_BWD_WIDE_MIN = 512;
+template <int HD>
+void launch_bwd(const AttnBwd& p, hipStream_t st) {
+  const int nb = (p.S + 31) / 32;
+  const dim3 block(256);
+  if ((long)((nb + 3) / 4) * p.H * p.B >= HB_BWD_WIDE_MIN)
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, 4>), dim3((nb + 3) / 4, p.H, p.B), block, 0, st, p);
+  else
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, 2>), dim3((nb + 1) / 2, p.H, p.B), block, 0, st, p);
+  if ((long)((nb + 3) / 4) * p.B * p.KVH >= HB_BWD_WIDE_MIN)
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD, 4>), dim3((nb + 3) / 4, p.B * p.KVH), block, 0, st, p);
+  else
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD, 2>), dim3((nb + 1) / 2, p.B * p.KVH), block, 0, st, p);
+}
+}  // namespace
+
 hipError_t attention_backward_fused(const AttnBwd& p, hipStream_t st) {
   if (p.S < 1 || p.Sp < p.S || p.Sp % 32 || p.H % p.KVH || (p.hd != 64 && p.hd != 128) || !p.lse || !p.D)
     return hipErrorInvalidValue;
-  const int nb = (p.S + 31) / 32;
-  const dim3 gq((nb + 1) / 2, p.H, p.B), gkv((nb + 1) / 2, p.B * p.KVH), block(256);
-  if (p.hd == 128) {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<128>, gq, block, 0, st, p);
-    hipLaunchKernelGGL(attn_bwd_dkv_kernel<128>, gkv, block, 0, st, p);
-  } else {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, gq, block, 0, st, p);
-    hipLaunchKernelGGL(attn_bwd_dkv_kernel<64>, gkv, block, 0, st, p);
-  }
+  if (p.hd == 128)
+    launch_bwd<128>(p, st);
+  else
+    launch_bwd<64>(p, st);
   return hipGetLastError();
 }
 
