@@ -76,8 +76,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
   constexpr int NKIND = 3;  // K rows, V rows, K^T columns
   constexpr int NLD = NKIND * PK * KT8 / (PW * 64);
   static_assert(NLD * PW * 64 == NKIND * PK * KT8, "loader coverage");
+  // two tile buffers: iteration n computes from buffer n & 1 while the tiles
+  // of n + 1 go into the other one (one barrier per iteration)
   constexpr int NTILE = NKIND * PK * KT8, NMERGE = PK == 2 ? PQ * MB * 16 * 64 * 4 / 16 : 0;
-  __shared__ f16x8 s_t[NTILE > NMERGE ? NTILE : NMERGE];
+  __shared__ f16x8 s_t[2 * NTILE > NMERGE ? 2 * NTILE : NMERGE];
   __shared__ float s_d[PQ][64];
 
   const int tid = threadIdx.x, lane = tid & 63, h2 = lane >> 5, li = lane & 31;
@@ -123,24 +125,40 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
       }
     }
   };
-  auto lstore = [&](bool with_t) {
+  auto lstore = [&](int buf, bool with_t) {
+    f16x8* st = s_t + buf * NTILE;
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int x = i * PW * 64 + tid, tile = x / KT8, y = x % KT8;
       if (tile / PK < 2)
-        s_t[tile * KT8 + row_chunk<HD>(y / NCH, y % NCH)] = reg[i];
+        st[tile * KT8 + row_chunk<HD>(y / NCH, y % NCH)] = reg[i];
       else if (with_t)
-        s_t[tile * KT8 + col_chunk(y >> 2, y & 3)] = reg[i];
+        st[tile * KT8 + col_chunk(y >> 2, y & 3)] = reg[i];
     }
   };
 
   const float sl2 = p.scale * HB_LOG2E;
   const int krow = swap23(li);
   const int niter = (nkb + PK - 1) / PK;
+  // the key loop of one pass: body(n, tile buffer) on every iteration's tiles
+  auto keyloop = [&](bool with_t, auto&& body) {
+    gload(0, with_t);
+    lstore(0, with_t);
+    if (niter > 1) gload(1, with_t);
+    lds_barrier();
+    for (int n = 0; n < niter; ++n) {
+      body(n, s_t + (n & 1) * NTILE);
+      if (n + 1 < niter) {
+        lstore((n + 1) & 1, with_t);  // that buffer was last read in iteration n - 1
+        if (n + 2 < niter) gload(n + 2, with_t);
+      }
+      lds_barrier();
+    }
+  };
   // S^T and dP^T of key block kb against this wave's queries; s becomes P
-  auto block = [&](int kb, f32x16& s, f32x16& dp) {
-    const f16x8* sk = s_t + kh * KT8;
-    const f16x8* sv = s_t + (PK + kh) * KT8;
+  auto block = [&](const f16x8* st, int kb, f32x16& s, f32x16& dp) {
+    const f16x8* sk = st + kh * KT8;
+    const f16x8* sv = st + (PK + kh) * KT8;
     s = f32x16{};
     dp = f32x16{};
 #pragma unroll
@@ -159,19 +177,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
 
   // pass 1: D = rowsum(P * dP) over this wave's key half, then over both
   float dsum = 0.f;
-  gload(0, false);
-  for (int n = 0; n < niter; ++n) {
-    lds_barrier();
-    lstore(false);
-    lds_barrier();
-    if (n + 1 < niter) gload(n + 1, false);
+  keyloop(false, [&](int n, const f16x8* st) {
     const int kb = n * PK + kh;
-    if (!active || kb > qb) continue;  // wave-uniform
+    if (!active || kb > qb) return;  // wave-uniform
     f32x16 s, dp;
-    block(kb, s, dp);
+    block(st, kb, s, dp);
 #pragma unroll
     for (int r = 0; r < 16; ++r) dsum += s[r] * dp[r];
-  }
+  });
   dsum += __shfl_xor(dsum, 32, 64);  // both lanes of a query pair
   float D = dsum;
   if constexpr (PK == 2) {
@@ -189,19 +202,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
   f32x16 o[MB];
 #pragma unroll
   for (int m = 0; m < MB; ++m) o[m] = f32x16{};
-  gload(0, true);
-  for (int n = 0; n < niter; ++n) {
-    lds_barrier();
-    lstore(true);
-    lds_barrier();
-    if (n + 1 < niter) gload(n + 1, true);
+  keyloop(true, [&](int n, const f16x8* st) {
     const int kb = n * PK + kh;
-    if (!active || kb > qb) continue;
+    if (!active || kb > qb) return;
     f32x16 s, dp;
-    block(kb, s, dp);
+    block(st, kb, s, dp);
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = s[r] * (dp[r] - D) * p.scale;
-    const f16x8* skt = s_t + (2 * PK + kh) * KT8;
+    const f16x8* skt = st + (2 * PK + kh) * KT8;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       f16x8 db;
@@ -213,12 +221,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
         o[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(skt[col_chunk(e, 2 * j + h2)], db, o[m], 0, 0, 0);
       }
     }
-  }
+  });
 
-  // with two key halves, half 1 hands its dQ^T to half 0 (same lane, same slots)
+  // with two key halves, half 1 hands its dQ^T to half 0 (same lane, same
+  // slots); the key loop ended on a barrier, so the tile buffers are free
   if constexpr (PK == 2) {
     float* s_o = (float*)s_t + qs * (MB * 16 * 64);
-    lds_barrier();
     if (kh == 1) {
 #pragma unroll
       for (int m = 0; m < MB; ++m)
@@ -254,9 +262,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
   constexpr int NKIND = 4;  // Q rows, dO rows, Q^T columns, dO^T columns
   constexpr int NLD = NKIND * PH * KT8 / (PW * 64);
   static_assert(NLD * PW * 64 == NKIND * PH * KT8, "loader coverage");
+  // two tile buffers (one barrier per iteration, as in the dQ kernel)
   constexpr int NTILE = NKIND * PH * KT8, NMERGE = PH == 2 ? PB * 2 * MB * 16 * 64 * 4 / 16 : 0;
-  __shared__ f16x8 s_t[NTILE > NMERGE ? NTILE : NMERGE];
-  __shared__ float s_ld[PH][2][32];  // log-sum-exp and D of the iteration's query blocks
+  __shared__ f16x8 s_t[2 * NTILE > NMERGE ? 2 * NTILE : NMERGE];
+  __shared__ float s_ld[2][PH][2][32];  // log-sum-exp and D of the iteration's query blocks
 
   const int tid = threadIdx.x, lane = tid & 63, h2 = lane >> 5, li = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -316,16 +325,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
       aux = qpos < p.S ? (which ? p.D[idx] : p.lse[idx]) : 0.f;
     }
   };
-  auto lstore = [&]() {
+  auto lstore = [&](int buf) {
+    f16x8* st = s_t + buf * NTILE;
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int x = i * PW * 64 + tid, tile = x / KT8, y = x % KT8;
       if (tile / PH < 2)
-        s_t[tile * KT8 + row_chunk<HD>(y / NCH, y % NCH)] = reg[i];
+        st[tile * KT8 + row_chunk<HD>(y / NCH, y % NCH)] = reg[i];
       else
-        s_t[tile * KT8 + col_chunk(y >> 2, y & 3)] = reg[i];
+        st[tile * KT8 + col_chunk(y >> 2, y & 3)] = reg[i];
     }
-    if (tid < PH * 2 * 32) s_ld[tid / 64][(tid >> 5) & 1][tid & 31] = aux;
+    if (tid < PH * 2 * 32) s_ld[buf][tid / 64][(tid >> 5) & 1][tid & 31] = aux;
   };
 
   const float sl2 = p.scale * HB_LOG2E;
@@ -336,20 +346,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
     dk[m] = f32x16{};
     dv[m] = f32x16{};
   }
-  gload(0);
-  for (int n = 0; n < niter; ++n) {
-    lds_barrier();
-    lstore();
-    lds_barrier();
-    if (n + 1 < niter) gload(n + 1);
-    if (!active || n * PH + qh >= npairs) continue;  // wave-uniform
+  auto body = [&](int n, int buf) {
+    if (!active || n * PH + qh >= npairs) return;  // wave-uniform
     int r, qb;
     pair_of(n, qh, r, qb);
-    if (qb < kb) continue;  // every query of the block precedes every key
-    const f16x8* sq = s_t + (0 * PH + qh) * KT8;
-    const f16x8* sd = s_t + (1 * PH + qh) * KT8;
-    const f16x8* sqt = s_t + (2 * PH + qh) * KT8;
-    const f16x8* sdt = s_t + (3 * PH + qh) * KT8;
+    if (qb < kb) return;  // every query of the block precedes every key
+    const f16x8* st = s_t + buf * NTILE;
+    const f16x8* sq = st + (0 * PH + qh) * KT8;
+    const f16x8* sd = st + (1 * PH + qh) * KT8;
+    const f16x8* sqt = st + (2 * PH + qh) * KT8;
+    const f16x8* sdt = st + (3 * PH + qh) * KT8;
     f32x16 s = {}, dp = {};
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
@@ -364,8 +370,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int qq = swap23(8 * (e >> 2) + 4 * h2 + (e & 3));
-      lq[e] = s_ld[qh][0][qq];
-      dq[e] = s_ld[qh][1][qq];
+      lq[e] = s_ld[buf][qh][0][qq];
+      dq[e] = s_ld[buf][qh][1][qq];
     }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -389,13 +395,24 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
         dk[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sqt[c], db, dk[m], 0, 0, 0);
       }
     }
+  };
+  gload(0);
+  lstore(0);
+  if (niter > 1) gload(1);
+  lds_barrier();
+  for (int n = 0; n < niter; ++n) {
+    body(n, n & 1);
+    if (n + 1 < niter) {
+      lstore((n + 1) & 1);  // that buffer was last read in iteration n - 1
+      if (n + 2 < niter) gload(n + 2);
+    }
+    lds_barrier();
   }
 
   // with two query halves, half 1 hands its dK^T and dV^T to half 0 of the
-  // same key block
+  // same key block (the loop ended on a barrier: the tile buffers are free)
   if constexpr (PH == 2) {
     float* s_o = (float*)s_t + kbi * (2 * MB * 16 * 64);
-    lds_barrier();
     if (qh == 1) {
 #pragma unroll
       for (int m = 0; m < MB; ++m)
