@@ -69,9 +69,9 @@ HB_DEV int col_chunk(int e, int c) { return e * 4 + (c ^ ((e >> 2) & 3)); }  // 
 
 }  // namespace
 
-template <int HD, int PQ>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
-  constexpr int PK = 4 / PQ, PW = PQ * PK;  // query blocks x key parts = 4 waves
+template <int HD, int PQ, int PK>
+__global__ __launch_bounds__(PQ * PK * 64, 1) void attn_bwd_dq_kernel(AttnBwd p) {
+  constexpr int PW = PQ * PK;  // waves: query blocks x key parts
   constexpr int KS = HD / 16, MB = HD / 32, NCH = HD / 8, KT8 = 4 * HD;
   constexpr int NKIND = 3;  // K rows, V rows, K^T columns
   constexpr int NLD = NKIND * PK * KT8 / (PW * 64);
@@ -255,9 +255,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwd p) {
     }
 }
 
-template <int HD, int PB>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
-  constexpr int PH = 4 / PB, PW = PB * PH;  // key blocks x query parts = 4 waves
+template <int HD, int PB, int PH>
+__global__ __launch_bounds__(PB * PH * 64, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
+  constexpr int PW = PB * PH;  // waves: key blocks x query parts
   constexpr int KS = HD / 16, MB = HD / 32, NCH = HD / 8, KT8 = 4 * HD;
   constexpr int NKIND = 4;  // Q rows, dO rows, Q^T columns, dO^T columns
   constexpr int NLD = NKIND * PH * KT8 / (PW * 64);
@@ -456,21 +456,36 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(AttnBwd p) {
 namespace {
 // Four query blocks (dQ) or four key blocks (dK/dV) per workgroup share each
 // staged tile once that still leaves two workgroups per CU (7B, one sequence
-// of 2048: forward + backward 136.1 -> 129.5 ms); otherwise two blocks, with
-// the key or query range split in halves.
+// of 2048: forward + backward 136.1 -> 129.5 ms; 8 query blocks for dQ:
+// 125.0 -> 119.9 ms); otherwise two blocks, with the key or query range split
+// in halves.
 constexpr long HB_BWD_WIDE_MIN = 512;
 template <int HD>
 void launch_bwd(const AttnBwd& p, hipStream_t st) {
   const int nb = (p.S + 31) / 32;
-  const dim3 block(256);
-  if ((long)((nb + 3) / 4) * p.H * p.B >= HB_BWD_WIDE_MIN)
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, 4>), dim3((nb + 3) / 4, p.H, p.B), block, 0, st, p);
+  const long hb = (long)p.H * p.B, zb = (long)p.KVH * p.B;
+  // dQ: 8 query blocks per workgroup (8 waves, hd = 128 only: one K, V and
+  // K^T tile set covers 512 threads' loads) while that still gives every CU
+  // one workgroup, else 4 with two workgroups per CU, else 2 with the key
+  // range split in halves. dK/dV: 4 key blocks, else 2 with the query range
+  // split (8 waves would need the K and V rows out of registers: the wave's
+  // dK, dV, K and V already fill 224 of its 256 registers)
+  bool dq8 = false;
+  if constexpr (HD == 128) {
+    if ((long)((nb + 7) / 8) * hb >= HB_BWD_WIDE_MIN / 2) {
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, 8, 1>), dim3((nb + 7) / 8, p.H, p.B), dim3(512), 0, st, p);
+      dq8 = true;
+    }
+  }
+  if (dq8) {
+  } else if ((long)((nb + 3) / 4) * hb >= HB_BWD_WIDE_MIN)
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, 4, 1>), dim3((nb + 3) / 4, p.H, p.B), dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, 2>), dim3((nb + 1) / 2, p.H, p.B), block, 0, st, p);
-  if ((long)((nb + 3) / 4) * p.B * p.KVH >= HB_BWD_WIDE_MIN)
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD, 4>), dim3((nb + 3) / 4, p.B * p.KVH), block, 0, st, p);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, 2, 2>), dim3((nb + 1) / 2, p.H, p.B), dim3(256), 0, st, p);
+  if ((long)((nb + 3) / 4) * zb >= HB_BWD_WIDE_MIN)
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD, 4, 1>), dim3((nb + 3) / 4, p.B * p.KVH), dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD, 2>), dim3((nb + 1) / 2, p.B * p.KVH), block, 0, st, p);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD, 2, 2>), dim3((nb + 1) / 2, p.B * p.KVH), dim3(256), 0, st, p);
 }
 }  // namespace
 
