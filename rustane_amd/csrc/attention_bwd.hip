@@ -15,13 +15,13 @@
 // at e*4 + (c ^ ((e >> 2) & 3))) gives A fragments of one hd row and 8
 // consecutive keys or queries.
 //
-// attn_bwd_dq_kernel, per (PQ query blocks, head, sequence), 4 waves = PQ
-// query blocks x 4/PQ key parts: S^T = K Q^T and dP^T = V dO^T per key block,
-// two passes over the keys (D first, then dQ^T += K^T dS^T); with two key
-// halves (PQ = 2, as the forward) the halves add their D and dQ through LDS.
+// attn_bwd_dq_kernel, per (PQ query blocks, head, sequence), PQ x PK waves
+// (PK key parts): S^T = K Q^T and dP^T = V dO^T per key block, two passes
+// over the keys (D first, then dQ^T += K^T dS^T); with two key halves
+// (PQ = 2, as the forward) the halves add their D and dQ through LDS.
 //
-// attn_bwd_dkv_kernel, per (PB key blocks, sequence and KV head), 4 waves =
-// PB key blocks x 4/PB query parts: the wave's K and V rows stay in registers
+// attn_bwd_dkv_kernel, per (PB key blocks, sequence and KV head), PB x PH
+// waves (PH query parts): the wave's K and V rows stay in registers
 // as B operands, S = Q K^T and dP = dO V^T per query block of every head of
 // the group (the GQA sum over heads is the loop), dV^T += dO^T P and
 // dK^T += Q^T dS; with two query halves (PB = 2) the halves add their
