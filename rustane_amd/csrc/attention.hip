@@ -32,15 +32,16 @@ namespace hb {
 // PQ = 4 (8 waves) for long or many sequences: each key block then serves 128
 // queries instead of 64, halving the L2 traffic per MFMA, once there are
 // enough groups of 4 query blocks to give every CU two workgroups; short
-// single sequences keep PQ = 2 (7B S = 512, B = 1: 256 workgroups).
-constexpr int PK = 2;  // key blocks per iteration (key halves)
+// single sequences keep PQ = 2 (7B S = 512, B = 1: 256 workgroups). PQ = 8
+// with PK = 1 (8 waves, each over the whole key range of its query block, no
+// merge) once groups of 8 still give every CU one workgroup.
 
 
 // SPLIT: Q, K, V and the probabilities in two-term fp16 form (common.hpp):
 // each score and output product runs hi*hi + hi*lo + lo*hi MFMAs (the lo*lo
 // term is below fp32 rounding of the sum), and the output rows are split rows.
-template <int HD, bool SPLIT, int PQ>
-__global__ __launch_bounds__(PQ * PK * 64, SPLIT ? 1 : 2) void attn_prefill_kernel(AttnPrefill p) {
+template <int HD, bool SPLIT, int PQ, int PK>
+__global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn_prefill_kernel(AttnPrefill p) {
   constexpr int PW = PQ * PK;          // waves
   constexpr int KS = HD / 16;          // k-steps over head dim
   constexpr int MB = HD / 32;          // 32-row blocks of O^T
@@ -53,7 +54,7 @@ __global__ __launch_bounds__(PQ * PK * 64, SPLIT ? 1 : 2) void attn_prefill_kern
   // V^T tiles (block kh: row e, chunk c at (PK+kh)*KT8 + e*4 + (c ^ ((e >> 2) & 3))),
   // then (SPLIT) the same two for the low parts; after the loop the region
   // holds the key-half-1 waves' O for the merge
-  constexpr int NTILE = NKIND * PK * KT8, NMERGE = PQ * MB * 16 * 64 * 4 / 16;
+  constexpr int NTILE = NKIND * PK * KT8, NMERGE = PK == 2 ? PQ * MB * 16 * 64 * 4 / 16 : 0;
   __shared__ f16x8 s_kv[NTILE > NMERGE ? NTILE : NMERGE];
   __shared__ float s_ml[PQ][2][64];
   const int tid = threadIdx.x, lane = tid & 63, h2 = lane >> 5, li = lane & 31;
@@ -209,27 +210,32 @@ __global__ __launch_bounds__(PQ * PK * 64, SPLIT ? 1 : 2) void attn_prefill_kern
   // query block (a wave with no key block has m = -inf and weight 0). Lane l
   // of both waves holds the same (query, row) slots, so the exchange is one
   // float per lane per register.
-  float* s_o = (float*)s_kv + qs * (MB * 16 * 64);  // [MB*16][64] per query block
-  lds_barrier();  // every wave is done with the tiles
-  if (kh == 1) {
+  float M = mrun, L = lrun;
+  if constexpr (PK == 2) {
+    float* s_o = (float*)s_kv + qs * (MB * 16 * 64);  // [MB*16][64] per query block
+    lds_barrier();  // every wave is done with the tiles
+    if (kh == 1) {
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s_o[(m * 16 + r) * 64 + lane] = o[m][r];
+      s_ml[qs][0][lane] = mrun;
+      s_ml[qs][1][lane] = lrun;
+    }
+    lds_barrier();
+    if (kh == 1 || !active) return;
+    const float mw = s_ml[qs][0][lane];
+    M = fmaxf(mrun, mw);
+    const float c0 = exp2f(mrun - M);  // key half 0 always holds block 0, so mrun is finite
+    const float cw = mw == -INFINITY ? 0.f : exp2f(mw - M);
+    L = lrun * c0 + cw * s_ml[qs][1][lane];
 #pragma unroll
     for (int m = 0; m < MB; ++m)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s_o[(m * 16 + r) * 64 + lane] = o[m][r];
-    s_ml[qs][0][lane] = mrun;
-    s_ml[qs][1][lane] = lrun;
+      for (int r = 0; r < 16; ++r) o[m][r] = o[m][r] * c0 + cw * s_o[(m * 16 + r) * 64 + lane];
+  } else {
+    if (!active) return;
   }
-  lds_barrier();
-  if (kh == 1 || !active) return;
-  const float mw = s_ml[qs][0][lane];
-  const float M = fmaxf(mrun, mw);
-  const float c0 = exp2f(mrun - M);  // key half 0 always holds block 0, so mrun is finite
-  const float cw = mw == -INFINITY ? 0.f : exp2f(mw - M);
-  const float L = lrun * c0 + cw * s_ml[qs][1][lane];
-#pragma unroll
-  for (int m = 0; m < MB; ++m)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[m][r] = o[m][r] * c0 + cw * s_o[(m * 16 + r) * 64 + lane];
 
   if (p.lse && qi < p.S && h2 == 0) p.lse[((size_t)b * p.H + h) * p.q_rows + qi] = M + log2f(L);
   if (qi < p.S) {
@@ -251,19 +257,19 @@ __global__ __launch_bounds__(PQ * PK * 64, SPLIT ? 1 : 2) void attn_prefill_kern
 }
 
 namespace {
-template <int PQ>
+template <int PQ, int PK>
 hipError_t launch_prefill(const AttnPrefill& p, hipStream_t st) {
   const int nqb = (p.S + 31) / 32;
   dim3 grid((nqb + PQ - 1) / PQ, p.H, p.B), block(PQ * PK * 64);
   const bool split = p.q_lo != nullptr;
   if (p.hd == 128 && split)
-    hipLaunchKernelGGL((attn_prefill_kernel<128, true, PQ>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_prefill_kernel<128, true, PQ, PK>), grid, block, 0, st, p);
   else if (p.hd == 128)
-    hipLaunchKernelGGL((attn_prefill_kernel<128, false, PQ>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_prefill_kernel<128, false, PQ, PK>), grid, block, 0, st, p);
   else if (p.hd == 64 && split)
-    hipLaunchKernelGGL((attn_prefill_kernel<64, true, PQ>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_prefill_kernel<64, true, PQ, PK>), grid, block, 0, st, p);
   else if (p.hd == 64)
-    hipLaunchKernelGGL((attn_prefill_kernel<64, false, PQ>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_prefill_kernel<64, false, PQ, PK>), grid, block, 0, st, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -272,11 +278,14 @@ hipError_t launch_prefill(const AttnPrefill& p, hipStream_t st) {
 
 hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
   if (p.q_lo != nullptr && (!p.k_lo || !p.vt_lo)) return hipErrorInvalidValue;
-  // PQ = 4 once it still gives two workgroups per CU (measured on the 7B
-  // shape: seq 2048 forward 33.2 -> 32.75 ms at B = 1, 239.6 -> 237.2 at B = 8)
+  // PQ = 8 (one workgroup per CU) or 4 (two) when the grid still fills the
+  // GPU (measured on the 7B shape: seq 2048 forward at B = 1 33.2 ms with
+  // PQ = 2, 32.75 with 4, 31.5 -> 31.2 with 8; seq 512 at B = 8 55.7 -> 55.2)
   const int nqb = (p.S + 31) / 32;
-  const long wide = (long)((nqb + 3) / 4) * p.H * p.B;  // workgroups with PQ = 4
-  return wide >= 512 ? launch_prefill<4>(p, st) : launch_prefill<2>(p, st);
+  const long hb = (long)p.H * p.B;
+  if ((long)((nqb + 7) / 8) * hb >= 256) return launch_prefill<8, 1>(p, st);
+  if ((long)((nqb + 3) / 4) * hb >= 512) return launch_prefill<4, 2>(p, st);
+  return launch_prefill<2, 2>(p, st);
 }
 
 // ---- decode: split the context into chunks of 512-key blocks ----------------
