@@ -115,6 +115,25 @@ def test_tiny_mha_full_sequence():
     st.close()
 
 
+def test_long_sequence_attention_kernels_hd128():
+    """Enough (query block, head, sequence) groups -- 16 sequences of 500 at 8
+    heads of 128 -- that the attention kernels take the variants the 7B shape
+    runs at one sequence of 2048: the forward and the dQ kernel with 8 query
+    blocks per workgroup, dK/dV with 4 key blocks; S = 500 keeps the padding
+    rows."""
+    cfg = tiny_config(dim=1024, hidden=512, heads=8, kv_heads=8, hd=128, nlayers=1, seq=512, vocab=512)
+    _, st, *_ = _run_case(cfg, 16, 500, seed=21)
+    st.close()
+
+
+def test_long_sequence_attention_kernels_hd64_gqa():
+    """The same at hd = 64 with GQA 16/8: dQ with 4 query blocks per
+    workgroup (8 is for hd = 128), dK/dV summing two query heads per group."""
+    cfg = tiny_config(dim=1024, hidden=512, heads=16, kv_heads=8, hd=64, nlayers=1, seq=512, vocab=512)
+    _, st, *_ = _run_case(cfg, 16, 500, seed=22)
+    st.close()
+
+
 def test_tiny_gqa_two_sequences_ragged_length():
     """GQA (dK/dV summed over each group's query heads) and S = 33, not a
     multiple of 64, so every padding row and column is exercised."""
