@@ -288,54 +288,61 @@ hipError_t attention_prefill(const AttnPrefill& p, hipStream_t st) {
   return launch_prefill<2, 2>(p, st);
 }
 
-// ---- decode: split the context into chunks of 512-key blocks ----------------
-// Grid (chunk, head, sequence), 16 waves per chunk, 32 keys of each 512-key
-// block per wave. hd/8 lanes share one key row (16-byte loads; one wave
-// instruction reads 1 KB of consecutive key rows). Per block each lane issues
-// all of its K and V loads before using any (V does not depend on the
+// ---- decode: split the context into chunks --------------------------------
+// Grid (chunk, head, sequence), NW waves per chunk. hd/8 lanes share one key
+// row (16-byte loads): one wave instruction reads KPW consecutive key rows
+// (1 KB), and the NW waves' instructions together cover one stripe of
+// NW * KPW keys; a block is NIT stripes (NW * 32 keys). Per block each lane
+// issues all of its K and V loads before using any (V does not depend on the
 // scores); each wave keeps its own online softmax state across the chunk's
-// blocks, and the 16 waves merge through LDS into one partial (max, sum,
+// blocks, and the waves merge through LDS into one partial (max, sum,
 // unnormalised output) per chunk -- or, when one chunk spans the whole
-// context, straight into the normalised fp16 attention row. Chunks past the
-// current position exit at once, so the launch shape does not depend on the
-// position (one HIP graph replays every step).
+// context, straight into the normalised fp16 attention row.
 //
-// Chunk length: enough chunks for about 256 workgroups over the B x H
-// (sequence, head) pairs, at most one per 512-key block. On the 7B shape
-// (32 heads) that is 5 one-block chunks at B = 1 and a single chunk at
-// B >= 8 (no partials, no combine). Measured on MI355X, 512-key blocks on 16
-// waves stream the cache as fast as 128- or 256-key blocks on 4 or 8 waves.
+// Chunks: n per (sequence, head), sized at every step from the position
+// (attn_chunk_keys: keys 0..pos in n near-equal ranges), so each of the
+// B x H x n workgroups streams the same share of the cache whatever the
+// position, and the launch shape does not depend on it (one HIP graph
+// replays every step). n is enough for about 256 workgroups (one per CU), at
+// most one per 512 keys of capacity: 5 chunks per head on the 7B shape at
+// B = 1 and 2304 keys, one at B >= 8 (no partials, no combine), where 8-wave
+// workgroups let two run on a CU, their blocks interleaving (B = 16: 97.5
+// against 99.3 us per layer with 16 waves, one workgroup per CU). At B = 1
+// the kernel is not bound by its workgroup count: 8 chunks of ~270 keys
+// (256 workgroups) take the same 11.0 us as 5, and the Wo prologue's combine
+// of 8 partials costs 0.8 us more.
 //
 // With several chunks the partials are combined by the consumer -- the Wo
 // GEMV prologue (gemv.hip) when B * chunks is small -- or by
 // attn_combine_kernel below, which folds them in the same order with the
 // same arithmetic, so both give the same attention output.
-constexpr int DBLOCK = 512;
-constexpr int DWAVES = 16;
+constexpr int DMIN_CHUNK = 512;  // fewest keys of ctx_max per chunk
 
 AttnChunking attn_decode_chunking(int ctx_max, int B, int H) {
-  const int nblk = (ctx_max + DBLOCK - 1) / DBLOCK;
-  const int want = std::max(1, std::min(nblk, 256 / std::max(1, B * H)));
-  const int per = (nblk + want - 1) / want;  // blocks per chunk
-  return AttnChunking{(nblk + per - 1) / per, per * DBLOCK};
+  const int bh = std::max(1, B * H);
+  const int most = std::max(1, (ctx_max + DMIN_CHUNK - 1) / DMIN_CHUNK);
+  const int n = std::max(1, std::min(most, 256 / bh));
+  return AttnChunking{n, n == 1 && bh >= 256 ? 8 : 16};
 }
 
 // SPLIT: q, K and V come in two-term fp16 form (common.hpp) and are summed to
 // fp32 as they are loaded (the arithmetic is fp32 throughout).
-template <int HD, bool SPLIT>
-__global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) {
-  constexpr int NT = DWAVES * 64;
-  constexpr int LPK = HD / 8;             // lanes per key row
-  constexpr int KPW = 64 / LPK;           // keys per wave instruction
-  constexpr int WKEYS = DBLOCK / DWAVES;  // keys per wave and block
-  constexpr int NIT = WKEYS / KPW;
-  __shared__ float s_m[DWAVES], s_l[DWAVES];
-  __shared__ float s_o[DWAVES][HD];
+template <int HD, bool SPLIT, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_decode_kernel(AttnDecode p) {
+  constexpr int NT = NW * 64;
+  constexpr int LPK = HD / 8;       // lanes per key row
+  constexpr int KPW = 64 / LPK;     // keys per wave instruction
+  constexpr int STRIPE = NW * KPW;  // keys per instruction of all waves
+  constexpr int NIT = 32 / KPW;     // instructions per block (32 keys per wave)
+  constexpr int BLOCK = NIT * STRIPE;
+  __shared__ float s_m[NW], s_l[NW];
+  __shared__ float s_o[NW][HD];
 
   const int pos = *p.d_pos;
-  const int c0 = blockIdx.x * p.chunk;
+  const int cl = attn_chunk_keys(pos, gridDim.x);
+  const int c0 = blockIdx.x * cl;
   if (c0 > pos) return;
-  const int cend = min(c0 + p.chunk, pos + 1);  // keys c0 .. cend-1
+  const int cend = min(c0 + cl, pos + 1);  // keys c0 .. cend-1
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (p.H / p.KVH);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -358,16 +365,16 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
 
   // Online softmax state of this lane's keys (m is wave-uniform).
   float m = -INFINITY, l = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int b0 = c0; b0 < cend; b0 += DBLOCK) {
-    const int kbase = b0 + wave * WKEYS + g;
+  for (int b0 = c0; b0 < cend; b0 += BLOCK) {
+    const int kbase = b0 + wave * KPW + g;  // key of instruction i: kbase + i * STRIPE
     constexpr int NL = SPLIT ? NIT : 1;
     f16x8 kr[NIT], krl[NL];
     const f16x8 zero8 = {};
 #pragma unroll
     for (int i = 0; i < NIT; ++i) {
-      const int kk = kbase + i * KPW;
-      kr[i] = kk <= pos ? *(const f16x8*)(kb + (size_t)kk * HD) : zero8;
-      if constexpr (SPLIT) krl[i] = kk <= pos ? *(const f16x8*)(p.k_lo + kvo + (size_t)kk * HD) : zero8;
+      const int kk = kbase + i * STRIPE;
+      kr[i] = kk < cend ? *(const f16x8*)(kb + (size_t)kk * HD) : zero8;
+      if constexpr (SPLIT) krl[i] = kk < cend ? *(const f16x8*)(p.k_lo + kvo + (size_t)kk * HD) : zero8;
     }
     // Without low parts the V loads go out with K's, before the scores. With
     // them they follow the scores, in two halves, so that K's registers are
@@ -377,9 +384,9 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
     auto load_v = [&](int i0) {
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        const int kk = kbase + (i0 + i) * KPW;
-        vr[i] = kk <= pos ? *(const f16x8*)(vb + (size_t)kk * HD) : zero8;
-        if constexpr (SPLIT) vrl[i] = kk <= pos ? *(const f16x8*)(p.v_lo + kvo + (size_t)kk * HD) : zero8;
+        const int kk = kbase + (i0 + i) * STRIPE;
+        vr[i] = kk < cend ? *(const f16x8*)(vb + (size_t)kk * HD) : zero8;
+        if constexpr (SPLIT) vrl[i] = kk < cend ? *(const f16x8*)(p.v_lo + kvo + (size_t)kk * HD) : zero8;
       }
     };
     if constexpr (!SPLIT) load_v(0);
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
       for (int e = 0; e < 8; ++e) d += qf[e] * kval(i, e);
 #pragma unroll
       for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-      sc[i] = (kbase + i * KPW <= pos) ? d * sl2 : -INFINITY;
+      sc[i] = (kbase + i * STRIPE < cend) ? d * sl2 : -INFINITY;
     }
     // wave-wide max over this block's keys (lanes of a group hold equal scores)
     float mb = sc[0];
@@ -440,13 +447,13 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
   __syncthreads();
   float M = s_m[0];
 #pragma unroll
-  for (int v = 1; v < DWAVES; ++v) M = fmaxf(M, s_m[v]);
-  // Wave weights exp2(m_w - M); a wave whose keys are all past pos has
+  for (int v = 1; v < NW; ++v) M = fmaxf(M, s_m[v]);
+  // Wave weights exp2(m_w - M); a wave whose keys are all past the chunk has
   // m_w = -inf and weight 0.
   auto wt = [&](int v) { return s_m[v] == -INFINITY ? 0.f : exp2f(s_m[v] - M); };
   float L = 0.f;
 #pragma unroll
-  for (int v = 0; v < DWAVES; ++v) L += wt(v) * s_l[v];
+  for (int v = 0; v < NW; ++v) L += wt(v) * s_l[v];
   const size_t head = (size_t)b * p.H + h;
   if (gridDim.x == 1) {
     // One chunk: the normalised attention row, fp16 (split rows [B][2*H*hd]
@@ -455,7 +462,7 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
     for (int e = tid; e < HD; e += NT) {
       float o = 0.f;
 #pragma unroll
-      for (int v = 0; v < DWAVES; ++v) o += wt(v) * s_o[v][e];
+      for (int v = 0; v < NW; ++v) o += wt(v) * s_o[v][e];
       o *= iL;
       const f16 hi = (f16)o;
       if (p.q_lo) {
@@ -472,7 +479,7 @@ __global__ __launch_bounds__(DWAVES * 64) void attn_decode_kernel(AttnDecode p) 
   for (int e = tid; e < HD; e += NT) {
     float o = 0.f;
 #pragma unroll
-    for (int v = 0; v < DWAVES; ++v) o += wt(v) * s_o[v][e];
+    for (int v = 0; v < NW; ++v) o += wt(v) * s_o[v][e];
     p.part_o[slot * HD + e] = o;
   }
   if (tid == 0) {
@@ -489,7 +496,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecode p, int nch
   constexpr int GPH = HD / 8;
   const int gid = blockIdx.x * 256 + threadIdx.x;
   if (gid >= p.B * p.H * GPH) return;
-  const int nvalid = min(*p.d_pos / p.chunk + 1, nch);
+  const int nvalid = attn_chunks_valid(*p.d_pos, nch);
   const int bh = gid / GPH, e0 = (gid % GPH) * 8;
   const float* pml = p.part_ml + (size_t)bh * nch * 2;
   const float* po = p.part_o + (size_t)bh * nch * HD + e0;
@@ -523,28 +530,36 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecode p, int nch
   *(f16x8*)(p.out + (size_t)bh * HD + e0) = o;
 }
 
-hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
-  const AttnChunking ch = attn_decode_chunking(p.ctx_max, p.B, p.H);
-  if (p.chunk != ch.keys) return hipErrorInvalidValue;
-  dim3 grid(ch.n, p.H, p.B), block(DWAVES * 64);
-  const bool split = p.q_lo != nullptr;
-  if (split && (!p.k_lo || !p.v_lo)) return hipErrorInvalidValue;
+namespace {
+template <int NW>
+hipError_t launch_decode(const AttnDecode& p, dim3 grid, bool split, hipStream_t st) {
+  const dim3 block(NW * 64);
   if (p.hd == 128 && split)
-    hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_decode_kernel<128, true, NW>), grid, block, 0, st, p);
   else if (p.hd == 128)
-    hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_decode_kernel<128, false, NW>), grid, block, 0, st, p);
   else if (p.hd == 64 && split)
-    hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_decode_kernel<64, true, NW>), grid, block, 0, st, p);
   else if (p.hd == 64)
-    hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((attn_decode_kernel<64, false, NW>), grid, block, 0, st, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
 }
+}  // namespace
+
+hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
+  const AttnChunking ch = attn_decode_chunking(p.ctx_max, p.B, p.H);
+  if (p.nch != ch.n) return hipErrorInvalidValue;
+  const dim3 grid(ch.n, p.H, p.B);
+  const bool split = p.q_lo != nullptr;
+  if (split && (!p.k_lo || !p.v_lo)) return hipErrorInvalidValue;
+  return ch.waves == 8 ? launch_decode<8>(p, grid, split, st) : launch_decode<16>(p, grid, split, st);
+}
 
 hipError_t attention_combine(const AttnDecode& p, hipStream_t st) {
   const AttnChunking ch = attn_decode_chunking(p.ctx_max, p.B, p.H);
-  if (p.chunk != ch.keys || ch.n < 2) return hipErrorInvalidValue;
+  if (p.nch != ch.n || ch.n < 2) return hipErrorInvalidValue;
   const int nch = ch.n;
   const int n = p.B * p.H * (p.hd / 8);
   if (p.hd == 128)

@@ -224,7 +224,6 @@ struct hb_kv {
   uint32_t *d_tok = nullptr, *d_next = nullptr, *d_hist = nullptr;
   float *x = nullptr, *x2 = nullptr, *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
   bool attn_in_wo = false;       // chunk partials combined by the Wo GEMV
-  int chunk = 0;                 // keys per attention chunk
   float* amax_val = nullptr;  // greedy argmax partials [B][vocab/16]
   int* amax_idx = nullptr;
   f16 *xn = nullptr, *qd = nullptr, *attn = nullptr, *gate = nullptr;
@@ -2218,7 +2217,7 @@ int enqueue_decode_layer_split(hb_kv* kv, int l, const KVTarget& t, hipStream_t 
   AttnDecode a{};
   a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
   a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
-  a.ctx_max = kv->ctx_cap; a.chunk = kv->chunk; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
+  a.ctx_max = kv->ctx_cap; a.nch = kv->nch; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
   a.part_ml = kv->part_ml; a.out = kv->attn;
   a.q_lo = kv->qd_lo; a.k_lo = t.k_lo; a.v_lo = t.v_lo;
   HIP_TRY(attention_decode(a, st));
@@ -2269,11 +2268,11 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     AttnDecode a{};
     a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
     a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
-    a.ctx_max = kv->ctx_cap; a.chunk = kv->chunk; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
+    a.ctx_max = kv->ctx_cap; a.nch = kv->nch; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
     a.part_ml = kv->part_ml; a.out = kv->attn;
     HIP_TRY(attention_decode(a, st));
     if (kv->nch > 1 && !kv->attn_in_wo) HIP_TRY(attention_combine(a, st));
-    const AttnIn ain{kv->part_o, kv->part_ml, kv->d_pos, c.heads, c.hd, kv->nch, kv->chunk};
+    const AttnIn ain{kv->part_o, kv->part_ml, kv->d_pos, c.heads, c.hd, kv->nch};
     HIP_TRY(gemv_residual(L.t_wo, kv->attn, kv->attn_in_wo ? &ain : nullptr, c.dim, B, c.q_dim,
                           EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
     HIP_TRY(prep_norm(kv->x2, L.g2, n2));
@@ -2345,7 +2344,6 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   kv->ctx_cap = (ctx_max + 63) & ~63;
   const AttnChunking ach = attn_decode_chunking(kv->ctx_cap, batch, m->cfg.heads);
   kv->nch = ach.n;
-  kv->chunk = ach.keys;
   kv->attn_in_wo = kv->nch > 1 && gemv_attn_fits(batch, m->cfg.q_dim, kv->nch);
   int r = ensure_rope(m, kv->ctx_cap);
   if (r != HB_OK) {

@@ -30,6 +30,17 @@ struct FastDiv {
   HB_DEV int div(int n) const { return (int)((__umulhi((uint32_t)n, m) + (uint32_t)n) >> s); }
 };
 
+// Decode-attention chunks at position pos (keys 0..pos) for n chunks per
+// (sequence, head): chunk c holds keys [c * len, min((c + 1) * len, pos + 1))
+// with len = ceil((pos + 1) / n); the first ceil((pos + 1) / len) <= n chunks
+// hold keys. The attention kernel, the Wo GEMV's combine prologue and the
+// combine kernel all take the split from here.
+__host__ __device__ inline int attn_chunk_keys(int pos, int n) { return (pos + n) / n; }
+__host__ __device__ inline int attn_chunks_valid(int pos, int n) {
+  const int len = attn_chunk_keys(pos, n);
+  return (pos + len) / len;
+}
+
 // x with bits 2 and 3 swapped: the key (or query) held in row slot x of a
 // 32x32 MFMA tile whose A rows were loaded in that order, so that the 8
 // accumulator registers 8j..8j+7 of lane half h hold the consecutive

@@ -30,10 +30,10 @@
 // path; it is used while the B staged rows fit in GEMV_NORM_LDS bytes.
 //
 // Attention prologue (Wo only): the decode attention leaves one partial
-// (max, sum, unnormalised output) per 512-key chunk, and every Wo workgroup
-// merges them into the fp16 attention rows it needs (all of them) in the same
-// way. With B * chunks <= GEMV_ATTN_MAXCH that is at most 8 x 130 floats per
-// (sequence, head) -- 133 KB per workgroup on the 7B shape at 4096 context --
+// (max, sum, unnormalised output) per chunk of the context, and every Wo
+// workgroup merges them into the fp16 attention rows it needs (all of them)
+// in the same way. With B * chunks <= GEMV_ATTN_MAXCH that is at most
+// 8 x 130 floats per (sequence, head) -- 133 KB per workgroup on the 7B shape --
 // fetched while the first weight loads are in flight, instead of a separate
 // combine launch (attention_combine, used when B * chunks is larger).
 #include <type_traits>
@@ -116,7 +116,7 @@ HB_DEV void stage_norm(const NormIn& nin, int B, int K, f16* s_x) {
 }
 
 // attn[b][h*hd + e] = fp16(sum_c w_c o_c[e] / sum_c w_c l_c), w_c = exp2(m_c - M),
-// M = max_c m_c over the chunks c <= *d_pos / chunk of attention_decode -- the
+// M = max_c m_c over the chunks of attention_decode that hold keys -- the
 // arithmetic and chunk order of attention_combine. One 8-dim group of one
 // (sequence, head) per thread and pass: the chunk maxima first, then the
 // chunk outputs in batches of 8 with every load of a batch issued before any
@@ -125,7 +125,7 @@ template <int NT>
 HB_DEV void stage_attn(const AttnIn& ai, int B, int K, f16* s_x) {
   constexpr int MAXCH = GEMV_ATTN_MAXCH;
   constexpr int CB = 8;  // chunk outputs in flight per batch
-  const int nvalid = min(*ai.d_pos / ai.chunk + 1, ai.nch);
+  const int nvalid = attn_chunks_valid(*ai.d_pos, ai.nch);
   const int gph = ai.hd / 8;
   const int ngroups = B * ai.H * gph;
   const int ld = xn_ld(K);
@@ -445,9 +445,11 @@ hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C
 }
 
 // ---- greedy token: reduce the argmax partials, advance the decode state ----
-// One workgroup of 256 threads per call; for each sequence every thread folds
-// a strided share of the partials (8 loads in flight per batch), then the
-// block reduces through LDS, with the same rules as argmax_partial. With
+// One workgroup of 16 waves per call, 16 / B waves (at least one) per
+// sequence, all sequences at once: each wave folds a strided share of its
+// sequence's partials (8 loads in flight per batch), then the sequence's
+// waves reduce through LDS, with the same rules as argmax_partial (the
+// result is the first index of the maximum whatever the folding order). With
 // tok/d_pos set it also does the decode-step bookkeeping: the token becomes
 // the next step's input, is appended to the history at row (pos - pos0), and
 // the position advances.
@@ -458,27 +460,30 @@ HB_DEV void amax_fold(float& best, int& idx, float v, int j) {
   }
 }
 
-__global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* __restrict__ pval,
-                                                            const int* __restrict__ pidx, int nblk,
-                                                            int B, uint32_t* __restrict__ next,
-                                                            uint32_t* tok, uint32_t* hist,
-                                                            int* d_pos, const int* d_pos0) {
+constexpr int AMAX_WAVES = 16;
+
+__global__ __launch_bounds__(AMAX_WAVES * 64) void argmax_reduce_kernel(
+    const float* __restrict__ pval, const int* __restrict__ pidx, int nblk, int B,
+    uint32_t* __restrict__ next, uint32_t* tok, uint32_t* hist, int* d_pos, const int* d_pos0) {
   constexpr int NB = 8;
-  __shared__ float s_v[4];
-  __shared__ int s_i[4];
+  __shared__ float s_v[AMAX_WAVES];
+  __shared__ int s_i[AMAX_WAVES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wps = max(1, AMAX_WAVES / B);  // waves per sequence
+  const int b = wave / wps, r = wave - b * wps;
   const int pos = d_pos ? *d_pos : 0;
-  for (int b = 0; b < B; ++b) {
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  if (b < B) {
     const float* pv = pval + (size_t)b * nblk;
     const int* pi = pidx + (size_t)b * nblk;
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i0 = tid; i0 < nblk; i0 += 256 * NB) {
+    const int stride = wps * 64;
+    for (int i0 = r * 64 + lane; i0 < nblk; i0 += stride * NB) {
       float v[NB];
       int j[NB];
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
-        const int i = i0 + u * 256;
+        const int i = i0 + u * stride;
         v[u] = i < nblk ? pv[i] : -INFINITY;
         j[u] = i < nblk ? pi[i] : 0x7fffffff;
       }
@@ -487,29 +492,28 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* __restr
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax_fold(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
-    if (lane == 0) {
-      s_v[wave] = best;
-      s_i[wave] = idx;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int w = 1; w < 4; ++w) amax_fold(best, idx, s_v[w], s_i[w]);
-      next[b] = (uint32_t)idx;
-      if (tok) {
-        tok[b] = (uint32_t)idx;
-        if (hist) hist[(size_t)(pos - *d_pos0) * B + b] = (uint32_t)idx;
-      }
-    }
-    __syncthreads();  // s_v reuse
   }
-  if (d_pos && tid == 0) *d_pos = pos + 1;  // every thread read *d_pos before the first barrier
+  if (lane == 0) {
+    s_v[wave] = best;
+    s_i[wave] = idx;
+  }
+  __syncthreads();  // also: every thread has read *d_pos
+  if (b < B && r == 0 && lane == 0) {
+    for (int w = 1; w < wps; ++w) amax_fold(best, idx, s_v[wave + w], s_i[wave + w]);
+    next[b] = (uint32_t)idx;
+    if (tok) {
+      tok[b] = (uint32_t)idx;
+      if (hist) hist[(size_t)(pos - *d_pos0) * B + b] = (uint32_t)idx;
+    }
+  }
+  if (d_pos && tid == 0) *d_pos = pos + 1;
 }
 
 hipError_t argmax_reduce(const float* pval, const int* pidx, int nblk, int B, uint32_t* next,
                          uint32_t* tok, uint32_t* hist, int* d_pos, const int* d_pos0,
                          hipStream_t st) {
   if (B < 1 || B > 16 || nblk < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(256), 0, st, pval, pidx, nblk, B, next,
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(AMAX_WAVES * 64), 0, st, pval, pidx, nblk, B, next,
                      tok, hist, d_pos, d_pos0);
   return hipGetLastError();
 }

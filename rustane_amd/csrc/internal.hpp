@@ -85,8 +85,8 @@ bool gemv_norm_fits(int B, int K);
 struct AttnIn {
   const float* part_o;   // [B][H][nch][hd]
   const float* part_ml;  // [B][H][nch][2]
-  const int* d_pos;      // chunks 0..*d_pos/chunk hold keys
-  int H, hd, nch, chunk;
+  const int* d_pos;      // chunks attn_chunks_valid(*d_pos, nch) hold keys
+  int H, hd, nch;
 };
 constexpr int GEMV_ATTN_MAXCH = 8;  // B * nch limit of the in-GEMV combine
 bool gemv_attn_fits(int B, int K, int nch);
@@ -161,7 +161,7 @@ struct AttnDecode {
   size_t bstride, hstride;
   const int* d_pos;  // keys 0..*d_pos are attended
   int B, H, KVH, hd, ctx_max;
-  int chunk;  // keys per chunk: attn_decode_chunking(ctx_max, B, H).keys
+  int nch;  // chunks per (sequence, head): attn_decode_chunking(ctx_max, B, H).n
   float scale;
   float* part_o;   // [B][H][nchunks][hd] unnormalised chunk outputs
   float* part_ml;  // [B][H][nchunks][2] chunk (max, sum) in log2 units
@@ -172,13 +172,14 @@ struct AttnDecode {
   // [B][2*H*hd].
   const f16 *q_lo = nullptr, *k_lo = nullptr, *v_lo = nullptr;
 };
-// Chunks of the decode context for B sequences of H heads: n chunks of `keys`
-// keys each (a multiple of 512), n * keys >= ctx_max.
+// Chunks of the decode context for B sequences of H heads: n chunks per
+// (sequence, head), each attn_chunk_keys(pos, n) keys long at position pos,
+// run by workgroups of `waves` waves.
 struct AttnChunking {
-  int n, keys;
+  int n, waves;
 };
 AttnChunking attn_decode_chunking(int ctx_max, int B, int H);
-// Partials of chunks 0..*d_pos/chunk; the Wo GEMV prologue or
+// Partials of the chunks that hold keys; the Wo GEMV prologue or
 // attention_combine turns them into the attention output. With one chunk
 // the kernel writes the attention rows (out) itself.
 hipError_t attention_decode(const AttnDecode& p, hipStream_t st);

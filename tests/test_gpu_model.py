@@ -221,10 +221,12 @@ def test_decode_separate_norm_path_matches_fused(m48):
 
 
 def test_decode_long_context_both_chunk_combines(m48):
-    """A 1030-token prompt spans three 512-key attention chunks. At batch 1 the
-    Wo GEMV combines the chunk partials (checked against the oracle); at batch 4
-    (4 x 3 chunks is past that path's limit of 8) a separate combine kernel
-    does, and its rows must agree with the batch-1 decoder."""
+    """A 1030-token prompt on 8 heads: the 1088-key capacity gives three
+    attention chunks per head (one per 512 keys of capacity, ~344 keys each at
+    this position). At batch 1 the Wo GEMV combines the chunk partials
+    (checked against the oracle); at batch 4 (4 x 3 chunks is past that
+    path's limit of 8) a separate combine kernel does, and its rows must agree
+    with the batch-1 decoder."""
     cfg, w, k = m48
     P, steps = 1030, 3
     tok = tokens_for(cfg, 4 * (P + steps), seed=71).reshape(4, P + steps)
