@@ -63,9 +63,13 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
   const int nqb = (p.S + 31) / 32;
   const int ngr = (nqb + PQ - 1) / PQ;
   const int gr = ngr - 1 - blockIdx.x;  // heaviest groups first
-  const int qb = gr * PQ + qs;          // >= nqb: this wave has no queries
+  // group gr holds the query blocks gr, gr + ngr, gr + 2 ngr, ...: every
+  // group spans the sequence, so the groups' causal work is nearly equal
+  // (contiguous groups left most CUs idle behind the last one); the
+  // arithmetic of a query block does not depend on its group
+  const int qb = gr + ngr * qs;  // >= nqb: this wave has no queries
   const bool active = qb < nqb;
-  const int nkb = min(gr * PQ + PQ, nqb);  // key blocks the group needs
+  const int nkb = gr + ngr * min(PQ - 1, (nqb - 1 - gr) / ngr) + 1;  // key blocks the group needs
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (p.H / p.KVH);
   const int q0 = qb * 32;
