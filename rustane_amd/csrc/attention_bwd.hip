@@ -87,9 +87,11 @@ __global__ __launch_bounds__(PQ * PK * 64, 1) void attn_bwd_dq_kernel(AttnBwd p)
   const int qs = wave % PQ, kh = wave / PQ;
   const int nqb = (p.S + 31) / 32, ngr = (nqb + PQ - 1) / PQ;
   const int gr = ngr - 1 - blockIdx.x;  // heaviest groups first
-  const int qb = gr * PQ + qs;
+  // query blocks gr, gr + ngr, ... (as in the forward kernel: groups of
+  // nearly equal causal work)
+  const int qb = gr + ngr * qs;
   const bool active = qb < nqb;
-  const int nkb = min(gr * PQ + PQ, nqb);
+  const int nkb = gr + ngr * min(PQ - 1, (nqb - 1 - gr) / ngr) + 1;
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (p.H / p.KVH), z = b * p.KVH + kvh;
   const int qi = qb * 32 + li;
@@ -272,12 +274,15 @@ __global__ __launch_bounds__(PB * PH * 64, 1) void attn_bwd_dkv_kernel(AttnBwd p
   const int kbi = wave % PB, qh = wave / PB;
   const int nb = (p.S + 31) / 32;  // key blocks = query blocks
   const int grp = blockIdx.x;      // group 0 sees the most query blocks: launched first
-  const int kb = grp * PB + kbi;
+  // key blocks grp, grp + ngr, ...: every group spans the sequence, so the
+  // groups' causal work is nearly equal
+  const int ngr = (nb + PB - 1) / PB;
+  const int kb = grp + ngr * kbi;
   const bool active = kb < nb;
   const int z = blockIdx.y, b = z / p.KVH, g = z - b * p.KVH;
   const int rep = p.H / p.KVH;
   const int ki = kb * 32 + li;
-  const int qstart = grp * PB;          // first query block that sees the group's keys
+  const int qstart = grp;              // first query block that sees the group's keys
   const int nq = nb - qstart;           // query blocks per head
   const int npairs = rep * nq;          // (head, query block) pairs
   const int niter = (npairs + PH - 1) / PH;
