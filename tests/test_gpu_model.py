@@ -155,6 +155,35 @@ def test_decode_teacher_forced_matches_oracle(m48):
     assert dec.length() == P + steps
 
 
+def test_decode_short_prompt_in_a_long_cache(m48):
+    """A 1-token prompt in a 2048-key cache: each head's context is split into
+    4 attention chunks sized from the position, so the first steps run chunks
+    of one key next to chunks that hold none. Batch 1 (partials combined in
+    the Wo GEMV) against the oracle, teacher-forced; batch 3 (3 x 4 chunks:
+    the separate combine kernel) row by row against batch 1."""
+    cfg, w, k = m48
+    P, steps, ctx = 1, 7, 2048
+    tok = tokens_for(cfg, 3 * (P + steps), seed=81).reshape(3, P + steps)
+    d1 = E.Decoder(k, batch=1, ctx_max=ctx)
+    d3 = E.Decoder(k, batch=3, ctx_max=ctx)
+    orc = O.DecodeOracle(oracle_cfg(cfg), oracle_weights(w), ctx_max=P + steps)
+    g1, _ = d1.prefill(tok[0, :P])
+    g3, _ = d3.prefill(tok[:, :P])
+    r1 = orc.prefill(tok[0, :P])
+    assert np.abs(g1[0] - r1).max() < LOGIT_ATOL
+    for i in range(steps):
+        g1, n1 = d1.step([tok[0, P + i]])
+        g3, n3 = d3.step(tok[:, P + i])
+        r1 = orc.step(int(tok[0, P + i]))
+        err = np.abs(g1[0] - r1).max()
+        print(f"step {i} (position {P + i}): max|dlogit| vs oracle {err:.2e}, batch-3 row 0 vs batch 1 "
+              f"{np.abs(g3[0] - g1[0]).max():.2e}", flush=True)
+        assert err < LOGIT_ATOL
+        assert np.abs(g3[0] - g1[0]).max() < 2e-3
+        assert int(n1[0]) == int(g1[0].argmax())
+    assert d1.length() == P + steps and d3.length() == P + steps
+
+
 def test_decode_equals_prefill_rows_on_gpu(m48):
     """Decode logits at position p equal row p of the device's own full forward."""
     cfg, w, k = m48
