@@ -446,10 +446,10 @@ hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C
 
 // ---- greedy token: reduce the argmax partials, advance the decode state ----
 // One workgroup per call (4 waves for B <= 4, else 16), NW / B waves (at
-// least one) per sequence, all sequences at once: each wave folds a strided share of its
-// sequence's partials (8 loads in flight per batch), then the sequence's
-// waves reduce through LDS, with the same rules as argmax_partial (the
-// result is the first index of the maximum whatever the folding order). With
+// least one) per sequence, all sequences at once: each wave folds a strided
+// share of its sequence's partials (8 loads in flight per batch), then the
+// sequence's waves reduce through LDS, with the same rules as argmax_partial
+// (the result is the first index of the maximum whatever the folding order). With
 // tok/d_pos set it also does the decode-step bookkeeping: the token becomes
 // the next step's input, is appended to the history at row (pos - pos0), and
 // the position advances.
