@@ -125,8 +125,14 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
 
   const int r0 = tid >> 3, c0 = tid & 7;
   const int ldst = r0 * 8 + (c0 ^ lds_swz(r0));
-  const f16* wb = W + c0 * 8;
-  const f16* xb = X + c0 * 8;
+  // Operand tiles are read through raw buffer descriptors with the sc1 (device
+  // scope) policy: the loads skip L1 allocation for data this workgroup never
+  // re-reads. 7B forward: B = 1 9.49-9.52 -> 9.42 ms, B = 8 56.3 -> 55.9 ms
+  // against plain global loads, bit-identical. Byte offsets are 32-bit: the
+  // launchers keep N*K and T*K below 2^31 elements.
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, -1, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, -1, 0x00020000);
+  constexpr int kSC1 = 16;  // cache policy: sc1
   int woff[WL], xoff[XL];
 #pragma unroll
   for (int i = 0; i < WL; ++i) woff[i] = min(f_base + r0 + RSTEP * i, N - 1) * kw;
@@ -140,9 +146,13 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
     constexpr int R = decltype(rs)::value;
     const int kw0 = k0 < kw ? k0 : k0 - kw;  // wave-uniform
 #pragma unroll
-    for (int i = 0; i < WL; ++i) wreg[R][i] = *(const f16x8*)(wb + woff[i] + kw0);
+    for (int i = 0; i < WL; ++i)
+      wreg[R][i] = __builtin_bit_cast(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(wrs, (uint32_t)(c0 * 8 + woff[i] + kw0) * 2u, 0, kSC1));
 #pragma unroll
-    for (int i = 0; i < XL; ++i) xreg[R][i] = *(const f16x8*)(xb + xoff[i] + k0);
+    for (int i = 0; i < XL; ++i)
+      xreg[R][i] = __builtin_bit_cast(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)(c0 * 8 + xoff[i] + k0) * 2u, 0, kSC1));
   };
   auto sstore = [&](auto rs) {
     constexpr int R = decltype(rs)::value;
