@@ -288,10 +288,10 @@ def main():
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs of
 # `bench.py --kernel-only` (FETCH_SIZE, then WRITE_SIZE), each scaled by the
 # counter's reading for the 1 GiB reference copy in the same run (FETCH_SIZE
-# reads 0.5x the copied bytes, WRITE_SIZE 1.0x): 2 * 106938 KiB + 14129 KiB.
+# reads 0.5x the copied bytes, WRITE_SIZE 1.0x): 2 * 106973 KiB + 14132.7 KiB.
 # Algorithmic bytes of one launch: W1|W3 180.4 MB + X 4.2 MB read, gate 11.3 MB
 # written = 195.8 MB.
-DOMINANT_TRAFFIC_BYTES = 233_477_120
+DOMINANT_TRAFFIC_BYTES = 233_552_589
 
 
 def time_dominant_kernel(k, cfg, T, launches, stream):
