@@ -65,9 +65,10 @@ struct EpiSumSq<E, std::void_t<decltype(E::kSumSq)>> : std::bool_constant<E::kSu
 // fixes the order: LDS reads of k-step 0 first, then every MFMA is followed by
 // one LDS read of the next k-step (k-steps 0..2), and the global loads are
 // spread one per MFMA over k-steps 0..2 while the LDS writes are spread over
-// k-steps WSTEP..3 (WSTEP = 1; 2 on 192x256 tiles, whose 7B FFN-up GEMM at 512
-// tokens runs 89.5 -> 86.6 us with the later start while the other tiles gain
-// nothing or lose up to 4%). Issuing the loads or the writes as a burst stalls the
+// k-steps WSTEP..3 (WSTEP = 2: with the operands read through buffer loads the
+// later start gives the loads of every tile shape another k-step to land, 7B
+// forward B = 1 9.49-9.53 -> 9.37-9.38 ms, seq 2048 31.4 -> 31.0 ms; WSTEP = 3
+// is slower at 4096 tokens). Issuing the loads or the writes as a burst stalls the
 // wave's in-order issue behind the memory queues and leaves the MFMA pipe idle
 // (one wave per SIMD has nothing else to issue).
 // Past the last slice the loads re-read the last slice (clamped), so every
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
     mfmas(F1);
     sstore(std::integral_constant<int, R ^ 1>{});
     // MFMA slot s = 0..4*NMF-1 in issue order
-    constexpr int WSTEP = (FT == 192 && TT == 256) ? 2 : 1;
+    constexpr int WSTEP = 2;
     constexpr int NSLOT = 4 * NMF, GSLOTS = 3 * NMF, WSLOTS = (4 - WSTEP) * NMF;
     __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // DS read, k-step 0
 #pragma unroll
