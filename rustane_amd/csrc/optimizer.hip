@@ -49,8 +49,13 @@ __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, const
                                                     const float* __restrict__ d_gscale) {
   const float gs = d_gscale ? *d_gscale : h.gscale;
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-    const f32x4 pv = ((const f32x4*)p)[i], gv = ((const f32x4*)g)[i];
-    const f32x4 mv = ((const f32x4*)m)[i], vv = ((const f32x4*)v)[i];
+    // non-temporal loads: every operand is read once (7B step 34.5-35.0 ->
+    // 34.0-34.1 ms); the stores stay ordinary (non-temporal stores measured
+    // far slower for write streams)
+    const f32x4 pv = __builtin_nontemporal_load(((const f32x4*)p) + i);
+    const f32x4 gv = __builtin_nontemporal_load(((const f32x4*)g) + i);
+    const f32x4 mv = __builtin_nontemporal_load(((const f32x4*)m) + i);
+    const f32x4 vv = __builtin_nontemporal_load(((const f32x4*)v) + i);
     f32x4 po, mo, vo;
     adamw4(pv, gv, mv, vv, gs, h, po, mo, vo);
     ((f32x4*)p)[i] = po;
@@ -110,8 +115,10 @@ __global__ __launch_bounds__(256) void adamw_tile_kernel(float* __restrict__ p,
     f16x4 o = {};
     if (r < R && c < C) {
       const size_t idx = (size_t)r * C + c;
-      const f32x4 pv = *(const f32x4*)(p + idx), gv = *(const f32x4*)(g + idx);
-      const f32x4 mv = *(const f32x4*)(m + idx), vv = *(const f32x4*)(v + idx);
+      const f32x4 pv = __builtin_nontemporal_load((const f32x4*)(p + idx));  // as adamw_kernel
+      const f32x4 gv = __builtin_nontemporal_load((const f32x4*)(g + idx));
+      const f32x4 mv = __builtin_nontemporal_load((const f32x4*)(m + idx));
+      const f32x4 vv = __builtin_nontemporal_load((const f32x4*)(v + idx));
       f32x4 po, mo, vo;
       adamw4(pv, gv, mv, vv, gs, h, po, mo, vo);
       *(f32x4*)(p + idx) = po;
