@@ -405,7 +405,8 @@ int check_token_count(const hb_model_config& c, long B, long S) {
 // capture: prefill is never captured), empty when the shape does not split.
 int residual_scratch(hb_model* m, int N, int T, int K, GemmScratch& out, int wgs = 256) {
   out = GemmScratch{m->splitk, m->splitk_floats, wgs};
-  const int S = gemm_splits(N, T, K, wgs);
+  bool wide;
+  const int S = std::max(gemm_splits(N, T, K, wgs), gemm_norm_splits(N, T, K, wgs, &wide));
   if (S <= 1) return HB_OK;
   const size_t need = (size_t)S * T * N;
   if (need > m->splitk_floats) {

@@ -21,6 +21,9 @@ struct GemmBatch {
 // Number of K splits the residual GEMM uses for this shape when given scratch
 // (1 = none), aiming at wgs workgroups; it needs splits * T * N floats.
 int gemm_splits(int N, int T, int K, int wgs = 256);
+// The same for gemm_residual_norm, which may use 256x128 tiles (*wide) for
+// long reductions; it needs splits * T * N floats too.
+int gemm_norm_splits(int N, int T, int K, int wgs, bool* wide);
 hipError_t gemm_store(const f16* W, const f16* X, int N, int T, int K, float* C, hipStream_t st);
 // kw (the residual, SwiGLU and QKV projections): 0 for plain X rows of K
 // halves; for split X rows (common.hpp) K = 2 * kw with kw the weights' row
