@@ -145,7 +145,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
 // splitk_reduce applies the epilogue. Measured GEMM time at 512 tokens, 7B
 // shapes: Wo 25.5 us (128x128 x 2 splits) against 26.3 us (256x128 x 4) and
 // 32.6 us unsplit; W2 57.7 us (128x128 x 2) against 53.2 us (256x128 x 4) and
-// 79.5 us unsplit. Two splits halve the partial-sum traffic of the reduce.
+// 79.5 us unsplit. Two splits halve the partial-sum traffic of the reduce;
+// the long-K residual + norm projections (W2) still take 256x128 x 4
+// (gemm_norm_splits), where the GEMM's gain outweighs the larger reduce.
 // K from 1024 splits too (600M shape, Wo with K = 1536 at 512 tokens: 96
 // workgroups of 64x128 unsplit, 144 of 128x128 in 3 splits; the batch-1
 // forward 2.28 -> 2.16 ms).
