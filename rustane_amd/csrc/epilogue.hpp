@@ -68,12 +68,20 @@ struct EpiSwiGLU {
   float* tap;  // nullable [T, 2*hidden] = h1 | h3
   int hidden;
   bool split = false;
+  // Decode with 8..16 sequences: gate in the decode GEMV's B-fragment order
+  // (gemv.hip): element (t, u) at ((u/32)*64 + t + 16*((u%32)/8))*8 + u%8, so
+  // the W2 GEMV reads each k-step's operand as one contiguous 1 KB block.
+  bool frag = false;
   HB_DEV void operator()(int t, int f0, f32x4 v) const {
     const int u = f0 >> 1;
     const float g0 = silu_f(v.x) * v.z, g1 = silu_f(v.y) * v.w;
     f16x2 g;
     g.x = (f16)g0;
     g.y = (f16)g1;
+    if (frag) {
+      *(f16x2*)(gate + ((size_t)(u >> 5) * 64 + t + 16 * ((u & 31) >> 3)) * 8 + (u & 7)) = g;
+      return;
+    }
     f16* row = gate + (size_t)t * (split ? 2 * hidden : hidden) + u;
     *(f16x2*)row = g;
     if (split) {

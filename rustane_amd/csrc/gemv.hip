@@ -218,11 +218,14 @@ enum { PRO_NONE = 0, PRO_NORM = 1, PRO_ATTN = 2 };
 // SPLIT (PRO_NONE only): X rows are split rows [B][2K] (common.hpp); every
 // weight fragment meets the hi and the lo half of the B operand, two MFMAs
 // into the same accumulator, so the weight stream is read once.
-template <int KS, int U, class Epi, int PRO, bool SPLIT>
+// XFRAG (PRO_NONE only): X is in B-fragment order (EpiSwiGLU::frag): the
+// operand of k-step s is the 1 KB block X + s*512, lane l's 16 bytes at l*8.
+template <int KS, int U, class Epi, int PRO, bool SPLIT, bool XFRAG = false>
 __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__ Wt,
                                                        const f16* __restrict__ X, int N, int B,
                                                        int K, Epi epi, NormIn nin, AttnIn ain) {
   static_assert(!SPLIT || PRO == PRO_NONE, "split rows come from memory");
+  static_assert(!XFRAG || (PRO == PRO_NONE && !SPLIT), "fragment-order rows come from memory");
   extern __shared__ f16x8 s_dyn[];  // staged B-operand rows [B][xn_ld(K)]
   __shared__ f32x4 red[KS][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -237,6 +240,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
                                      : X + (size_t)(xok ? col : 0) * (SPLIT ? 2 * K : K) + kq;
   auto bop = [&](int s) -> f16x8 {
     const f16x8 zero8 = {};
+    if constexpr (XFRAG) return xok ? *(const f16x8*)(X + ((size_t)s * 64 + lane) * 8) : zero8;
     return xok ? *(const f16x8*)(xrow + (size_t)s * 32) : zero8;
   };
   auto bopl = [&](int s) -> f16x8 {  // low half of a split row
@@ -369,8 +373,16 @@ constexpr int GEMV_U = 4;   // 1 KB weight loads in flight per wave
 
 template <class Epi>
 hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, const AttnIn* ain, int N,
-                       int B, int K, const Epi& epi, hipStream_t st, bool split = false) {
+                       int B, int K, const Epi& epi, hipStream_t st, bool split = false,
+                       bool xfrag = false) {
   if (B < 1 || B > 16 || N % 16 || K % 32) return hipErrorInvalidValue;
+  if (xfrag) {  // X rows in B-fragment order: the plain one-row-block kernel
+    if (split || nin || ain) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE, false, true>), dim3(N / 16),
+                       dim3(GEMV_KS * 64), 0, st, (const f16x8*)Wt, X, N, B, K, epi, NormIn{},
+                       AttnIn{});
+    return hipGetLastError();
+  }
   if (split) {
     if (nin || ain) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE, true>), dim3(N / 16),
@@ -422,8 +434,8 @@ bool gemv_attn_fits(int B, int K, int nch) {
 }
 
 hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, int B, int K,
-                         const EpiResidual& e, hipStream_t st, bool split) {
-  return launch_gemv(Wt, X, nullptr, ain, N, B, K, e, st, split);
+                         const EpiResidual& e, hipStream_t st, bool split, bool xfrag) {
+  return launch_gemv(Wt, X, nullptr, ain, N, B, K, e, st, split, xfrag);
 }
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                        const EpiSwiGLU& e, hipStream_t st, bool split) {

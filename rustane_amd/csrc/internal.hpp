@@ -95,8 +95,9 @@ constexpr int GEMV_ATTN_MAXCH = 8;  // B * nch limit of the in-GEMV combine
 bool gemv_attn_fits(int B, int K, int nch);
 // split: X rows are split rows [B, 2K] (common.hpp), read from memory (no
 // prologue); the weights are still [N, K].
+// xfrag: X in B-fragment order (EpiSwiGLU::frag), no prologue.
 hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, int B, int K,
-                         const EpiResidual& e, hipStream_t st, bool split = false);
+                         const EpiResidual& e, hipStream_t st, bool split = false, bool xfrag = false);
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                        const EpiSwiGLU& e, hipStream_t st, bool split = false);
 hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
