@@ -477,6 +477,9 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(AttnDecode p) {
         f16* op = p.out + (size_t)b * 2 * p.H * HD + h * HD + e;
         op[0] = hi;
         op[(size_t)p.H * HD] = (f16)(o - (float)hi);
+      } else if (p.out_frag) {  // the Wo GEMV's B-fragment order over K = H*hd
+        const int k = h * HD + e;
+        p.out[((size_t)(k >> 5) * 64 + b + 16 * ((k & 31) >> 3)) * 8 + (k & 7)] = hi;
       } else {
         p.out[head * HD + e] = hi;
       }
@@ -562,6 +565,7 @@ hipError_t attention_decode(const AttnDecode& p, hipStream_t st) {
   const dim3 grid(ch.n, p.H, p.B);
   const bool split = p.q_lo != nullptr;
   if (split && (!p.k_lo || !p.v_lo)) return hipErrorInvalidValue;
+  if (p.out_frag && (ch.n != 1 || split || p.B > 16 || (p.H * p.hd) % 32)) return hipErrorInvalidValue;
   return ch.waves == 8 ? launch_decode<8>(p, grid, split, st) : launch_decode<16>(p, grid, split, st);
 }
 

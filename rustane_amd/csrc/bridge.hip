@@ -2271,11 +2271,14 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
     a.ctx_max = kv->ctx_cap; a.nch = kv->nch; a.scale = 1.0f / sqrtf((float)c.hd); a.part_o = kv->part_o;
     a.part_ml = kv->part_ml; a.out = kv->attn;
+    // 8+ sequences with one chunk: attention rows in Wo's B-fragment order
+    // (as the gate for W2 below)
+    a.out_frag = B >= 8 && kv->nch == 1 && c.q_dim % 32 == 0;
     HIP_TRY(attention_decode(a, st));
     if (kv->nch > 1 && !kv->attn_in_wo) HIP_TRY(attention_combine(a, st));
     const AttnIn ain{kv->part_o, kv->part_ml, kv->d_pos, c.heads, c.hd, kv->nch};
     HIP_TRY(gemv_residual(L.t_wo, kv->attn, kv->attn_in_wo ? &ain : nullptr, c.dim, B, c.q_dim,
-                          EpiResidual{kv->x, kv->x2, c.dim, alpha}, st));
+                          EpiResidual{kv->x, kv->x2, c.dim, alpha}, st, false, a.out_frag));
     HIP_TRY(prep_norm(kv->x2, L.g2, n2));
     // 8+ sequences: the gate goes to W2 in B-fragment order (one 1 KB
     // operand block per k-step instead of B row pieces; 7B B = 16 decode

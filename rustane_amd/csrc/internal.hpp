@@ -175,6 +175,10 @@ struct AttnDecode {
   // layouts, all set or all NULL; the attention rows are then split rows
   // [B][2*H*hd].
   const f16 *q_lo = nullptr, *k_lo = nullptr, *v_lo = nullptr;
+  // One chunk, no low parts: out in the decode GEMV's B-fragment order over
+  // K = H*hd (element (b, k) at ((k/32)*64 + b + 16*((k%32)/8))*8 + k%8, 16
+  // row slots) instead of rows.
+  bool out_frag = false;
 };
 // Chunks of the decode context for B sequences of H heads: n chunks per
 // (sequence, head), each attn_chunk_keys(pos, n) keys long at position pos,
