@@ -2244,9 +2244,13 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
   // fit in LDS (B <= 3 at dim 4096): five launches per layer. Otherwise a
   // separate rmsnorm launch writes xn before each of those GEMVs.
   const bool fused = gemv_norm_fits(B, c.dim);
+  // 8+ sequences: the separate norms write xn in the GEMVs' B-fragment order
+  // (as the gate and the attention rows), one 1 KB operand block per k-step
+  const bool xfrag = !fused && B >= 8 && c.dim % 32 == 0;
   auto prep_norm = [&](const float* x, const float* gamma, NormIn& n) -> hipError_t {
     n = NormIn{x, gamma, c.norm_eps};
-    return fused ? hipSuccess : rmsnorm(x, c.dim, gamma, B, c.dim, c.norm_eps, kv->xn, nullptr, st);
+    return fused ? hipSuccess
+                 : rmsnorm(x, c.dim, gamma, B, c.dim, c.norm_eps, kv->xn, nullptr, st, false, xfrag);
   };
   HIP_TRY(embedding(m->embed, kv->d_tok, B, c.dim, c.vocab, kv->x, m->ctx->d_err, st));
   for (int l = 0; l < c.nlayers; ++l) {
@@ -2265,7 +2269,8 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     e.k = t.k; e.k_bstride = t.k_bstride; e.k_hstride = t.k_hstride;
     e.v = t.v; e.v_bstride = t.v_bstride; e.v_hstride = t.v_hstride; e.vt = nullptr; e.vt_ld = 0;
     e.tap = nullptr;
-    HIP_TRY(gemv_qkv(L.t_wqkv, kv->xn, fused ? &n1 : nullptr, c.q_dim + 2 * c.kv_dim, B, c.dim, e, st));
+    HIP_TRY(gemv_qkv(L.t_wqkv, kv->xn, fused ? &n1 : nullptr, c.q_dim + 2 * c.kv_dim, B, c.dim, e, st,
+                     false, xfrag));
     AttnDecode a{};
     a.q = kv->qd; a.k = t.k; a.v = t.v; a.bstride = t.k_bstride; a.hstride = t.k_hstride;
     a.d_pos = kv->d_pos; a.B = B; a.H = c.heads; a.KVH = c.kv_heads; a.hd = c.hd;
@@ -2286,7 +2291,7 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
     const bool frag = B >= 8 && c.hidden % 32 == 0;
     EpiSwiGLU sg{kv->gate, nullptr, c.hidden};
     sg.frag = frag;
-    HIP_TRY(gemv_swiglu(L.t_w13, kv->xn, fused ? &n2 : nullptr, 2 * c.hidden, B, c.dim, sg, st));
+    HIP_TRY(gemv_swiglu(L.t_w13, kv->xn, fused ? &n2 : nullptr, 2 * c.hidden, B, c.dim, sg, st, false, xfrag));
     HIP_TRY(gemv_residual(L.t_w2, kv->gate, nullptr, c.dim, B, c.hidden,
                           EpiResidual{kv->x2, kv->x, c.dim, alpha}, st, false, frag));
   }
@@ -2299,7 +2304,7 @@ int enqueue_decode_step(hb_kv* kv, hipStream_t st) {
   } else {
     NormIn nf;
     HIP_TRY(prep_norm(kv->x, m->gamma_f, nf));
-    HIP_TRY(gemv_logits(m->t_embed, kv->xn, fused ? &nf : nullptr, c.vocab, B, c.dim, el, st));
+    HIP_TRY(gemv_logits(m->t_embed, kv->xn, fused ? &nf : nullptr, c.vocab, B, c.dim, el, st, false, xfrag));
   }
   HIP_TRY(argmax_reduce(kv->amax_val, kv->amax_idx, c.vocab / 16, B, kv->d_next, kv->d_tok,
                         kv->d_hist, kv->d_pos, kv->d_pos0, st));

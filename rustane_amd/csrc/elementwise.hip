@@ -72,7 +72,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
       o.y = v[i].y * r * g[i].y;
       o.z = v[i].z * r * g[i].z;
       o.w = v[i].w * r * g[i].w;
-      store_f16x4(orow + threadIdx.x * 4 + i * 1024, o, lo);
+      const int c = threadIdx.x * 4 + i * 1024;
+      if (split == 2)  // the decode GEMVs' B-fragment order (EpiSwiGLU::frag), t < 16
+        *(f16x4*)(out + ((size_t)(c >> 5) * 64 + t + 16 * ((c & 31) >> 3)) * 8 + (c & 7)) = f16x4_hi(o);
+      else
+        store_f16x4(orow + c, o, lo);
     }
   } else {
     for (int c = threadIdx.x * 4; c < dim; c += 1024) {
@@ -90,15 +94,19 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
       o.y = v.y * r * g.y;
       o.z = v.z * r * g.z;
       o.w = v.w * r * g.w;
-      store_f16x4(orow + c, o, lo);
+      if (split == 2)
+        *(f16x4*)(out + ((size_t)(c >> 5) * 64 + t + 16 * ((c & 31) >> 3)) * 8 + (c & 7)) = f16x4_hi(o);
+      else
+        store_f16x4(orow + c, o, lo);
     }
   }
 }
 
 hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
-                   f16* out, float* rms_inv, hipStream_t st, bool split) {
+                   f16* out, float* rms_inv, hipStream_t st, bool split, bool frag) {
   if (T <= 0) return hipSuccess;
-  const int sp = split ? 1 : 0;
+  if (frag && (split || T > 16 || dim % 32)) return hipErrorInvalidValue;
+  const int sp = frag ? 2 : split ? 1 : 0;
   switch (dim % 1024 == 0 ? dim / 1024 : 0) {
 #define HB_NORM(n)                                                                              \
   case n:                                                                                       \

@@ -311,7 +311,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(const f16x8* __restrict__
 // the B rows in registers (XS fragments, K <= 32 * XS * KS), so the rows are
 // read once per workgroup. Same per-block arithmetic as gemv_kernel (one
 // MFMA chain per wave over its K range, waves summed in order).
-template <int KS, int XS, int U, class Epi>
+template <int KS, int XS, int U, class Epi, bool XFRAG = false>
 __global__ __launch_bounds__(KS * 64) void gemv_xreg_kernel(const f16x8* __restrict__ Wt,
                                                             const f16* __restrict__ X, int N, int B,
                                                             int K, Epi epi) {
@@ -326,7 +326,13 @@ __global__ __launch_bounds__(KS * 64) void gemv_xreg_kernel(const f16x8* __restr
   f16x8 xr[XS];
 #pragma unroll
   for (int j = 0; j < XS; ++j) {
-    const f16x8 v = j < ns ? *(const f16x8*)(xrow + (size_t)j * 32) : zero8;
+    f16x8 v = zero8;
+    if (j < ns) {
+      if constexpr (XFRAG)  // B-fragment order: k-step s at X + s*512
+        v = *(const f16x8*)(X + ((size_t)(s_begin + j) * 64 + lane) * 8);
+      else
+        v = *(const f16x8*)(xrow + (size_t)j * 32);
+    }
     xr[j] = xok ? v : zero8;
   }
   const int nrb = N >> 4;
@@ -376,11 +382,17 @@ hipError_t launch_gemv(const f16* Wt, const f16* X, const NormIn* nin, const Att
                        int B, int K, const Epi& epi, hipStream_t st, bool split = false,
                        bool xfrag = false) {
   if (B < 1 || B > 16 || N % 16 || K % 32) return hipErrorInvalidValue;
-  if (xfrag) {  // X rows in B-fragment order: the plain one-row-block kernel
+  if (xfrag) {  // X in B-fragment order (no prologue)
     if (split || nin || ain) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE, false, true>), dim3(N / 16),
-                       dim3(GEMV_KS * 64), 0, st, (const f16x8*)Wt, X, N, B, K, epi, NormIn{},
-                       AttnIn{});
+    if (K <= 32 * GEMV_XS * GEMV_KS && N / 16 > GEMV_XREG_WGS) {
+      const int nrb = N / 16, per = (nrb + GEMV_XREG_WGS - 1) / GEMV_XREG_WGS;
+      hipLaunchKernelGGL((gemv_xreg_kernel<GEMV_KS, GEMV_XS, GEMV_XREG_U, Epi, true>), dim3((nrb + per - 1) / per),
+                         dim3(GEMV_KS * 64), 0, st, (const f16x8*)Wt, X, N, B, K, epi);
+    } else {
+      hipLaunchKernelGGL((gemv_kernel<GEMV_KS, GEMV_U, Epi, PRO_NONE, false, true>), dim3(N / 16),
+                         dim3(GEMV_KS * 64), 0, st, (const f16x8*)Wt, X, N, B, K, epi, NormIn{},
+                         AttnIn{});
+    }
     return hipGetLastError();
   }
   if (split) {
@@ -438,19 +450,19 @@ hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, 
   return launch_gemv(Wt, X, nullptr, ain, N, B, K, e, st, split, xfrag);
 }
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const EpiSwiGLU& e, hipStream_t st, bool split) {
-  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st, split);
+                       const EpiSwiGLU& e, hipStream_t st, bool split, bool xfrag) {
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st, split, xfrag);
 }
 hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const EpiLogits& e, hipStream_t st, bool split) {
-  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st, split);
+                       const EpiLogits& e, hipStream_t st, bool split, bool xfrag) {
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st, split, xfrag);
 }
 hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                    const EpiQKV& e, hipStream_t st, bool split) {
+                    const EpiQKV& e, hipStream_t st, bool split, bool xfrag) {
   if (e.S < 1 || e.hd < 1) return hipErrorInvalidValue;
   EpiQKV ep = e;
   ep.prepare();
-  return launch_gemv(Wt, X, nin, nullptr, N, B, K, ep, st, split);
+  return launch_gemv(Wt, X, nin, nullptr, N, B, K, ep, st, split, xfrag);
 }
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st) {
   return launch_gemv(Wt, X, nullptr, nullptr, N, B, K, EpiStore{C, N}, st);

@@ -99,11 +99,14 @@ bool gemv_attn_fits(int B, int K, int nch);
 hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, int B, int K,
                          const EpiResidual& e, hipStream_t st, bool split = false, bool xfrag = false);
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const EpiSwiGLU& e, hipStream_t st, bool split = false);
+                       const EpiSwiGLU& e, hipStream_t st, bool split = false,
+                       bool xfrag = false);
 hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                       const EpiLogits& e, hipStream_t st, bool split = false);
+                       const EpiLogits& e, hipStream_t st, bool split = false,
+                       bool xfrag = false);
 hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
-                    const EpiQKV& e, hipStream_t st, bool split = false);
+                    const EpiQKV& e, hipStream_t st, bool split = false,
+                       bool xfrag = false);
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st);
 // Greedy token from the logits GEMV's argmax partials ([B][nblk] each). With
 // tok != NULL it also feeds the token back (tok, hist row pos - *d_pos0) and
@@ -198,8 +201,10 @@ hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int voca
                      int* err, hipStream_t st);
 // Rows r < T of x at x + r*row_stride (floats), dim contiguous; out rows are
 // [T, dim], or split rows [T, 2*dim] (common.hpp).
+// frag: out in the decode GEMVs' B-fragment order over 16 row slots (T <= 16;
+// EpiSwiGLU::frag) instead of rows.
 hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
-                   f16* out, float* rms_inv, hipStream_t st, bool split = false);
+                   f16* out, float* rms_inv, hipStream_t st, bool split = false, bool frag = false);
 // Per-row cross-entropy (targets nullable) and argmax (nullable).
 hipError_t cross_entropy(const float* logits, const uint32_t* targets, int T, int vocab,
                          float* loss, uint32_t* argmax, int* err, hipStream_t st);
