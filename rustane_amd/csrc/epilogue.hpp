@@ -69,8 +69,7 @@ struct EpiSwiGLU {
   int hidden;
   bool split = false;
   // Decode with 8..16 sequences: gate in the decode GEMV's B-fragment order
-  // (gemv.hip): element (t, u) at ((u/32)*64 + t + 16*((u%32)/8))*8 + u%8, so
-  // the W2 GEMV reads each k-step's operand as one contiguous 1 KB block.
+  // (EpiSwiGLUFrag below); only gemv_swiglu reads this flag.
   bool frag = false;
   HB_DEV void operator()(int t, int f0, f32x4 v) const {
     const int u = f0 >> 1;
@@ -78,10 +77,6 @@ struct EpiSwiGLU {
     f16x2 g;
     g.x = (f16)g0;
     g.y = (f16)g1;
-    if (frag) {
-      *(f16x2*)(gate + ((size_t)(u >> 5) * 64 + t + 16 * ((u & 31) >> 3)) * 8 + (u & 7)) = g;
-      return;
-    }
     f16* row = gate + (size_t)t * (split ? 2 * hidden : hidden) + u;
     *(f16x2*)row = g;
     if (split) {
@@ -97,6 +92,21 @@ struct EpiSwiGLU {
       r[hidden + u] = v.z;
       r[hidden + u + 1] = v.w;
     }
+  }
+};
+
+// The SwiGLU gate of EpiSwiGLU in the decode GEMV's B-fragment order over 16
+// row slots: element (t, u) at ((u/32)*64 + t + 16*((u%32)/8))*8 + u%8, so
+// the W2 GEMV reads each k-step's operand as one contiguous 1 KB block. A
+// type of its own, so that the prefill GEMM's SwiGLU epilogue stays as it is.
+struct EpiSwiGLUFrag {
+  f16* gate;
+  HB_DEV void operator()(int t, int f0, f32x4 v) const {
+    const int u = f0 >> 1;
+    f16x2 g;
+    g.x = (f16)(silu_f(v.x) * v.z);
+    g.y = (f16)(silu_f(v.y) * v.w);
+    *(f16x2*)(gate + ((size_t)(u >> 5) * 64 + t + 16 * ((u & 31) >> 3)) * 8 + (u & 7)) = g;
   }
 };
 

@@ -451,6 +451,10 @@ hipError_t gemv_residual(const f16* Wt, const f16* X, const AttnIn* ain, int N, 
 }
 hipError_t gemv_swiglu(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                        const EpiSwiGLU& e, hipStream_t st, bool split, bool xfrag) {
+  if (e.frag) {
+    if (e.split || e.tap || B > 16 || e.hidden % 32) return hipErrorInvalidValue;
+    return launch_gemv(Wt, X, nin, nullptr, N, B, K, EpiSwiGLUFrag{e.gate}, st, split, xfrag);
+  }
   return launch_gemv(Wt, X, nin, nullptr, N, B, K, e, st, split, xfrag);
 }
 hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
