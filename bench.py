@@ -15,10 +15,17 @@ Also reported on the same line:
                 replayed from one HIP graph; tok/s and HBM GB/s;
   prefill_b8    the same forward at batch 8;
   prefill       every other prefill workload: 7B seq 2048 at batch 1 and 8,
-                600M-shape at batch 1 and 8, 5B-shape at batch 4 (seq 512);
-  cpu_baseline  the fp32 CPU oracle timed on this host's CPU share on bounded
-                samples: the 7B forward (headline), each prefill workload's
-                forward and the 7B batch-1 decode step.
+                48M (512d/1536h/8L, 8x64) at batch 1, 600M-shape at batch 1
+                and 8, 5B-shape at batch 4 (seq 512);
+  stages_b1     the headline forward's device time per stage (hb_forward_timed,
+                the reference's forward_timed split: QKV, attention, Wo,
+                residual + norm, FFN up, FFN down, ...), per layer;
+  cpu_baseline  the fp32 CPU oracle timed on this host's CPU share the way the
+                reference's forward probe times its forward (1 warmup, median
+                of 3): whole forwards up to 20 layers; the 5B and 7B shapes as
+                1- and 2-layer stacks (per-layer cost = their difference), so
+                the scaling to all layers is measured, not assumed; and the
+                7B decode step at batch 1 and 16.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -174,6 +181,11 @@ def main():
     roofline, _ = time_dominant_kernel(k, cfg, B * S, args.kernel_launches, stream)
 
     extra = {}
+    # ---- per-stage device time of the same forward (hb_forward_timed) ----
+    extra["stages_b1"] = bench_stages(k, cfg, d_tok, d_tgt, B, S)
+    up_in_fwd = extra["stages_b1"]["per_layer_us"]["ffn_up"]
+    roofline["us_per_launch_in_forward"] = round(up_in_fwd, 2)
+    roofline["frac_in_forward"] = round(roofline["flop_per_launch"] / (up_in_fwd * 1e-6) / MFMA_PEAK_F16, 4)
     # ---- batch 8 prefill ----
     if not args.no_b8 and B == 1:
         B8 = 8
@@ -236,6 +248,8 @@ def main():
             dec.kv.close()
         if not args.no_cpu_baseline:
             dec_res["cpu_baseline_b1"] = cpu_baseline_decode(cfg, args.decode_ctx)
+            if "b16" in dec_res:
+                dec_res["cpu_baseline_b16"] = cpu_baseline_decode(cfg, args.decode_ctx, batch=16, timed_seqs=2)
         extra["decode"] = dec_res
 
     # ---- validation loop (windows of a resident token stream) ----
@@ -330,9 +344,39 @@ def time_dominant_kernel(k, cfg, T, launches, stream):
         f"{achieved:.1f} TFLOP/s ({achieved/2500*100:.1f}% of dense fp16 peak)")
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": 2500.0, "unit": "TFLOP/s",
                 "frac": round(achieved / 2500.0, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
+                "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE of this kernel, scaled by a 1 GiB copy "
+                                  "(profiles/ffn_up_gemm_7b_b1_counters.md), not measured in this run",
                 "kernel": "gemm_nt_kernel<192,256,2,2,EpiSwiGLU> (FFN up, W1|W3 + SwiGLU)",
-                "flop_per_launch": up_flops, "us_per_launch": round(up_ms * 1e3, 2)}
+                "flop_per_launch": up_flops, "us_per_launch": round(up_ms * 1e3, 2),
+                "timing": "us_per_launch: launches back to back (HIP events around a graph of them); "
+                          "us_per_launch_in_forward: inside the forward, from hb_forward_timed"}
     return roofline, up_ms
+
+
+def bench_stages(k, cfg, d_tok, d_tgt, B, S, reps=3):
+    """hb_forward_timed on the headline forward (the reference's forward_timed,
+    layer.rs:821-1015, as device times): each stage's time per layer (layers
+    1..L-1; the two-term first layer alone), the median of `reps` timed
+    forwards."""
+    import torch
+    runs = []
+    for _ in range(reps + 1):
+        runs.append(k.model.forward_timed(d_tok.data_ptr(), d_tgt.data_ptr(), B, S))
+    torch.cuda.synchronize()
+    runs = runs[1:]
+    med = {n: float(np.median([r[n] for r in runs])) for n in runs[0]}
+    n = med["layers_summed"]
+    per = {"qkv": "sdpa_qkv_ms", "attention": "sdpa_attention_ms", "wo": "wo_ms",
+           "residual_rmsnorm2": "residual_rmsnorm2_ms", "ffn_up": "ffn_up_ms", "ffn_down": "ffn_down_ms",
+           "ffn_residual_norm": "ffn_residual_norm_ms"}
+    res = {"per_layer_us": {a: round(med[b] * 1e3 / n, 2) for a, b in per.items()},
+           "layer0_us": round(med["layer0_ms"] * 1e3, 1), "embedding_us": round(med["embedding_ms"] * 1e3, 1),
+           "logits_us": round(med["logits_ms"] * 1e3, 1), "cross_entropy_us": round(med["cross_entropy_ms"] * 1e3, 1),
+           "total_ms": round(med["total_ms"], 3), "layers_summed": int(n),
+           "note": "eager launches with an event after each stage (median of 3 forwards); the graph-replayed "
+                   "forward of the headline runs without those events"}
+    log(f"[bench] stages B={B}: {res}")
+    return res
 
 
 def bench_validate(k, cfg, stream, steps=32):
@@ -523,11 +567,13 @@ def _threads_limited():
     return threadpool_limits(limits=cpu_threads())
 
 
-def _oracle_layer(cfg):
+def _oracle_layer(cfg, layer=0):
+    """The seeded fp32 weights of one layer (hb_model_init_synthetic's tensor
+    ids 16*layer + 0..6), in the oracle's LayerW."""
     import oracle as O
     from rustane_amd import hip_bridge as hb
     d, q, kv, h = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden
-    n = lambda tid, cnt: hb.synth_normal(SEED, tid, cnt, STD)
+    n = lambda tid, cnt: hb.synth_normal(SEED, 16 * layer + tid, cnt, STD)
     return O.LayerW(wq=n(0, d * q), wk=n(1, d * kv), wv=n(2, d * kv), wo=n(3, q * d), w1=n(4, d * h),
                     w3=n(5, d * h), w2=n(6, d * h), gamma1=np.ones(d, np.float32),
                     gamma2=np.ones(d, np.float32))
@@ -536,57 +582,69 @@ def _oracle_layer(cfg):
 _CPU_SAMPLES = {}
 
 
-def cpu_forward_sample(cfg, B, S, full_below_layers=9):
-    """fp32 oracle forward of one sequence of S tokens on the host (the
-    reference has no batch dimension: B sequences take B times as long).
-    Models of up to `full_below_layers` layers run whole; deeper ones run one
-    layer plus the head (final norm, logits, CE) and are scaled to nlayers x
-    layer + head. Best of 2. Returns (seconds per B-sequence forward, note)."""
+def _median_of_3(fn):
+    """1 warmup + median of 3 timed calls, the reference's forward probe
+    (crates/engine/tests/bench_fwd_only_scale.rs:74-86)."""
+    fn()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[1]
+
+
+def cpu_forward_sample(cfg, B, S, whole_up_to_layers=20):
+    """fp32 oracle forward of one sequence of S tokens on the host (embedding ..
+    per-position CE), timed as the reference's forward probe times its forward:
+    1 warmup + median of 3. Models of up to `whole_up_to_layers` layers run
+    whole. Deeper ones run as a 1-layer and a 2-layer stack of the model's
+    own first layers: their difference is one layer, the rest the embedding
+    and head, and nlayers x layer + head is the forward. The reference has no
+    batch dimension: B sequences take B times one. Returns (seconds per
+    B-sequence forward, note)."""
     key = (cfg.dim, cfg.hidden, cfg.nlayers, cfg.heads, cfg.vocab, S)
     if key in _CPU_SAMPLES:
         t_seq, note = _CPU_SAMPLES[key]
         return B * t_seq, note
+    import dataclasses
+
     import oracle as O
     from rustane_amd import hip_bridge as hb
-    oc = O.Config.of(cfg)
     d = cfg.dim
-    lw = _oracle_layer(cfg)
     E = hb.synth_normal(SEED, hb.HB_SYNTH_EMBED_ID, cfg.vocab * d, STD)
     tok = hb.synth_tokens(42, 0, cfg.vocab, S + 1)
-    x0 = O.mtrans(O.embedding_forward(E, d, tok[:-1]), S, d)
-    rope = O.rope_table(S, cfg.hd)
-    whole = cfg.nlayers < full_below_layers
-    lt, ht = [], []
-    for _ in range(2):
-        t0 = time.perf_counter()
-        x = x0
-        for _l in range(cfg.nlayers if whole else 1):
-            x, _ = O.layer_forward(oc, lw, x, S, rope)
-        lt.append(time.perf_counter() - t0)
-        t0 = time.perf_counter()
-        xf, _ = O.rmsnorm_channel_first(x, np.ones(d, np.float32), d, S)
-        logits = O.sgemm_at(O.mtrans(xf, d, S), S, d, E, cfg.vocab, np.zeros(S * cfg.vocab, np.float32))
-        O.cross_entropy_batch(logits, tok[1:], cfg.vocab)
-        ht.append(time.perf_counter() - t0)
-    if whole:
-        t_seq = min(lt) + min(ht)
-        note = f"whole forward {t_seq:.2f} s"
+
+    def stack(L):
+        oc = dataclasses.replace(O.Config.of(cfg), nlayers=L, seq=max(S, 1))
+        w = O.ModelW(embed=E, layers=[_oracle_layer(cfg, l) for l in range(L)], gamma_final=np.ones(d, np.float32))
+        return lambda: O.model_forward(oc, w, tok[:-1], tok[1:])
+
+    if cfg.nlayers <= whole_up_to_layers:
+        t_seq = _median_of_3(stack(cfg.nlayers))
+        note = f"whole {cfg.nlayers}-layer forward {t_seq:.3f} s (1 warmup + median of 3)"
     else:
-        t_seq = cfg.nlayers * min(lt) + min(ht)
-        note = f"{cfg.nlayers} x {min(lt)*1e3:.0f} ms (1 layer timed) + {min(ht)*1e3:.0f} ms head = {t_seq:.2f} s"
+        t1, t2 = _median_of_3(stack(1)), _median_of_3(stack(2))
+        layer = t2 - t1
+        head = max(t1 - layer, 0.0)
+        t_seq = head + cfg.nlayers * layer
+        note = (f"1-layer forward {t1:.3f} s, 2-layer {t2:.3f} s (1 warmup + median of 3 each): "
+                f"{layer * 1e3:.0f} ms per layer + {head * 1e3:.0f} ms embedding/head, "
+                f"x{cfg.nlayers} layers = {t_seq:.2f} s")
     _CPU_SAMPLES[key] = (t_seq, note)
     return B * t_seq, note
 
 
 def cpu_baseline(cfg, S):
     """Headline CPU baseline: the fp32 oracle's 7B-shape forward at B=1 on this
-    host's CPU share (one layer + the head timed, scaled to 32 layers)."""
+    host's CPU share (cpu_forward_sample: 1- and 2-layer stacks, 1 warmup +
+    median of 3 each, scaled to 32 layers)."""
     ctx = _threads_limited()
     try:
         t, note = cpu_forward_sample(cfg, 1, S)
         res = {"value": round(S / t, 2), "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
                "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
-               "sample": f"fp32 numpy oracle, 7B-shape forward at B=1 S={S}: {note} (best of 2)"}
+               "sample": f"fp32 numpy oracle, 7B-shape forward at B=1 S={S}: {note}"}
         log(f"[bench] cpu baseline: {res}")
         return res
     finally:
@@ -594,11 +652,13 @@ def cpu_baseline(cfg, S):
             ctx.unregister()
 
 
-def cpu_baseline_decode(cfg, ctx_len=2048):
-    """fp32 oracle decode step (DecodeOracle.step) of the 7B shape at batch 1
-    and position ctx_len on the host: one step through a 1-layer and a
-    2-layer model with a filled K/V cache gives the per-layer and the head
-    cost; a 32-layer step is head + 32 x layer. Median of 3 steps each."""
+def cpu_baseline_decode(cfg, ctx_len=2048, batch=1, timed_seqs=1):
+    """fp32 oracle decode step (DecodeOracle.step) of the 7B shape at position
+    ctx_len on the host: one step through a 1-layer and a 2-layer model with a
+    filled K/V cache gives the per-layer and the head cost; a 32-layer step
+    is head + 32 x layer. Median of 3 steps each. The reference decodes one
+    sequence at a time (no batch dimension): a batch of B takes B sequence
+    steps, and timed_seqs of them (each its own cache) are timed."""
     import dataclasses
 
     import oracle as O
@@ -607,27 +667,34 @@ def cpu_baseline_decode(cfg, ctx_len=2048):
     try:
         lw = _oracle_layer(cfg)
         E = hb.synth_normal(SEED, hb.HB_SYNTH_EMBED_ID, cfg.vocab * cfg.dim, STD)
-        times = {}
-        for L in (1, 2):
-            oc = dataclasses.replace(O.Config.of(cfg), nlayers=L, seq=ctx_len + 8)
-            w = O.ModelW(embed=E, layers=[lw] * L, gamma_final=np.ones(cfg.dim, np.float32))
-            dec = O.DecodeOracle(oc, w, ctx_max=ctx_len + 8)
-            rng = np.random.default_rng(L)
-            dec.k[:] = rng.standard_normal(dec.k.shape, dtype=np.float32)
-            dec.v[:] = rng.standard_normal(dec.v.shape, dtype=np.float32)
-            dec.pos = ctx_len
-            ts = []
-            for i in range(3):
-                t0 = time.perf_counter()
-                dec.step(int(i))
-                ts.append(time.perf_counter() - t0)
-            times[L] = sorted(ts)[1]
-        layer = max(times[2] - times[1], 1e-6)
-        head = max(times[1] - layer, 0.0)
-        step = head + cfg.nlayers * layer
-        res = {"value": round(1.0 / step, 3), "unit": "tok/s", "ms_per_step": round(step * 1e3, 1),
+        steps = []
+        for sq in range(timed_seqs):
+            times = {}
+            for L in (1, 2):
+                oc = dataclasses.replace(O.Config.of(cfg), nlayers=L, seq=ctx_len + 8)
+                w = O.ModelW(embed=E, layers=[lw] * L, gamma_final=np.ones(cfg.dim, np.float32))
+                dec = O.DecodeOracle(oc, w, ctx_max=ctx_len + 8)
+                rng = np.random.default_rng(10 * sq + L)
+                dec.k[:] = rng.standard_normal(dec.k.shape, dtype=np.float32)
+                dec.v[:] = rng.standard_normal(dec.v.shape, dtype=np.float32)
+                dec.pos = ctx_len
+                ts = []
+                for i in range(3):
+                    t0 = time.perf_counter()
+                    dec.step(int(i + 7 * sq))
+                    ts.append(time.perf_counter() - t0)
+                times[L] = sorted(ts)[1]
+            layer = max(times[2] - times[1], 1e-6)
+            head = max(times[1] - layer, 0.0)
+            steps.append((head + cfg.nlayers * layer, layer, head))
+        seq_step = float(np.mean([t for t, _, _ in steps]))
+        layer, head = float(np.mean([l for _, l, _ in steps])), float(np.mean([h for _, _, h in steps]))
+        step = batch * seq_step
+        who = (f"B={batch}: {timed_seqs} of the {batch} sequences timed, each {seq_step * 1e3:.0f} ms; "
+               f"{batch} x one sequence per step" if batch > 1 else "B=1")
+        res = {"value": round(batch / step, 3), "unit": "tok/s", "ms_per_step": round(step * 1e3, 1),
                "cores": cpu_threads(), "kind": "port", "cpu_model": cpu_model(),
-               "sample": f"fp32 numpy DecodeOracle.step at position {ctx_len}, B=1: {cfg.nlayers} x "
+               "sample": f"fp32 numpy DecodeOracle.step at position {ctx_len}, {who}: {cfg.nlayers} x "
                          f"{layer*1e3:.1f} ms per layer + {head*1e3:.1f} ms embedding/head (median of 3 "
                          f"steps of 1- and 2-layer models with a filled K/V cache)"}
         log(f"[bench] cpu baseline (decode): {res}")
@@ -639,10 +706,11 @@ def cpu_baseline_decode(cfg, ctx_len=2048):
 
 def bench_prefill_configs(k7, cfg7, stream, cpu=True):
     """Prefill forwards (embedding .. per-position CE) of the other workloads:
-    7B-shape at seq 2048 (batch 1 and 8, on the headline model), 600M-shape
+    7B-shape at seq 2048 (batch 1 and 8, on the headline model), the 48M
+    workload (512d/1536h/8L, 8x64, vocab 32000) at batch 1, 600M-shape
     (1536d/4096h/20L, 12x128) at batch 1 and 8 and 5B-shape (2560d/6912h/60L,
-    20x128) at batch 4, both seq 512, each on seeded N(0, 0.02) device
-    weights; wall time over repeated hb_forward_device calls."""
+    20x128) at batch 4, all seq 512 but the first, each on seeded N(0, 0.02)
+    device weights; wall time over repeated hb_forward_device calls."""
     import torch
     from rustane_amd import hip_bridge as hb
     from rustane_amd.engine import CompiledKernels, ModelConfig
@@ -684,14 +752,15 @@ def bench_prefill_configs(k7, cfg7, stream, cpu=True):
     for B in (1, 8):
         out[f"7b_s2048_b{B}"] = run(k7, cfg7, B, 2048, 3 if B == 1 else 2)
         log(f"[bench] prefill 7B S=2048 B={B}: {out[f'7b_s2048_b{B}']}")
-    for name, mk, batches in (("600m", ModelConfig.llama_600m, (1, 8)), ("5b", ModelConfig.llama_5b, (4,))):
+    for name, mk, batches in (("48m", ModelConfig.llama_48m, (1,)), ("600m", ModelConfig.llama_600m, (1, 8)),
+                              ("5b", ModelConfig.llama_5b, (4,))):
         cfg = mk()
         k = CompiledKernels.compile(cfg)
         k.ctx.set_stream(stream.cuda_stream)
         try:
             k.init_synthetic(SEED, STD)
             for B in batches:
-                out[f"{name}_s512_b{B}"] = run(k, cfg, B, 512, 10 if B == 1 else 5)
+                out[f"{name}_s512_b{B}"] = run(k, cfg, B, 512, (40 if name == "48m" else 10) if B == 1 else 5)
                 log(f"[bench] prefill {name} S=512 B={B}: {out[f'{name}_s512_b{B}']}")
         finally:
             torch.cuda.synchronize()

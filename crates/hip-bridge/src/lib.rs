@@ -105,6 +105,27 @@ pub mod sys {
         pub grad_clip: f32,
     }
 
+    /// Per-stage device time of one forward (ForwardTimings, layer.rs:821-1015):
+    /// stage sums over layers 1..nlayers-1, the first layer in layer0_ms.
+    #[repr(C)]
+    #[derive(Debug, Clone, Copy, Default, PartialEq)]
+    pub struct hb_forward_timings {
+        pub embedding_ms: f32,
+        pub rmsnorm1_ms: f32,
+        pub sdpa_qkv_ms: f32,
+        pub sdpa_attention_ms: f32,
+        pub wo_ms: f32,
+        pub residual_rmsnorm2_ms: f32,
+        pub ffn_up_ms: f32,
+        pub ffn_down_ms: f32,
+        pub ffn_residual_norm_ms: f32,
+        pub logits_ms: f32,
+        pub cross_entropy_ms: f32,
+        pub layer0_ms: f32,
+        pub total_ms: f32,
+        pub layers_summed: i32,
+    }
+
     /// ForwardResult's host views (full_model.rs:73-81); each pointer nullable.
     #[repr(C)]
     #[derive(Debug, Clone, Copy)]
@@ -195,6 +216,16 @@ pub mod sys {
             d_mean_loss: *mut f32,
         ) -> c_int;
         pub fn hb_model_reserve(model: *mut hb_model, b: c_int, s: c_int) -> c_int;
+        pub fn hb_forward_timed(
+            model: *mut hb_model,
+            d_tokens: *const u32,
+            d_targets: *const u32,
+            b: c_int,
+            s: c_int,
+            d_per_pos_loss: *mut f32,
+            d_mean_loss: *mut f32,
+            out: *mut hb_forward_timings,
+        ) -> c_int;
 
         // per-kernel entry points (device buffers)
         pub fn hb_op_rmsnorm(

@@ -199,6 +199,49 @@ int hb_forward_device(hb_model* model, const uint32_t* d_tokens, const uint32_t*
  * so that later calls of that size allocate nothing. */
 int hb_model_reserve(hb_model* model, int B, int S);
 
+/*
+ * Device time of each stage of one forward. Replaces ForwardTimings /
+ * forward_timed (layer.rs:821-1015), which time one layer's CPU norms, the
+ * staging of each ANE input, the three ANE graphs and the readbacks; here the
+ * inputs stay on the device (no staging or readback stage) and each stage is
+ * the kernels between two HIP events on the stream:
+ *   rmsnorm1_ms           the separate input norms (layer 0's; later layers'
+ *                         come out of the previous W2 reduction, below)
+ *   sdpa_qkv_ms           Q/K/V projection + RoPE + K/V^T scatter   (sdpaFwd)
+ *   sdpa_attention_ms     causal attention                          (sdpaFwd)
+ *   wo_ms                 Wo projection (split-K partial sums)      (woFwd)
+ *   residual_rmsnorm2_ms  split-K reduction + residual + RMSNorm2
+ *   ffn_up_ms             W1|W3 projection + SwiGLU                 (ffnFused)
+ *   ffn_down_ms           W2 projection (split-K partial sums)      (ffnFused)
+ *   ffn_residual_norm_ms  its reduction + residual + the next layer's norm
+ * The per-layer stages are summed over layers 1 .. nlayers-1
+ * (layers_summed of them); the first layer, on two-term operands by default
+ * (hb_model_set_precise_layers), is layer0_ms. total_ms spans the whole
+ * forward, embedding to mean loss. The events add a little time of their
+ * own between launches.
+ */
+typedef struct hb_forward_timings {
+  float embedding_ms;
+  float rmsnorm1_ms;
+  float sdpa_qkv_ms;
+  float sdpa_attention_ms;
+  float wo_ms;
+  float residual_rmsnorm2_ms;
+  float ffn_up_ms;
+  float ffn_down_ms;
+  float ffn_residual_norm_ms;
+  float logits_ms;
+  float cross_entropy_ms;
+  float layer0_ms;
+  float total_ms;
+  int32_t layers_summed;
+} hb_forward_timings;
+/* hb_forward_device's launches run eagerly with an event after each stage;
+ * synchronous. Losses and mean (nullable device buffers) equal
+ * hb_forward_device's bit for bit. */
+int hb_forward_timed(hb_model* model, const uint32_t* d_tokens, const uint32_t* d_targets, int B, int S,
+                     float* d_per_pos_loss, float* d_mean_loss, hb_forward_timings* out);
+
 /* ---- per-kernel entry points (device buffers, async) -----------------------
  * The reference runs each layer as CPU RMSNorm -> sdpaFwd -> woFwd -> CPU
  * residual + RMSNorm -> ffnFused (layer.rs:684-806). These expose the same
@@ -227,8 +270,11 @@ int hb_op_wo_fwd(hb_model* model, int layer, const void* d_attn_f16, const float
  * capture, tight serving loops, harnesses that forbid hipMalloc). The split-K
  * partial sums live in a fixed 16 MiB device array inside the library (one per
  * GPU, held until the process ends), which covers every shape; results equal
- * hb_op_wo_fwd's bit for bit. Calls that overlap on one GPU share that array
- * and race: keep them ordered on one stream. */
+ * hb_op_wo_fwd's bit for bit. Calls on one GPU share that array: outside a
+ * graph capture each call waits (on its stream) for the previous call's use
+ * of it, so calls from different streams or contexts run one after another;
+ * under capture no such wait is recorded, and graph replays that overlap on
+ * one GPU race -- keep them ordered on one stream. */
 int hb_op_wo_fwd_noalloc(hb_model* model, int layer, const void* d_attn_f16, const float* d_x, int T,
                          float* d_x2);
 /*
@@ -434,9 +480,11 @@ int hb_train_forward(hb_model* m, const uint32_t* h_tokens, const uint32_t* h_ta
                      float* h_per_pos_loss, float* h_mean_loss, const hb_forward_result* out);
 /* backward (full_model.rs:414-483) from the caches of the last
  * hb_train_forward: ADDS the gradients of loss_scale * (mean CE of each
- * sequence) to opt's gradient arena, as hb_forward_backward does.
- * HB_E_STATE without a kept forward (each forward serves one backward).
- * Synchronous. */
+ * sequence) to opt's gradient arena, as hb_forward_backward does. The
+ * softcap is the one the kept forward ran with (the reference passes the
+ * forward's softcap again), even if hb_model_set_softcap or an inference
+ * forward changed the model's since. HB_E_STATE without a kept forward
+ * (each forward serves one backward). Synchronous. */
 int hb_train_backward(hb_model* m, hb_opt* opt, float loss_scale);
 
 /* ---- RSTK checkpoints (bin/train.rs:165-202) ------------------------------ */

@@ -197,6 +197,10 @@ struct TrainState {
   // hb_train_forward left its activations for hb_train_backward (the
   // reference's ForwardResult.caches); any other training call clears it.
   bool kept = false;
+  // The softcap the kept logits were computed with: the backward's
+  // derivative must use it even if hb_model_set_softcap (or an inference
+  // forward with another softcap) ran in between.
+  float softcap = 0.f;
   // device staging of ForwardResult's host views, grown on demand
   float* views = nullptr;
   size_t views_floats = 0;
@@ -321,10 +325,18 @@ int ensure_staging(hb_model* m, size_t floats) {
   return HB_OK;
 }
 
+// True while the context's current stream is being captured into a graph:
+// nothing may allocate, free or synchronise then.
+bool capturing(hb_model* m) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(m->ctx->stream(), &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
 int ensure_workspace(hb_model* m, long T, long Tpad, bool need_split = false) {
   Workspace& w = m->ws;
   const bool split = need_split || m->precise_layers > 0 || w.split;
   if (T <= w.cap_T && Tpad <= w.cap_Tpad && w.split == split) return HB_OK;
+  if (capturing(m)) return fail(HB_E_STATE, "the workspace must grow to %ld tokens while the stream is captured", T);
   T = std::max(T, w.cap_T);
   Tpad = std::max(Tpad, w.cap_Tpad);
   const hb_model_config& c = m->cfg;
@@ -401,8 +413,10 @@ int check_token_count(const hb_model_config& c, long B, long S) {
   return HB_OK;
 }
 
-// Scratch for a residual GEMM of this shape: grown on demand (outside any
-// capture: prefill is never captured), empty when the shape does not split.
+// Scratch for a residual GEMM of this shape: grown on demand, empty when the
+// shape does not split. A captured forward (forward_device_impl) reserves it
+// before the capture starts; growing it during a capture is refused
+// (HB_E_STATE), since it would allocate and synchronise inside the graph.
 int residual_scratch(hb_model* m, int N, int T, int K, GemmScratch& out, int wgs = 256) {
   out = GemmScratch{m->splitk, m->splitk_floats, wgs};
   bool wide;
@@ -410,6 +424,8 @@ int residual_scratch(hb_model* m, int N, int T, int K, GemmScratch& out, int wgs
   if (S <= 1) return HB_OK;
   const size_t need = (size_t)S * T * N;
   if (need > m->splitk_floats) {
+    if (capturing(m))
+      return fail(HB_E_STATE, "split-K scratch must grow to %zu floats while the stream is captured", need);
     HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
     if (m->splitk) HIP_TRY(hipFree(m->splitk));
     m->splitk = nullptr;
@@ -495,8 +511,40 @@ int zero_vt_pad(hb_model* m, f16* vt, int B, int S, hipStream_t st);
 // xn, attn, x2n and gate (GEMM K doubled, weights read once per half), Q, K,
 // V with low parts, split attention; the norm that feeds layer l is written
 // split when l < np. kv.k_lo / kv.v_lo must be set for those layers.
+// Stage boundaries of a timed forward (hb_forward_timed): an event is
+// recorded on the stream after each stage's launches, and the time between
+// consecutive events is added to that stage. Null in every other forward.
+enum Stage {
+  ST_EMBED, ST_NORM1, ST_QKV, ST_ATTN, ST_WO, ST_WO_NORM, ST_FFN_UP, ST_FFN_DOWN, ST_FFN_NORM,
+  ST_LOGITS, ST_CE, ST_COUNT
+};
+struct StageTimer {
+  hipStream_t st;
+  std::vector<hipEvent_t> ev;
+  std::vector<std::pair<int, int>> tag;  // (stage, layer) that ends at ev[i]
+  int layer = -1;
+  hipEvent_t next(int stage) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    ev.push_back(e);
+    tag.emplace_back(stage, layer);
+    return e;
+  }
+  hipError_t mark(int stage) {
+    hipEvent_t e = next(stage);
+    return e ? hipEventRecord(e, st) : hipErrorOutOfMemory;
+  }
+  ~StageTimer() {
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+  }
+};
+#define HB_MARK(tm, stage) \
+  do {                     \
+    if (tm) HIP_TRY((tm)->mark(stage)); \
+  } while (0)
+
 int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_tap, bool xn_ready,
-              const float* next_gamma, int np) {
+              const float* next_gamma, int np, StageTimer* tm = nullptr) {
   const hb_model_config& c = m->cfg;
   Workspace& w = m->ws;
   const LayerW& L = m->layers[l];
@@ -509,7 +557,11 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
     return fail(HB_E_STATE, "split-operand buffers missing");
   const int f = sp ? 2 : 1;  // K multiplier of this layer's products
 
-  if (!xn_ready) HIP_TRY(rmsnorm(w.x, c.dim, L.g1, T, c.dim, c.norm_eps, w.xn, nullptr, st, sp));
+  if (tm) tm->layer = l;
+  if (!xn_ready) {
+    HIP_TRY(rmsnorm(w.x, c.dim, L.g1, T, c.dim, c.norm_eps, w.xn, nullptr, st, sp));
+    HB_MARK(tm, ST_NORM1);
+  }
   EpiQKV e{};
   e.q_dim = c.q_dim;
   e.kv_dim = c.kv_dim;
@@ -540,6 +592,7 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
   HIP_TRY(gemm_qkv(L.wqkv, w.xn, c.q_dim + 2 * c.kv_dim, T, f * c.dim, e, st, c.dim));
   TRY(zero_vt_pad(m, w.vt, B, S, st));
   if (sp) TRY(zero_vt_pad(m, w.vt_lo, B, S, st));
+  HB_MARK(tm, ST_QKV);
   AttnPrefill a{};
   a.q = w.q;
   a.q_rows = Sp;
@@ -561,19 +614,27 @@ int run_layer(hb_model* m, int l, int B, int S, const KVTarget& kv, float* qkv_t
     a.vt_lo = w.vt_lo;
   }
   HIP_TRY(attention_prefill(a, st));
+  HB_MARK(tm, ST_ATTN);
   GemmScratch so, s2;
   TRY(residual_scratch(m, c.dim, T, f * c.q_dim, so));
   HIP_TRY(gemm_residual_norm(L.wo, w.attn, c.dim, T, f * c.q_dim, EpiResidual{w.x, w.x2, c.dim, alpha},
-                             NormOut{L.g2, c.norm_eps, w.xn, sp}, &so, st, c.q_dim));
+                             NormOut{L.g2, c.norm_eps, w.xn, sp}, &so, st, c.q_dim,
+                             tm ? tm->next(ST_WO) : nullptr));
+  HB_MARK(tm, ST_WO_NORM);
   HIP_TRY(gemm_swiglu(L.w13, w.xn, 2 * c.hidden, T, f * c.dim, EpiSwiGLU{w.gate, nullptr, c.hidden, sp}, st,
                       c.dim));
+  HB_MARK(tm, ST_FFN_UP);
   TRY(residual_scratch(m, c.dim, T, f * c.hidden, s2));
   const EpiResidual e2{w.x2, w.x, c.dim, alpha};
-  if (next_gamma)
+  if (next_gamma) {
     HIP_TRY(gemm_residual_norm(L.w2, w.gate, c.dim, T, f * c.hidden, e2,
-                               NormOut{next_gamma, c.norm_eps, w.xn, sp_next}, &s2, st, c.hidden));
-  else
+                               NormOut{next_gamma, c.norm_eps, w.xn, sp_next}, &s2, st, c.hidden,
+                               tm ? tm->next(ST_FFN_DOWN) : nullptr));
+    HB_MARK(tm, ST_FFN_NORM);
+  } else {
     HIP_TRY(gemm_residual(L.w2, w.gate, c.dim, T, f * c.hidden, e2, &s2, st, c.hidden));
+    HB_MARK(tm, ST_FFN_DOWN);
+  }
   return HB_OK;
 }
 
@@ -644,6 +705,11 @@ static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_FLOATS];
 // uses these addresses, never the array's name (a host-side stand-in).
 constexpr int NOALLOC_MAX_DEVICES = 64;
 static float* g_scratch_dev[NOALLOC_MAX_DEVICES];
+// Last use of each device's array: calls outside a graph capture wait for it
+// on their own stream and record it afterwards, so two calls from different
+// streams (contexts, hb_ctx_set_stream) run one after the other instead of
+// sharing the partial sums.
+static hipEvent_t g_scratch_ev[NOALLOC_MAX_DEVICES];
 static std::mutex g_scratch_mu;
 
 static int scratch_setup(int device) {
@@ -651,8 +717,10 @@ static int scratch_setup(int device) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (g_scratch_dev[device]) return HB_OK;
   void* p = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !p) return fail(HB_E_DEVICE, "scratch address on device %d: %s", device, hipGetErrorString(e));
+  if (!g_scratch_ev[device]) e = hipEventCreateWithFlags(&g_scratch_ev[device], hipEventDisableTiming);
+  if (e != hipSuccess) return fail(HB_E_DEVICE, "scratch event on device %d: %s", device, hipGetErrorString(e));
   g_scratch_dev[device] = (float*)p;
   return HB_OK;
 }
@@ -1880,7 +1948,21 @@ extern "C" int hb_model_reserve(hb_model* m, int B, int S) {
 }
 
 static int forward_enqueue(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets, int B, int S,
-                           float* d_loss, float* d_logits, float* d_mean);
+                           float* d_loss, float* d_logits, float* d_mean, StageTimer* tm = nullptr);
+
+// Allocates what forward_enqueue of (B, S) uses -- the workspace and the
+// split-K scratch of the residual projections, for plain and two-term
+// layers -- so that a capture of it allocates nothing.
+static int forward_reserve(hb_model* m, int B, int S) {
+  const hb_model_config& c = m->cfg;
+  TRY(ensure_workspace(m, (long)B * S, (long)B * S_pad_of(S)));
+  GemmScratch g;
+  for (int f = 1; f <= (m->precise_layers > 0 ? 2 : 1); ++f) {
+    TRY(residual_scratch(m, c.dim, B * S, f * c.q_dim, g));
+    TRY(residual_scratch(m, c.dim, B * S, f * c.hidden, g));
+  }
+  return HB_OK;
+}
 
 // HB_NO_GRAPH=1 runs the forward and decode launches eagerly (for profiling
 // individual launches).
@@ -1926,6 +2008,12 @@ static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint
   m->fwd_exec = nullptr;
   m->fwd_graph = nullptr;
   m->fwd_key = hb_model::FwdKey{};
+  // everything the launches need is allocated before the capture starts
+  TRY(forward_reserve(m, B, S));
+  if (!(key() == k)) {  // the reservation moved the split-K scratch: capture on the next call
+    m->fwd_seen = key();
+    return forward_enqueue(m, d_tokens, d_targets, B, S, d_loss, d_logits, d_mean);
+  }
   // the capture stream starts after the work already queued on the context stream
   HIP_TRY(hipStreamSynchronize(ctx->stream()));
   hipStream_t saved = ctx->user;
@@ -1948,27 +2036,79 @@ static int forward_device_impl(hb_model* m, const uint32_t* d_tokens, const uint
 }
 
 static int forward_enqueue(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets, int B, int S,
-                           float* d_loss, float* d_logits, float* d_mean) {
+                           float* d_loss, float* d_logits, float* d_mean, StageTimer* tm) {
   const hb_model_config& c = m->cfg;
   const long T = (long)B * S;
   Workspace& w = m->ws;
   hipStream_t st = m->ctx->stream();
   HIP_TRY(embedding(m->embed, d_tokens, (int)T, c.dim, c.vocab, w.x, m->ctx->d_err, st));
+  HB_MARK(tm, ST_EMBED);
   const KVTarget kv = scratch_kv(m, B, S);
   // Each layer leaves the next norm (the final one after the last layer) in xn.
   for (int l = 0; l < c.nlayers; ++l)
     TRY(run_layer(m, l, B, S, kv, nullptr, l > 0,
-                  l + 1 < c.nlayers ? m->layers[l + 1].g1 : m->gamma_f, m->precise_layers));
+                  l + 1 < c.nlayers ? m->layers[l + 1].g1 : m->gamma_f, m->precise_layers, tm));
+  if (tm) tm->layer = -1;
   float* logits = d_logits ? d_logits : w.logits;
   const int fl = m->precise_layers == c.nlayers ? 2 : 1;  // split final rows (run_layer)
   HIP_TRY(gemm_logits(m->embed, w.xn, c.vocab, (int)T, fl * c.dim, EpiLogits{logits, c.vocab, c.softcap}, st,
                       c.dim));
+  HB_MARK(tm, ST_LOGITS);
   if (d_targets) {
     float* loss = d_loss ? d_loss : w.loss;
     HIP_TRY(cross_entropy(logits, d_targets, (int)T, c.vocab, loss, nullptr, m->ctx->d_err, st));
     if (d_mean) HIP_TRY(mean_reduce(loss, (int)T, d_mean, st));
+    HB_MARK(tm, ST_CE);
   }
   return HB_OK;
+}
+
+// forward_timed (layer.rs:821-1015) on the device: the launches of
+// hb_forward_device, eager, with an event after each stage.
+extern "C" int hb_forward_timed(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets, int B,
+                                int S, float* d_loss, float* d_mean, hb_forward_timings* out) {
+  HB_INJECT_CHECK();
+  if (!m || !out) return fail(HB_E_INVALID, "null argument");
+  const hb_model_config& c = m->cfg;
+  if (B <= 0 || S <= 0 || S > c.seq) return fail(HB_E_INVALID, "need B >= 1 and 1 <= S <= seq (%d)", c.seq);
+  TRY(check_token_count(c, B, S));
+  if (!weights_ready(m)) return fail(HB_E_STATE, "weights not uploaded");
+  if (!d_tokens) return fail(HB_E_INVALID, "null tokens");
+  DeviceGuard g(m->ctx->device);
+  TRY(forward_reserve(m, B, S));
+  hipStream_t st = m->ctx->stream();
+  StageTimer tm{st};
+  TRY(tm.mark(-1) == hipSuccess ? HB_OK : fail(HB_E_DEVICE, "event record failed"));
+  TRY(forward_enqueue(m, d_tokens, d_targets, B, S, d_loss, nullptr, d_mean, &tm));
+  HIP_TRY(hipStreamSynchronize(st));
+  float stage[ST_COUNT] = {}, layer0 = 0.f;
+  for (size_t i = 1; i < tm.ev.size(); ++i) {
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, tm.ev[i - 1], tm.ev[i]));
+    const int s_ = tm.tag[i].first, l = tm.tag[i].second;
+    if (l == 0)
+      layer0 += ms;
+    else
+      stage[s_] += ms;
+  }
+  float total = 0.f;
+  HIP_TRY(hipEventElapsedTime(&total, tm.ev.front(), tm.ev.back()));
+  *out = hb_forward_timings{};
+  out->embedding_ms = stage[ST_EMBED];
+  out->rmsnorm1_ms = stage[ST_NORM1];
+  out->sdpa_qkv_ms = stage[ST_QKV];
+  out->sdpa_attention_ms = stage[ST_ATTN];
+  out->wo_ms = stage[ST_WO];
+  out->residual_rmsnorm2_ms = stage[ST_WO_NORM];
+  out->ffn_up_ms = stage[ST_FFN_UP];
+  out->ffn_down_ms = stage[ST_FFN_DOWN];
+  out->ffn_residual_norm_ms = stage[ST_FFN_NORM];
+  out->logits_ms = stage[ST_LOGITS];
+  out->cross_entropy_ms = stage[ST_CE];
+  out->layer0_ms = layer0;
+  out->total_ms = total;
+  out->layers_summed = c.nlayers - 1;
+  return check_err_word(m->ctx);
 }
 
 extern "C" int hb_forward_device(hb_model* m, const uint32_t* d_tokens, const uint32_t* d_targets,
@@ -2099,8 +2239,16 @@ extern "C" int hb_op_wo_fwd_noalloc(hb_model* m, int layer, const void* attn, co
   if (!sp) return fail(HB_E_STATE, "no-alloc scratch not set up on device %d", m->ctx->device);
   DeviceGuard g(m->ctx->device);
   const GemmScratch so{sp, NOALLOC_SCRATCH_FLOATS, 256};
+  hipStream_t st = m->ctx->stream();
+  // ordered after the previous use of the array unless the stream is being
+  // captured (a graph's replays are ordered by whoever launches them)
+  const bool cap = capturing(m);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  hipEvent_t ev = g_scratch_ev[m->ctx->device];
+  if (!cap) HIP_TRY(hipStreamWaitEvent(st, ev, 0));
   HIP_TRY(gemm_residual(m->layers[layer].wo, (const f16*)attn, c.dim, T, c.q_dim,
-                        EpiResidual{x, x2, c.dim, alpha_of(c)}, &so, m->ctx->stream()));
+                        EpiResidual{x, x2, c.dim, alpha_of(c)}, &so, st));
+  if (!cap) HIP_TRY(hipEventRecord(ev, st));
   return HB_OK;
 }
 
@@ -2397,9 +2545,12 @@ extern "C" int hb_kv_create(hb_model* m, int batch, int ctx_max, hb_kv** out) {
   const size_t o_po = take(B * c.heads * kv->nch * c.hd * 4), o_pml = take(B * c.heads * kv->nch * 8);
   const size_t o_aval = take(B * (c.vocab / 16) * 4), o_aidx = take(B * (c.vocab / 16) * 4);
   // xn, attn and gate hold split rows [B, 2K] in split layers
-  const size_t o_xn = take(2 * B * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(2 * B * c.q_dim * 2);
+  // xn and attn also hold B-fragment order (16 row slots of K halves) at 8+
+  // sequences, gate at any batch: each at least 16 rows
+  const size_t rows16 = std::max<size_t>(2 * B, 16);
+  const size_t o_xn = take(rows16 * c.dim * 2), o_qd = take(B * c.q_dim * 2), o_attn = take(rows16 * c.q_dim * 2);
   // gate: split rows [B][2*hidden], or (B >= 8) B-fragment order over 16 row slots
-  const size_t o_gate = take(std::max<size_t>(2 * B, 16) * c.hidden * 2), o_qdlo = take(B * c.q_dim * 2);
+  const size_t o_gate = take(rows16 * c.hidden * 2), o_qdlo = take(B * c.q_dim * 2);
   char* sb = nullptr;
   e = hipMalloc(&sb, off);
   if (e != hipSuccess) {
@@ -2694,6 +2845,7 @@ int train_forward(hb_model* m, int B, int S) {
   const int qkv = c.q_dim + 2 * c.kv_dim;
   const float alpha = alpha_of(c);
   const size_t khs = (size_t)Sp * c.hd, kbs = (size_t)c.kv_heads * khs;
+  ts->softcap = c.softcap;
   HIP_TRY(embedding(m->embed, ts->tok, T, c.dim, c.vocab, ts->act[0].x, m->ctx->d_err, st));
   for (int l = 0; l < c.nlayers; ++l) {
     const LayerW& L = m->layers[l];
@@ -2722,7 +2874,7 @@ int train_forward(hb_model* m, int B, int S) {
     HIP_TRY(gemm_residual(L.w2, A.gate, c.dim, T, c.hidden, EpiResidual{A.x2, xout, c.dim, alpha}, &s2, st));
   }
   HIP_TRY(rmsnorm(ts->xL, c.dim, m->gamma_f, T, c.dim, c.norm_eps, ts->xf, nullptr, st));
-  HIP_TRY(gemm_logits(m->embed, ts->xf, c.vocab, T, c.dim, EpiLogits{ts->logits, c.vocab, c.softcap}, st));
+  HIP_TRY(gemm_logits(m->embed, ts->xf, c.vocab, T, c.dim, EpiLogits{ts->logits, c.vocab, ts->softcap}, st));
   HIP_TRY(cross_entropy(ts->logits, ts->tgt, T, c.vocab, ts->loss, nullptr, m->ctx->d_err, st));
   HIP_TRY(mean_reduce(ts->loss, T, ts->mean, st));
   return HB_OK;
@@ -2801,7 +2953,7 @@ int train_backward_impl(hb_model* m, hb_opt* o, int B, int S, float loss_scale) 
   int fexp = 0;
   (void)frexpf(16384.0f / gs, &fexp);
   const float f = ldexpf(1.0f, fexp - 1), inv_f = ldexpf(1.0f, 1 - fexp);
-  HIP_TRY(ce_backward(ts->logits, ts->tgt, T, c.vocab, Vp, gs * f, c.softcap, ts->dl, st));
+  HIP_TRY(ce_backward(ts->logits, ts->tgt, T, c.vocab, Vp, gs * f, ts->softcap, ts->dl, st));
   HIP_TRY(transpose_f16(ts->dl, T, c.vocab, Vp, 0, ts->dlT, Tp, 0, 1, st));
   GemmScratch se;
   TRY(residual_scratch(m, d, T, Vp, se, 512));
@@ -2917,7 +3069,7 @@ int train_forward_views(hb_model* m, int B, int S, const hb_forward_result* r) {
   TrainState* ts = m->train;
   hipStream_t st = m->ctx->stream();
   const size_t T = (size_t)B * S, TV = T * c.vocab, Td = T * c.dim;
-  const bool want_cap = r->logits_capped && c.softcap > 0.f;
+  const bool want_cap = r->logits_capped && ts->softcap > 0.f;
   const size_t need = (r->dlogits ? TV : 0) + (want_cap ? TV : 0) + (r->x_prenorm ? Td : 0) +
                       (r->x_final ? Td : 0) + T;
   if (need > ts->views_floats) {
@@ -2940,7 +3092,7 @@ int train_forward_views(hb_model* m, int B, int S, const hb_forward_result* r) {
   float* d_fin = take(r->x_final != nullptr, Td);
   float* d_rinv = take(true, T);
   if (d_dl || d_cap)
-    HIP_TRY(ce_grad_views(ts->logits, ts->tgt, (int)T, c.vocab, 1.0f / (float)S, c.softcap, d_dl, d_cap, st));
+    HIP_TRY(ce_grad_views(ts->logits, ts->tgt, (int)T, c.vocab, 1.0f / (float)S, ts->softcap, d_dl, d_cap, st));
   // the forward's own rms_inv (same kernel, same reduction order)
   HIP_TRY(rmsnorm(ts->xL, c.dim, m->gamma_f, (int)T, c.dim, c.norm_eps, ts->xf, d_rinv, st));
   if (d_pre || d_fin)

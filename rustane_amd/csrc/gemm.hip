@@ -259,10 +259,12 @@ hipError_t gemm_residual(const f16* W, const f16* X, int N, int T, int K, const 
   return launch_gemm(W, X, N, T, K, e, scr, st, {}, kw);
 }
 hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
-                              const NormOut& no, const GemmScratch* scr, hipStream_t st, int kw) {
+                              const NormOut& no, const GemmScratch* scr, hipStream_t st, int kw,
+                              hipEvent_t mid) {
   if (e.ld != N) return hipErrorInvalidValue;
   bool wide = false;
   const int S = scr ? gemm_norm_splits(N, T, K, scr->wgs, &wide) : 1;
+  hipError_t err2 = hipSuccess;
   if (S > 1) {
     const size_t stride = (size_t)T * N;
     if (!scr->p || (size_t)S * stride > scr->floats || (long)N * K >= (1L << 31)) return hipErrorInvalidValue;
@@ -270,6 +272,7 @@ hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, c
         wide ? launch_tile<256, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S, {}, kw)
              : launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S, {}, kw);
     if (err != hipSuccess) return err;
+    if (mid && (err2 = hipEventRecord(mid, st)) != hipSuccess) return err2;
     switch (N % 1024 == 0 ? N / 1024 : 0) {
 #define HB_RN(n)                                                                                \
   case n:                                                                                       \
@@ -286,6 +289,7 @@ hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, c
   }
   const hipError_t err = launch_gemm(W, X, N, T, K, e, nullptr, st, {}, kw);
   if (err != hipSuccess) return err;
+  if (mid && (err2 = hipEventRecord(mid, st)) != hipSuccess) return err2;
   return rmsnorm(e.out, N, no.gamma, T, N, no.eps, no.xn, nullptr, st, no.split);
 }
 hipError_t gemm_swiglu(const f16* W, const f16* X, int N, int T, int K, const EpiSwiGLU& e,

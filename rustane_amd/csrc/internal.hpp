@@ -38,8 +38,11 @@ struct NormOut {
   f16* xn;             // [T, N], or split rows [T, 2N]
   bool split = false;
 };
+// mid (nullable): an event recorded after the projection, before the
+// reduction / norm launch (a timed forward's stage boundary).
 hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, const EpiResidual& e,
-                              const NormOut& no, const GemmScratch* scr, hipStream_t st, int kw = 0);
+                              const NormOut& no, const GemmScratch* scr, hipStream_t st, int kw = 0,
+                              hipEvent_t mid = nullptr);
 hipError_t gemm_swiglu(const f16* W, const f16* X, int N, int T, int K, const EpiSwiGLU& e,
                        hipStream_t st, int kw = 0);
 hipError_t gemm_logits(const f16* W, const f16* X, int N, int T, int K, const EpiLogits& e,

@@ -281,6 +281,30 @@ def forward_logits(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional
     return ForwardLogits(loss=loss, losses=losses, logits=logits)
 
 
+def forward_timed(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelWeights], tokens,
+                  targets, softcap: float = 0.0, batch: int = 1):
+    """forward_timed (layer.rs:850-1015) for the whole model (hb_forward_timed):
+    the forward's mean loss and the device time of each of its stages (a dict
+    of hb_forward_timings' fields, in ms). The tokens go to device buffers
+    first (torch provides them); the timed forward is hb_forward_device's."""
+    import torch
+    kernels.ensure_weights(weights)
+    kernels.set_softcap(softcap)
+    tok = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+    if tok.size % batch:
+        raise ValueError("token count not divisible by batch")
+    S = tok.size // batch
+    dt = torch.from_numpy(tok.view(np.int32).copy()).cuda()
+    dg = None
+    if targets is not None:
+        dg = torch.from_numpy(np.ascontiguousarray(targets, dtype=np.uint32).reshape(-1).view(np.int32).copy()).cuda()
+    dm = torch.zeros(1, device="cuda")
+    torch.cuda.synchronize()
+    t = kernels.model.forward_timed(dt.data_ptr(), None if dg is None else dg.data_ptr(), batch, S, None,
+                                    dm.data_ptr() if dg is not None else None)
+    return float(dm.cpu()[0]), t
+
+
 @dataclass
 class ForwardCaches:
     """ForwardResult.caches (full_model.rs:75; layer.rs ForwardCache per layer):
@@ -289,6 +313,8 @@ class ForwardCaches:
     kernels: "CompiledKernels"
     batch: int
     seq: int
+    softcap: float = 0.0
+    tokens: Optional[np.ndarray] = None
 
 
 @dataclass
@@ -321,7 +347,8 @@ def forward(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[ModelW
     views = ["dlogits", "x_final", "x_prenorm", "rms_inv_final"] + (["logits_capped"] if softcap > 0 else [])
     loss, _, v = kernels.model.train_forward(tok, targets, batch, S, views)
     flat = (lambda a: a.reshape(-1)) if batch == 1 else (lambda a: a)
-    return ForwardResult(loss=loss, caches=ForwardCaches(kernels, batch, S), dlogits=v["dlogits"],
+    caches = ForwardCaches(kernels, batch, S, float(softcap), tok.copy())
+    return ForwardResult(loss=loss, caches=caches, dlogits=v["dlogits"],
                          x_final=flat(v["x_final"]), x_prenorm=flat(v["x_prenorm"]),
                          rms_inv_final=v["rms_inv_final"],
                          logits_capped=v.get("logits_capped", np.zeros(0, np.float32)))
@@ -332,11 +359,18 @@ def backward(cfg: ModelConfig, kernels: CompiledKernels, weights: Optional[Model
              ws=None) -> None:
     """full_model.rs:414-483 from fwd.caches (hb_train_backward): the
     gradients of loss_scale * mean CE are ADDED to grads (the device gradient
-    arena of a ModelOptState). `tokens` and `softcap` are the forward's (kept
-    on the device with the caches); `ws` is accepted for the reference's
-    signature, the workspace lives on the device."""
+    arena of a ModelOptState). `tokens` and `softcap` must be the forward's
+    (its activations, capped logits included, stay on the device with the
+    caches): anything else raises ValueError before the caches are used;
+    `ws` is accepted for the reference's signature, the workspace lives on
+    the device."""
     if fwd.caches.kernels is not kernels or grads.kernels is not kernels:
         raise ValueError("fwd and grads must belong to these kernels")
+    if float(softcap) != fwd.caches.softcap:
+        raise ValueError(f"softcap {softcap} differs from the forward's {fwd.caches.softcap}")
+    tok = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+    if fwd.caches.tokens is not None and not np.array_equal(tok, fwd.caches.tokens):
+        raise ValueError("tokens differ from the forward's")
     kernels.ensure_weights(weights)
     grads.opt.backward(loss_scale)
 

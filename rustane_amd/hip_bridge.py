@@ -93,6 +93,18 @@ class hb_forward_result(C.Structure):
                                           "logits_capped")]
 
 
+class hb_forward_timings(C.Structure):
+    """Per-stage device time of one forward (ForwardTimings, layer.rs:821-1015):
+    stage sums over layers 1..nlayers-1, the first layer in layer0_ms."""
+    _fields_ = [(n, C.c_float) for n in (
+        "embedding_ms", "rmsnorm1_ms", "sdpa_qkv_ms", "sdpa_attention_ms", "wo_ms", "residual_rmsnorm2_ms",
+        "ffn_up_ms", "ffn_down_ms", "ffn_residual_norm_ms", "logits_ms", "cross_entropy_ms", "layer0_ms",
+        "total_ms")] + [("layers_summed", C.c_int32)]
+
+    def as_dict(self) -> dict:
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
 class hb_rstk_header(C.Structure):
     """RSTK checkpoint header (bin/train.rs:175-183) after the magic."""
     _fields_ = [(n, C.c_uint32) for n in ("version", "step", "dim", "nlayers", "vocab", "seq")]
@@ -132,6 +144,7 @@ SIGNATURES = {
     "hb_forward": [_P, _P, _P, _I, _I, _P, _P, _P],
     "hb_forward_device": [_P, _P, _P, _I, _I, _P, _P, _P],
     "hb_model_reserve": [_P, _I, _I],
+    "hb_forward_timed": [_P, _P, _P, _I, _I, _P, _P, _P],
     "hb_op_rmsnorm": [_P, _P, _P, _I, _I, _F, _P, _P],
     "hb_op_embedding": [_P, _P, _I, _P],
     "hb_op_sdpa_fwd": [_P, _I, _P, _I, _I, _P, _P],
@@ -342,6 +355,12 @@ class Model:
 
     def reserve(self, B: int, S: int) -> None:
         call("hb_model_reserve", self.handle, B, S)
+
+    def forward_timed(self, d_tokens: int, d_targets, B: int, S: int, d_loss=None, d_mean=None) -> dict:
+        """hb_forward_timed on device buffers (addresses): per-stage device times in ms."""
+        t = hb_forward_timings()
+        call("hb_forward_timed", self.handle, d_tokens, d_targets, B, S, d_loss, d_mean, C.byref(t))
+        return t.as_dict()
 
     def set_precise_layers(self, n: int) -> None:
         """hb_model_set_precise_layers: the first n layers run on two-term fp16 operands."""

@@ -5,6 +5,11 @@ from rustane_amd.engine import ModelConfig, ModelWeights
 
 F32 = np.float32
 
+# Parity comparisons of this pytest run (label, max |dlogit|, max rel dloss,
+# agreeing and compared top-1 positions, whether against the oracle); printed
+# by conftest.py's terminal summary.
+PARITY = []
+
 
 def tiny_config(**kw) -> ModelConfig:
     """Smallest shape the library accepts (dims multiple of 64, hd 64); seq 40 is

@@ -20,6 +20,27 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (run with -m gpu)")
 
 
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """The parity numbers of every full-size comparison that ran (max |dlogit|,
+    max relative per-position loss error, top-1 agreement), and the top-1
+    agreement pooled over the comparisons with the oracle."""
+    from tests._util import PARITY
+    if not PARITY:
+        return
+    tr = terminalreporter
+    tr.write_sep("-", "parity (bars: max|dlogit| <= 2e-2, rel dloss <= 1e-3, top-1 >= 99.5%)")
+    for r in PARITY:
+        rel = "" if r["rel"] is None else f" rel dloss {r['rel']:.2e}"
+        tr.write_line(f"{r['label']}: max|dlogit| {r['err']:.2e}{rel} top-1 {r['same']}/{r['n']} "
+                      f"= {100.0 * r['same'] / r['n']:.2f}%")
+    o = [r for r in PARITY if r["oracle"]]
+    if o:
+        same, n = sum(r["same"] for r in o), sum(r["n"] for r in o)
+        tr.write_line(f"pooled over {len(o)} oracle comparisons: top-1 {same}/{n} = {100.0 * same / n:.2f}%, "
+                      f"max|dlogit| {max(r['err'] for r in o):.2e}, max rel dloss "
+                      f"{max((r['rel'] for r in o if r['rel'] is not None), default=0.0):.2e}")
+
+
 @pytest.fixture(scope="session")
 def gpu():
     """torch (device memory and streams only) + one hip_bridge context bound to

@@ -572,6 +572,46 @@ def test_forward_result_then_backward(softcap):
         st.close()
 
 
+def test_backward_keeps_the_forwards_softcap():
+    """An inference forward with another softcap between the pair (it sets the
+    model's softcap to its own) leaves the backward unchanged: the kept logits
+    were capped with the training forward's softcap (full_model.rs:234-239),
+    so the backward's tanh derivative uses that one. A backward called with
+    another softcap or other tokens than the forward's is refused."""
+    cfg = tiny_config(heads=4, kv_heads=2)
+    k = CompiledKernels.compile(cfg)
+    w = ModelWeights.synthetic(cfg, seed=42, std=0.05)
+    st = E.ModelOptState(k, E.TrainConfig(), weights=w)
+    try:
+        S = cfg.seq
+        tok = tokens_for(cfg, S + 1, seed=43)
+        st.opt.zero_grads()
+        fwd = E.forward(cfg, k, None, tok[:-1], tok[1:], softcap=0.5)
+        E.forward_ws(cfg, k, None, tok[:-1], tok[1:], softcap=0.0)
+        with pytest.raises(ValueError):
+            E.backward(cfg, k, None, fwd, tok[:-1], 0.0, 256.0, st)
+        other = tok[:-1].copy()
+        other[0] = (other[0] + 1) % cfg.vocab
+        with pytest.raises(ValueError):
+            E.backward(cfg, k, None, fwd, other, 0.5, 256.0, st)
+        E.backward(cfg, k, None, fwd, tok[:-1], 0.5, 256.0, st)
+        pair = _device_grads(st.opt, cfg.nlayers)
+        st.opt.zero_grads()
+        k.set_softcap(0.5)
+        st.opt.forward_backward(tok[:-1], tok[1:], 1, S, 256.0)
+        fused = _device_grads(st.opt, cfg.nlayers)
+        for name, a, b in _pairs(pair, fused):
+            np.testing.assert_array_equal(a, b, err_msg=name)
+        # and the softcap matters here: without it the gradients differ
+        st.opt.zero_grads()
+        k.set_softcap(0.0)
+        st.opt.forward_backward(tok[:-1], tok[1:], 1, S, 256.0)
+        uncapped = _device_grads(st.opt, cfg.nlayers)
+        assert any(not np.array_equal(a, b) for _, a, b in _pairs(pair, uncapped))
+    finally:
+        st.close()
+
+
 def test_error_paths():
     cfg = tiny_config()
     k = CompiledKernels.compile(cfg)

@@ -39,14 +39,24 @@ seq 512 1.26e-2 / 8.4e-4 / 99.6%, seq 2048 1.37e-2 / 6.8e-4 / 99.56%; decode
 1.04e-2 and 41/41), so the bars are applied as stated: logits and per-position
 loss on every sequence, greedy top-1 >= 99.5% as a flip rate. Over n compared
 positions a rate allows the flips of the 98% quantile of Binomial(n, 0.005)
-(flips_allowed: 1 of 41, 6 of 512, 17 of 2048), checked per sequence, per
-test and pooled over the module (test_zz_pooled_flip_rate). A bare count
-bar would not test the rate: an implementation exactly at 99.5% flips at
-least one of 41 positions 19% of the time, and any change of fp32 summation
+(flips_allowed: 6 of 512, 17 of 2048), checked per sequence and per test, and
+the pooled point estimate over every oracle comparison of the module must
+itself reach 99.5% (test_zz_pooled_flip_rate). A bare count bar per sequence
+would not test the rate: an implementation exactly at 99.5% flips more than
+2 of 512 positions about half the time, and any change of fp32 summation
 order anywhere in the model moves which near-tied positions flip (logits move
 by ~1e-2 through 32 layers). Two device computations that each meet the
 rate (decode against the device's own prefill, batch 16 against batch 1)
-are held to twice it.
+are held to twice it. Every comparison is also listed, with its numbers, at
+the end of the pytest run (conftest.py's terminal summary).
+
+Decode is compared teacher-forced at each of the benchmark's 256 steps after
+the 2048-token prompt, at batch 1 and for row 0 of batch 16. The oracle's
+logits for step i are row 2048 + i of one oracle forward over the 2304
+tokens (the oracle's decode step at position p is row p of its forward over
+tokens 0..p, Appendix A item 8; DecodeOracle.step is run for the first steps
+on the same cache and checked against those rows), which costs one forward
+instead of 256 steps through 26 GB of fp32 weights.
 
 Two device runs of one sequence (batch 8 against batch 1) use different tile
 shapes and K splits, so their fp32 sums differ in order; each lies within the
@@ -72,7 +82,7 @@ import pytest
 import oracle as O
 from rustane_amd import engine as E
 from rustane_amd.engine import CompiledKernels, ModelConfig
-from tests._util import oracle_cfg, synthetic_oracle_weights, tokens_for
+from tests._util import PARITY, oracle_cfg, synthetic_oracle_weights, tokens_for
 
 pytestmark = pytest.mark.gpu
 
@@ -146,6 +156,8 @@ def _compare(label, V, g_logits, g_losses, r_logits, r_losses, rate=FLIP_RATE,
     same = int((gl.argmax(-1) == rl.argmax(-1)).sum())
     top1 = same / gl.shape[0]
     print(f"{label}: max|dlogit|={err:.3e} max rel dloss={rel:.3e} top1={top1:.4f}", flush=True)
+    PARITY.append(dict(label=label, err=err, rel=rel, same=same, n=gl.shape[0],
+                       oracle=label.endswith("vs oracle")))
     if label.endswith("vs oracle"):
         _compare.agree.append((same, gl.shape[0]))
     if tally is not None:
@@ -245,8 +257,9 @@ def test_5b_b4_matches_oracle(m5b):
 # 7B shape: prefill at seq 512 and 2048, greedy decode after 2048 positions
 # ---------------------------------------------------------------------------
 P7 = 2048          # decode prompt = the seq-2048 prefill's tokens
-DEC_STEPS = 40     # teacher-forced decode steps checked against the oracle
+DEC_STEPS = 256    # teacher-forced decode steps checked against the oracle (the benchmark's 256)
 DEC_LONG = 256     # free-running greedy steps checked against the device's own prefill
+DEC_STEPWISE = 3   # oracle decode steps run one by one, against the oracle forward's rows
 
 
 @pytest.fixture(scope="module")
@@ -266,23 +279,41 @@ def tok7(m7b):
 
 @pytest.fixture(scope="module")
 def orc7(m7b, tok7):
-    """Oracle decoder after the 2048-token prefill (its full forward kept)."""
+    """Oracle forward over the prompt and the DEC_STEPS teacher-forced tokens
+    (prefill_out: logits and losses of all P7 + DEC_STEPS positions), kept as
+    a DecodeOracle with every position's K/V cached."""
     orc = O.DecodeOracle(m7b.oc, m7b.ow, ctx_max=P7 + DEC_STEPS)
     t0 = time.time()
-    orc.prefill(tok7[:P7], targets=tok7[1:P7 + 1])
-    print(f"7B oracle prefill of {P7} tokens in {time.time() - t0:.1f} s", flush=True)
+    orc.prefill(tok7[:P7 + DEC_STEPS], targets=tok7[1:P7 + DEC_STEPS + 1])
+    print(f"7B oracle forward of {P7 + DEC_STEPS} tokens in {time.time() - t0:.1f} s", flush=True)
     return orc
 
 
 @pytest.fixture(scope="module")
-def orc7_steps(orc7, tok7):
-    """Oracle logits of the DEC_STEPS teacher-forced steps after the prompt."""
-    out = []
+def orc7_steps(m7b, orc7, tok7):
+    """Oracle logits of the DEC_STEPS teacher-forced decode steps after the
+    prompt: step i (token P7 + i at position P7 + i) is row P7 + i of the
+    oracle forward. The first DEC_STEPWISE steps are also run through
+    DecodeOracle.step, rewound to position P7 on the same K/V cache, and must
+    give those rows (to fp32 summation order)."""
+    V = m7b.cfg.vocab
+    rows = orc7.prefill_out["logits"].reshape(P7 + DEC_STEPS, V)[P7:]
+    orc7.pos = P7
     t0 = time.time()
-    for i in range(DEC_STEPS):
-        out.append(orc7.step(int(tok7[P7 + i])))
-    print(f"7B oracle: {DEC_STEPS} decode steps in {time.time() - t0:.1f} s", flush=True)
-    return out
+    for i in range(DEC_STEPWISE):
+        d = float(np.abs(orc7.step(int(tok7[P7 + i])) - rows[i]).max())
+        print(f"7B oracle decode step {i} vs oracle forward row {P7 + i}: max|dlogit| {d:.2e}", flush=True)
+        assert d <= 1e-3, (i, d)
+    print(f"7B oracle: {DEC_STEPWISE} decode steps in {time.time() - t0:.1f} s", flush=True)
+    return [rows[i] for i in range(DEC_STEPS)]
+
+
+def _oracle_prefix(orc7, V):
+    """The oracle forward restricted to the first P7 positions (causal: rows < P7
+    of the longer forward are the P7-token forward's rows)."""
+    out = orc7.prefill_out
+    losses = np.asarray(out["losses"]).reshape(-1)[:P7]
+    return out["logits"].reshape(-1, V)[:P7], losses, float(np.float64(losses).mean())
 
 
 @pytest.mark.timeout(400)
@@ -295,16 +326,15 @@ def test_7b_s512_b8_matches_oracle(m7b):
     _check_batch(m7b, 8, 512, 47, [0, 7], "7B S=512 B=8", f32_rows=())
 
 
-@pytest.mark.timeout(400)
+@pytest.mark.timeout(600)
 def test_7b_s2048_b1_matches_oracle(m7b, tok7, orc7):
     cfg = m7b.cfg
     res = m7b.forward(tok7[:P7], tok7[1:P7 + 1], 1)
-    ref = orc7.prefill_out
+    r_logits, r_losses, r_loss = _oracle_prefix(orc7, cfg.vocab)
     tally = []
-    _compare("7B S=2048 B=1 vs oracle", cfg.vocab, res.logits, res.losses, ref["logits"], ref["losses"],
-             tally=tally)
+    _compare("7B S=2048 B=1 vs oracle", cfg.vocab, res.logits, res.losses, r_logits, r_losses, tally=tally)
     _check_tally("7B S=2048 B=1", tally)
-    assert abs(res.loss - float(ref["loss"])) <= LOSS_RTOL * float(ref["loss"])
+    assert abs(res.loss - r_loss) <= LOSS_RTOL * r_loss
 
 
 @pytest.mark.timeout(300)
@@ -316,10 +346,9 @@ def test_7b_s2048_b8_matches_oracle(m7b, tok7, orc7):
     res = m7b.forward(tok[:, :-1], tok[:, 1:], B)
     gl = res.logits.reshape(B, P7, cfg.vocab)
     gs = res.losses.reshape(B, P7)
-    ref = orc7.prefill_out
+    r_logits, r_losses, _ = _oracle_prefix(orc7, cfg.vocab)
     tally = []
-    _compare("7B S=2048 B=8 row 0 vs oracle", cfg.vocab, gl[0], gs[0], ref["logits"], ref["losses"],
-             tally=tally)
+    _compare("7B S=2048 B=8 row 0 vs oracle", cfg.vocab, gl[0], gs[0], r_logits, r_losses, tally=tally)
     _check_tally("7B S=2048 B=8", tally)
     for b in (1, B - 1):
         one = m7b.forward(tok[b, :-1], tok[b, 1:], 1)
@@ -327,13 +356,13 @@ def test_7b_s2048_b8_matches_oracle(m7b, tok7, orc7):
                  bar_scale=BAR_DEVICE_PAIR)
 
 
-@pytest.mark.timeout(300)
+@pytest.mark.timeout(400)
 def test_7b_decode_b1_teacher_forced_matches_oracle(m7b, tok7, orc7, orc7_steps):
     cfg = m7b.cfg
     dec = E.Decoder(m7b.k, batch=1, ctx_max=P7 + DEC_STEPS)
     try:
         gl, gn = dec.prefill(tok7[:P7])
-        rl = orc7.prefill_out["logits"].reshape(P7, cfg.vocab)[-1]
+        rl = _oracle_prefix(orc7, cfg.vocab)[0][-1]
         errs, agree = [float(np.abs(gl[0] - rl).max())], [int(gn[0]) == int(rl.argmax())]
         for i in range(DEC_STEPS):
             gl, gn = dec.step([tok7[P7 + i]])
@@ -342,6 +371,8 @@ def test_7b_decode_b1_teacher_forced_matches_oracle(m7b, tok7, orc7, orc7_steps)
             agree.append(int(gn[0]) == int(rl.argmax()))
             assert int(gn[0]) == int(gl[0].argmax())
         print(f"7B decode B=1 after {P7}: max|dlogit|={max(errs):.3e}", flush=True)
+        PARITY.append(dict(label=f"7B decode B=1, {DEC_STEPS} teacher-forced steps vs oracle", err=max(errs),
+                           rel=None, same=int(sum(agree)), n=len(agree), oracle=True))
         assert max(errs) <= LOGIT_ATOL
         _compare.agree.append((int(sum(agree)), len(agree)))
         _check_flips(f"7B decode B=1 after {P7} vs oracle", int(sum(agree)), len(agree))
@@ -350,12 +381,13 @@ def test_7b_decode_b1_teacher_forced_matches_oracle(m7b, tok7, orc7, orc7_steps)
         dec.kv.close()
 
 
-@pytest.mark.timeout(300)
+@pytest.mark.timeout(400)
 def test_7b_decode_b16_rows_match_oracle_and_batch_one(m7b, tok7, orc7, orc7_steps):
-    """Batch 16: row 0 carries the oracle's sequence (teacher-forced, its logits
-    compared with the oracle at every step); row 15 is compared with a batch-1
-    decoder fed the same tokens, greedy token included."""
-    cfg, B, n = m7b.cfg, 16, 4
+    """Batch 16: row 0 carries the oracle's sequence (teacher-forced: its logits
+    and its greedy token compared with the oracle at every one of the 256
+    steps); row 15 is compared with a batch-1 decoder fed the same tokens,
+    greedy token included."""
+    cfg, B, n = m7b.cfg, 16, DEC_STEPS
     others = [tokens_for(cfg, P7 + n, seed=49, stream=b) for b in range(1, B)]
     tok = np.stack([tok7[:P7 + n]] + others)
     db = E.Decoder(m7b.k, batch=B, ctx_max=P7 + n)
@@ -363,21 +395,29 @@ def test_7b_decode_b16_rows_match_oracle_and_batch_one(m7b, tok7, orc7, orc7_ste
     try:
         lb, nb = db.prefill(tok[:, :P7])
         l1, _ = d1.prefill(tok[B - 1, :P7])
-        rl = orc7.prefill_out["logits"].reshape(P7, cfg.vocab)[-1]
+        rl = _oracle_prefix(orc7, cfg.vocab)[0][-1]
         errs = [float(np.abs(lb[0] - rl).max())]
+        agree0 = [int(nb[0]) == int(rl.argmax())]
         cross = [float(np.abs(lb[B - 1] - l1[0]).max())]
         same1 = int(int(lb[B - 1].argmax()) == int(l1[0].argmax()))
         for i in range(n):
             lb, nb = db.step(tok[:, P7 + i])
             l1, _ = d1.step([tok[B - 1, P7 + i]])
             errs.append(float(np.abs(lb[0] - orc7_steps[i]).max()))
+            agree0.append(int(nb[0]) == int(orc7_steps[i].argmax()))
             cross.append(float(np.abs(lb[B - 1] - l1[0]).max()))
             assert int(nb[0]) == int(lb[0].argmax())
             same1 += int(int(nb[B - 1]) == int(l1[0].argmax()))
         print(f"7B decode B=16: row 0 vs oracle max|dlogit|={max(errs):.3e}; row 15 vs batch 1 "
               f"{max(cross):.3e}", flush=True)
+        PARITY.append(dict(label=f"7B decode B=16 row 0, {n} teacher-forced steps vs oracle", err=max(errs),
+                           rel=None, same=int(sum(agree0)), n=len(agree0), oracle=True))
+        PARITY.append(dict(label="7B decode B=16 row 15 vs batch 1", err=max(cross), rel=None, same=same1,
+                           n=n + 1, oracle=False))
         assert max(errs) <= LOGIT_ATOL
         assert max(cross) <= LOGIT_ATOL
+        _compare.agree.append((int(sum(agree0)), len(agree0)))
+        _check_flips("7B decode B=16 row 0 vs oracle", int(sum(agree0)), len(agree0))
         _check_flips("7B decode B=16 row 15 vs batch 1", same1, n + 1, rate=2 * FLIP_RATE)
     finally:
         db.kv.close()
@@ -428,6 +468,8 @@ def _greedy_against_prefill(m7b, B, rows, seed):
         tally.append((same, got.shape[0]))
         print(f"7B decode B={B} row {b}: {got.shape[0]} decoded positions vs device prefill rows: "
               f"max|dlogit|={err:.3e} top1 {same}/{got.shape[0]}", flush=True)
+        PARITY.append(dict(label=f"7B greedy B={B} row {b}, {got.shape[0]} steps vs device prefill rows",
+                           err=err, rel=None, same=same, n=got.shape[0], oracle=False))
         assert err <= LOGIT_ATOL
     _check_tally(f"7B decode B={B} vs prefill rows", tally, rate=2 * FLIP_RATE)
 
@@ -449,3 +491,4 @@ def test_zz_pooled_flip_rate():
         pytest.skip("no oracle comparison ran")
     same, n = sum(a for a, _ in _compare.agree), sum(c for _, c in _compare.agree)
     _check_flips("all oracle comparisons", same, n)
+    assert same / n >= 1.0 - FLIP_RATE, (same, n)  # the contract's 99.5%, as a point estimate

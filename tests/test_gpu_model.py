@@ -425,6 +425,78 @@ def test_decode_equals_prefill_rows_with_precise_layers(gpu, n):
         np.testing.assert_array_equal(out[i], cur)
 
 
+def test_forward_timed_stages(gpu):
+    """hb_forward_timed (forward_timed, layer.rs:821-1015): the same launches as
+    hb_forward_device (losses equal bit for bit), each stage's device time
+    positive, the stages adding up to the forward's span (the events between
+    them take a little time of their own)."""
+    import torch
+    cfg = ModelConfig.make(dim=1024, hidden=2816, heads=8, nlayers=3, seq=256, vocab=2048, hd=128)
+    k = CompiledKernels.compile(cfg)
+    k.init_synthetic(91)
+    B, S = 2, 256
+    tok = tokens_for(cfg, B * (S + 1), seed=92).reshape(B, S + 1)
+    dt = torch.from_numpy(tok[:, :-1].astype(np.int32).copy()).cuda()
+    dg = torch.from_numpy(tok[:, 1:].astype(np.int32).copy()).cuda()
+    l0, l1 = torch.empty(B * S, device="cuda"), torch.empty(B * S, device="cuda")
+    m0, m1 = torch.empty(1, device="cuda"), torch.empty(1, device="cuda")
+    hb.call("hb_forward_device", k.model.handle, dt.data_ptr(), dg.data_ptr(), B, S, l0.data_ptr(), None,
+            m0.data_ptr())
+    k.ctx.synchronize()
+    torch.cuda.synchronize()
+    t = k.model.forward_timed(dt.data_ptr(), dg.data_ptr(), B, S, l1.data_ptr(), m1.data_ptr())
+    torch.cuda.synchronize()
+    assert torch.equal(l0, l1) and torch.equal(m0, m1)
+    print("forward_timed:", {n: round(v, 4) for n, v in t.items()}, flush=True)
+    assert t["layers_summed"] == cfg.nlayers - 1
+    stages = ["embedding_ms", "sdpa_qkv_ms", "sdpa_attention_ms", "wo_ms", "residual_rmsnorm2_ms", "ffn_up_ms",
+              "ffn_down_ms", "ffn_residual_norm_ms", "logits_ms", "cross_entropy_ms", "layer0_ms"]
+    for n in stages:
+        assert t[n] > 0.0, n
+    assert t["rmsnorm1_ms"] == 0.0  # later layers' input norms come out of the W2 reduction
+    parts = sum(t[n] for n in stages)
+    assert parts <= t["total_ms"] * 1.0001 and parts >= 0.9 * t["total_ms"], (parts, t["total_ms"])
+    loss, t2 = E.forward_timed(cfg, k, None, tok[:, :-1], tok[:, 1:], batch=B)
+    assert abs(loss - float(m0.cpu()[0])) == 0.0 and t2["layers_summed"] == cfg.nlayers - 1
+
+
+def test_forward_graph_capture_across_shapes(gpu):
+    """hb_forward_device alternating between shapes through the eager ->
+    captured -> replayed sequence: B=1, B=8, B=1 x3 and back. The model's
+    split-K scratch has to grow for B=8 (Wo and W2 split K at these sizes),
+    which the library does before it captures, never inside a capture; every
+    call equals that shape's first (eager) forward bit for bit."""
+    import torch
+    cfg = ModelConfig.make(dim=1024, hidden=2816, heads=8, nlayers=2, seq=256, vocab=2048, hd=128)
+    k = CompiledKernels.compile(cfg)
+    k.init_synthetic(81)
+    S = 256
+    bufs, ref = {}, {}
+    for B in (1, 8):
+        tok = tokens_for(cfg, B * (S + 1), seed=82 + B).reshape(B, S + 1)
+        bufs[B] = (torch.from_numpy(tok[:, :-1].astype(np.int32).copy()).cuda(),
+                   torch.from_numpy(tok[:, 1:].astype(np.int32).copy()).cuda(),
+                   torch.empty(B * S, device="cuda"), torch.empty(B * S, cfg.vocab, device="cuda"),
+                   torch.empty(1, device="cuda"))
+
+    def fwd(B):
+        dt, dg, loss, logits, mean = bufs[B]
+        hb.call("hb_forward_device", k.model.handle, dt.data_ptr(), dg.data_ptr(), B, S, loss.data_ptr(),
+                logits.data_ptr(), mean.data_ptr())
+        k.ctx.synchronize()
+        torch.cuda.synchronize()
+        return loss.clone(), logits.clone(), mean.clone()
+
+    for i, B in enumerate((1, 1, 1, 8, 8, 8, 1, 1, 1, 8, 1, 8, 8, 1)):
+        got = fwd(B)
+        if B not in ref:
+            ref[B] = got
+            continue
+        for a, b in zip(got, ref[B]):
+            assert torch.equal(a, b), (i, B)
+    assert not torch.equal(ref[1][2], ref[8][2])
+
+
 def test_forward_graph_replays_match_eager(gpu):
     """Repeated identical hb_forward_device calls replay one captured HIP graph
     (first call eager, second captured). Every replay -- with eager forwards

@@ -136,7 +136,8 @@ def test_every_header_entry_point_is_declared_with_the_same_signature():
 
 def test_structs_match_the_header_field_for_field():
     hdr, rs = header_structs(), rust_structs()
-    assert set(hdr) == {"hb_model_config", "hb_train_config", "hb_forward_result", "hb_rstk_header"}
+    assert set(hdr) == {"hb_model_config", "hb_train_config", "hb_forward_result", "hb_forward_timings",
+                        "hb_rstk_header"}
     for name, fields in hdr.items():
         assert rs.get(name) == fields, (name, fields, rs.get(name))
 
