@@ -141,6 +141,15 @@ struct EpiLogits {
 //   out[2i] = x[2i] c - x[2i+1] s,   out[2i+1] = x[2i+1] c + x[2i] s.
 // Token t is position s = pos0 + t % S of sequence b = t / S (prefill), or
 // position *d_pos of sequence b = t (decode, S = 1, pos0 read from d_pos).
+//
+// EpiQKV holds the parameters; the kernels run EpiQKVAt<DECODE, MODE>, which
+// fixes at compile time whether the position comes from d_pos (decode) or
+// from the token index (prefill), and which outputs exist (mode()): the
+// optional low parts and tap, tested per quad, cost the 7B QKV epilogue
+// ~4 us and the 5B one at 2048 tokens ~8 us when they are runtime branches. A runtime d_pos test in the prefill GEMM left a load
+// on one side of a branch in every quad, and the wait it needs at the join
+// (vmcnt(0) on gfx950, where stores count too) serialised every quad's stores
+// behind the previous ones: 7B QKV epilogue 9.5 us, 5B at 2048 tokens 39 us.
 struct EpiQKV {
   int q_dim, kv_dim, hd, S, heads, kv_heads;
   const float2* rope;  // [hd/2][rope_ld] (cos, sin), pair-major
@@ -168,8 +177,9 @@ struct EpiQKV {
     div_S = FastDiv((uint32_t)S);
     div_hd = FastDiv((uint32_t)hd);
   }
+  template <bool DEC>
   HB_DEV void pos_of(int t, int& b, int& s) const {
-    if (d_pos) {
+    if constexpr (DEC) {
       b = t;
       s = *d_pos;
     } else {
@@ -189,11 +199,12 @@ struct EpiQKV {
   struct Aux {
     float2 c0, c1;
   };
-  HB_DEV Aux load(int t, int f0, int fb) const {
+  template <bool DEC>
+  HB_DEV Aux load_at(int t, int f0, int fb) const {
     Aux a{};
     if (fb < q_dim + kv_dim) {
       int b, s;
-      pos_of(t, b, s);
+      pos_of<DEC>(t, b, s);
       const int fr = fb - region_start(fb);
       const int e = fr - div_hd.div(fr) * hd + (f0 - fb);
       const float2* rp = rope + (size_t)(e >> 1) * rope_ld + s;
@@ -202,9 +213,17 @@ struct EpiQKV {
     }
     return a;
   }
-  HB_DEV void operator()(int t, int f0, f32x4 v4, const Aux& a, int fb) const {
+  // Output modes of the kernels' instances (EpiQKVAt): PLAIN writes fp16 Q,
+  // K and V^T and/or V rows (every layer but the two-term ones); SPLIT also
+  // writes the low parts (q_lo .. vt_lo); FULL also the fp32 tap.
+  enum Mode { PLAIN = 0, SPLIT = 1, FULL = 2 };
+  __host__ int mode() const {
+    return tap ? FULL : (q_lo || k_lo || v_lo || vt_lo) ? SPLIT : PLAIN;
+  }
+  template <bool DEC, int MODE>
+  HB_DEV void store_at(int t, int f0, f32x4 v4, const Aux& a, int fb) const {
     int b, s;
-    pos_of(t, b, s);
+    pos_of<DEC>(t, b, s);
     const int r0 = region_start(fb), fr = fb - r0;
     const int h = div_hd.div(fr), e = fr - h * hd + (f0 - fb);
     f32x4 o = v4;
@@ -215,6 +234,26 @@ struct EpiQKV {
       o.w = v4.w * a.c1.x + v4.z * a.c1.y;
     }
     const f16x4 oh = f16x4_hi(o);
+    if constexpr (MODE == PLAIN) {
+      // one f16x4 store per quad (Q, K or V rows) and, for V^T, four
+      // 2-byte stores; every branch is wave-uniform (fb)
+      if (r0 == 0) {
+        const size_t hs = (size_t)q_rows * hd;
+        *(f16x4*)(q + b * (heads * hs) + h * hs + (size_t)(DEC ? 0 : s) * hd + e) = oh;
+      } else if (r0 == q_dim) {
+        *(f16x4*)(k + b * k_bstride + h * k_hstride + (size_t)s * hd + e) = oh;
+      } else {
+        if (v) *(f16x4*)(v + b * v_bstride + h * v_hstride + (size_t)s * hd + e) = oh;
+        if (vt) {
+          f16* p = vt + ((size_t)b * kv_heads + h) * hd * vt_ld + (size_t)e * vt_ld + s;
+          p[0] = oh.x;
+          p[vt_ld] = oh.y;
+          p[2 * vt_ld] = oh.z;
+          p[3 * vt_ld] = oh.w;
+        }
+      }
+      return;
+    }
     // Q, K and V rows share one addressing form: base + b*bstride + h*hstride + s*hd + e
     f16 *base, *base_lo;
     size_t bs, hs;
@@ -224,7 +263,7 @@ struct EpiQKV {
       base_lo = q_lo;
       hs = (size_t)q_rows * hd;
       bs = (size_t)heads * hs;
-      if (d_pos) srow = 0;  // decode keeps one Q row per sequence
+      if (DEC) srow = 0;  // decode keeps one Q row per sequence
     } else if (r0 == q_dim) {
       base = k;
       base_lo = k_lo;
@@ -258,10 +297,18 @@ struct EpiQKV {
     }
     if (tap) *(f32x4*)(tap + (size_t)t * (q_dim + 2 * kv_dim) + f0) = o;
   }
-  HB_DEV Aux load(int t, int f0) const { return load(t, f0, f0 & ~31); }
-  HB_DEV void operator()(int t, int f0, f32x4 v4) const {
-    (*this)(t, f0, v4, load(t, f0), f0 & ~31);
+};
+
+template <bool DECODE, int MODE>
+struct EpiQKVAt : EpiQKV {
+  EpiQKVAt() = default;
+  __host__ explicit EpiQKVAt(const EpiQKV& e) : EpiQKV(e) {}
+  HB_DEV Aux load(int t, int f0, int fb) const { return load_at<DECODE>(t, f0, fb); }
+  HB_DEV void operator()(int t, int f0, f32x4 v4, const Aux& a, int fb) const {
+    store_at<DECODE, MODE>(t, f0, v4, a, fb);
   }
+  HB_DEV Aux load(int t, int f0) const { return load(t, f0, f0 & ~31); }
+  HB_DEV void operator()(int t, int f0, f32x4 v4) const { (*this)(t, f0, v4, load(t, f0), f0 & ~31); }
 };
 
 // ---- training (backward) epilogues ----

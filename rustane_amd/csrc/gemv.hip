@@ -464,9 +464,20 @@ hipError_t gemv_logits(const f16* Wt, const f16* X, const NormIn* nin, int N, in
 hipError_t gemv_qkv(const f16* Wt, const f16* X, const NormIn* nin, int N, int B, int K,
                     const EpiQKV& e, hipStream_t st, bool split, bool xfrag) {
   if (e.S < 1 || e.hd < 1) return hipErrorInvalidValue;
-  EpiQKV ep = e;
-  ep.prepare();
-  return launch_gemv(Wt, X, nin, nullptr, N, B, K, ep, st, split, xfrag);
+  auto run = [&](auto dec, auto mode) {
+    EpiQKVAt<decltype(dec)::value, decltype(mode)::value> ep(e);
+    ep.prepare();
+    return launch_gemv(Wt, X, nin, nullptr, N, B, K, ep, st, split, xfrag);
+  };
+  using Dec = std::integral_constant<bool, true>;
+  using Pre = std::integral_constant<bool, false>;
+  using Plain = std::integral_constant<int, EpiQKV::PLAIN>;
+  using Split = std::integral_constant<int, EpiQKV::SPLIT>;
+  using Full = std::integral_constant<int, EpiQKV::FULL>;
+  const int mode = e.mode();
+  if (e.d_pos)
+    return mode == EpiQKV::PLAIN ? run(Dec{}, Plain{}) : mode == EpiQKV::SPLIT ? run(Dec{}, Split{}) : run(Dec{}, Full{});
+  return mode == EpiQKV::PLAIN ? run(Pre{}, Plain{}) : mode == EpiQKV::SPLIT ? run(Pre{}, Split{}) : run(Pre{}, Full{});
 }
 hipError_t gemv_store(const f16* Wt, const f16* X, int N, int B, int K, float* C, hipStream_t st) {
   return launch_gemv(Wt, X, nullptr, nullptr, N, B, K, EpiStore{C, N}, st);
