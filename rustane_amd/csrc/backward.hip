@@ -1,5 +1,5 @@
 // Training backward: the elementwise and reduction kernels between the
-// backward GEMMs (gemm.hip, epilogues in epilogue.hpp). Everything here is
+// backward GEMMs (gemm_train.hip, epilogues in epilogue.hpp). Everything here is
 // HBM-bound byte work; the products themselves run on the MFMA GEMM.
 //
 // Layout conventions of the backward (the reference works channel-first

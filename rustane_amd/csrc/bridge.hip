@@ -1,6 +1,6 @@
 // C ABI of libhip_bridge.so (declared in include/hip_bridge.h): contexts, the
 // device model, the prefill forward, the per-kernel entry points and the decode
-// loop. Host orchestration only; kernels live in gemm.hip, gemv.hip,
+// loop. Host orchestration only; kernels live in gemm*.hip, gemv.hip,
 // attention.hip and elementwise.hip.
 #include <algorithm>
 #include <atomic>

@@ -24,7 +24,7 @@ struct EpiStore {
 };
 
 // Split-K partial sums of the prefill GEMM: split blockIdx.y writes
-// p[blockIdx.y * split_stride + t * ld + f0 ..]; splitk_reduce (gemm.hip) adds
+// p[blockIdx.y * split_stride + t * ld + f0 ..]; splitk_reduce (gemm_launch.hpp) adds
 // the splits in order and applies the real epilogue.
 struct EpiSplit {
   float* p;
@@ -38,7 +38,10 @@ struct EpiSplit {
 // out = res + alpha * v (fp32 residual stream). woFwd + vsma (layer.rs:784) and
 // the ffnFused residual (kernels/ffn_fused.rs:74-77). The prefill GEMM loads
 // the residual quads (load) for a group of quads before storing any of them;
-// res may be the same buffer as out.
+// res may be the same buffer as out. One explicit fma per element: left to
+// the compiler, whether v * alpha + r is fused differs between the kernel
+// instances (tile shapes), and with it the result of a token row between
+// batch sizes.
 struct EpiResidual {
   const float* res;
   float* out;
@@ -48,10 +51,10 @@ struct EpiResidual {
   HB_DEV f32x4 load(int t, int f0, int = 0) const { return *(const f32x4*)(res + (size_t)t * ld + f0); }
   HB_DEV void operator()(int t, int f0, f32x4 v, const f32x4& r, int = 0) const {
     f32x4 y;
-    y.x = v.x * alpha + r.x;
-    y.y = v.y * alpha + r.y;
-    y.z = v.z * alpha + r.z;
-    y.w = v.w * alpha + r.w;
+    y.x = __builtin_fmaf(v.x, alpha, r.x);
+    y.y = __builtin_fmaf(v.y, alpha, r.y);
+    y.z = __builtin_fmaf(v.z, alpha, r.z);
+    y.w = __builtin_fmaf(v.w, alpha, r.w);
     *(f32x4*)(out + (size_t)t * ld + f0) = y;
   }
   HB_DEV void operator()(int t, int f0, f32x4 v) const { (*this)(t, f0, v, load(t, f0)); }
@@ -228,6 +231,10 @@ struct EpiQKV {
     const int h = div_hd.div(fr), e = fr - h * hd + (f0 - fb);
     f32x4 o = v4;
     if (r0 < q_dim + kv_dim) {
+      // Contraction is left to the compiler here: explicit fma forms, and
+      // contract(off), make the 256x256 instances spill 620-660 bytes to
+      // scratch. The fusion it picks is the same in every prefill tile shape
+      // (a batch row equals its sequence run alone, bit for bit, tested).
       o.x = v4.x * a.c0.x - v4.y * a.c0.y;
       o.y = v4.y * a.c0.x + v4.x * a.c0.y;
       o.z = v4.z * a.c1.x - v4.w * a.c1.y;

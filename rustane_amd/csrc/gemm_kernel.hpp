@@ -1,4 +1,4 @@
-// Prefill GEMM kernel (launch policy in gemm.hip).
+// Prefill GEMM kernel (launch policy in gemm_launch.hpp).
 //
 // C^T tile = W_tile · X_tile^T on v_mfma_f32_32x32x16_f16:
 //   W [N, K] fp16, K contiguous (weights repacked output-major at upload)

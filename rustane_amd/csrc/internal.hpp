@@ -5,7 +5,7 @@
 
 namespace hb {
 
-// ---- prefill GEMM (gemm.hip) ----
+// ---- prefill GEMM (gemm.hip, gemm_qkv.hip, gemm_ffn.hip, gemm_train.hip) ----
 // Scratch for split-K partial sums (fp32); see gemm_splits.
 struct GemmScratch {
   float* p;
