@@ -16,7 +16,8 @@ Also reported on the same line:
   prefill_b8    the same forward at batch 8;
   prefill       every other prefill workload: 7B seq 2048 at batch 1 and 8,
                 48M (512d/1536h/8L, 8x64) at batch 1, 600M-shape at batch 1
-                and 8, 5B-shape at batch 4 (seq 512);
+                and 8, 5B-shape at batch 4 (seq 512), each with its device
+                time per stage and layer (hb_forward_timed);
   stages_b1     the headline forward's device time per stage (hb_forward_timed,
                 the reference's forward_timed split: QKV, attention, Wo,
                 residual + norm, FFN up, FFN down, ...), per layer;
@@ -28,8 +29,10 @@ Also reported on the same line:
                 7B decode step at batch 1 and 16.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
+  python bench.py --model 600m --no-decode ...   (one workload alone, for profiling)
 """
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -42,6 +45,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 MFMA_PEAK_F16 = 2.5e15  # dense fp16, MI355X
+MODELS = {"7b": "llama_7b", "5b": "llama_5b", "600m": "llama_600m", "48m": "llama_48m"}
 HBM_PEAK = 8.0e12
 
 SEED = 1234
@@ -98,6 +102,9 @@ def main():
                     help="only the training forward + backward section (for profiling)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (timed) and a 1 GiB device copy, for counter runs")
+    ap.add_argument("--model", choices=sorted(MODELS), default="7b",
+                    help="shape of the main forward (default: the benchmark's 7B headline; the others "
+                         "are for profiling one workload alone, and skip the other prefill workloads)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -113,8 +120,9 @@ def main():
     stream = torch.cuda.Stream()  # default priority
     torch.cuda.set_stream(stream)
 
-    cfg = ModelConfig.llama_7b(seq=max(args.seq, 2048))
-    log(f"[bench] 7B-shape model: {cfg.param_count()/1e9:.3f}B params")
+    cfg = dataclasses.replace(getattr(ModelConfig, MODELS[args.model])(), seq=max(args.seq, 2048))
+    name = args.model.upper()
+    log(f"[bench] {name}-shape model: {cfg.param_count()/1e9:.3f}B params")
     k = CompiledKernels.compile(cfg)
     k.ctx.set_stream(stream.cuda_stream)
     t0 = time.time()
@@ -214,7 +222,7 @@ def main():
         log(f"[bench] prefill B=8: {ms8:.3f} ms, {extra['prefill_b8']}")
 
     # ---- the other prefill workloads ----
-    if not args.no_configs and B == 1 and S == 512:
+    if not args.no_configs and B == 1 and S == 512 and args.model == "7b":
         extra["prefill"] = bench_prefill_configs(k, cfg, stream, cpu=not args.no_cpu_baseline)
 
     # ---- decode ----
@@ -274,7 +282,7 @@ def main():
         extra["cpu_baseline"] = cpu_baseline(cfg, S)
 
     line = {
-        "metric": "prefill tok/s at 7B-shape seq512 fp16; decode tok/s + % of HBM peak",
+        "metric": f"prefill tok/s at {name}-shape seq{S} fp16; decode tok/s + % of HBM peak",
         "value": round(tok_s, 1),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -286,7 +294,8 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic (seeded N(0,0.02) weights, uniform tokens)",
-        "config": {"workload": "7B-shape prefill forward + CE (4096d/11008h/32L, 32x128 heads, vocab 32000)",
+        "config": {"workload": f"{name}-shape prefill forward + CE ({cfg.dim}d/{cfg.hidden}h/{cfg.nlayers}L, "
+                               f"{cfg.heads}x{cfg.hd} heads, vocab {cfg.vocab})",
                    "global_batch": B, "seq_len": S, "parallelism": "single-gpu",
                    "tflop_per_forward": round(flops / 1e12, 4),
                    "mfma_frac_whole_forward": round(flops / (ms_wall / 1e3) / MFMA_PEAK_F16, 4),
@@ -636,15 +645,15 @@ def cpu_forward_sample(cfg, B, S, whole_up_to_layers=20):
 
 
 def cpu_baseline(cfg, S):
-    """Headline CPU baseline: the fp32 oracle's 7B-shape forward at B=1 on this
-    host's CPU share (cpu_forward_sample: 1- and 2-layer stacks, 1 warmup +
-    median of 3 each, scaled to 32 layers)."""
+    """Headline CPU baseline: the fp32 oracle's forward of the main model at
+    B=1 on this host's CPU share (cpu_forward_sample: for the 7B shape 1- and
+    2-layer stacks, 1 warmup + median of 3 each, scaled to 32 layers)."""
     ctx = _threads_limited()
     try:
         t, note = cpu_forward_sample(cfg, 1, S)
         res = {"value": round(S / t, 2), "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
                "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
-               "sample": f"fp32 numpy oracle, 7B-shape forward at B=1 S={S}: {note}"}
+               "sample": f"fp32 numpy oracle, {cfg.nlayers}-layer {cfg.dim}d forward at B=1 S={S}: {note}"}
         log(f"[bench] cpu baseline: {res}")
         return res
     finally:
@@ -736,7 +745,8 @@ def bench_prefill_configs(k7, cfg7, stream, cpu=True):
         fl = fwd_flops(cfg, B, S)
         r = {"ms_per_forward": round(ms, 3), "tok_per_s": round(B * S / ms * 1e3, 1),
              "tflop_per_s": round(fl / ms / 1e9, 1), "mfma_frac": round(fl / (ms / 1e3) / MFMA_PEAK_F16, 4),
-             "tflop_per_forward": round(fl / 1e12, 3), "loss": round(float(dm.cpu()[0]), 5)}
+             "tflop_per_forward": round(fl / 1e12, 3), "loss": round(float(dm.cpu()[0]), 5),
+             "stages": bench_stages(k, cfg, dt, dg, B, S)}
         if cpu:
             lim = _threads_limited()
             try:
