@@ -62,7 +62,15 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
   const int qs = wave % PQ, kh = wave / PQ;
   const int nqb = (p.S + 31) / 32;
   const int ngr = (nqb + PQ - 1) / PQ;
-  const int gr = ngr - 1 - blockIdx.x;  // heaviest groups first
+  // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+  // L2. The remap gives each XCD a contiguous range of (group, head,
+  // sequence) in that order, so the groups that read one head's K and V run
+  // on one XCD and that XCD's L2 fetches them once, instead of every XCD
+  // fetching every head.
+  const int nwg = gridDim.x * gridDim.y * gridDim.z;
+  const int wg = xcd_remap(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), nwg);
+  const int gx = wg % gridDim.x, hy = (wg / gridDim.x) % gridDim.y, bz = wg / (gridDim.x * gridDim.y);
+  const int gr = ngr - 1 - gx;  // heaviest groups first within a head
   // group gr holds the query blocks gr, gr + ngr, gr + 2 ngr, ...: every
   // group spans the sequence, so the groups' causal work is nearly equal
   // (contiguous groups left most CUs idle behind the last one); the
@@ -70,7 +78,7 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
   const int qb = gr + ngr * qs;  // >= nqb: this wave has no queries
   const bool active = qb < nqb;
   const int nkb = gr + ngr * min(PQ - 1, (nqb - 1 - gr) / ngr) + 1;  // key blocks the group needs
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int h = hy, b = bz;
   const int kvh = h / (p.H / p.KVH);
   const int q0 = qb * 32;
   const int qi = q0 + li;
