@@ -548,8 +548,8 @@ def cpu_baseline_adam(n_params, sample=1 << 26):
 
 
 def cpu_threads():
-    """Host threads the CPU baselines use: this process's CPU share. A GPU box
-    allots each GPU a share of its host (OMP_NUM_THREADS, 16 per GPU there);
+    """Host threads the CPU baselines use: this process's CPU share. A
+    multi-GPU host may allot each GPU a share of its cores (OMP_NUM_THREADS);
     elsewhere every CPU this process may run on."""
     avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)

@@ -1,8 +1,8 @@
 """Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
 
 CPU: the oracle still reproduces its committed outputs (a regression guard on
-the checker itself). GPU: the device path meets the parity bars against the
-fixtures directly, without running the oracle on the box.
+the oracle itself). GPU: the device path meets the parity bars against the
+fixtures directly, without running the oracle on the GPU host.
 """
 import os
 
