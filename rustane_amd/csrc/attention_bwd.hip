@@ -40,8 +40,8 @@ namespace {
 HB_DEV void store_grad4(const AttnBwd& p, int b, int s, int col, int f0, f32x4 v, bool rope) {
   f32x4 o = v;
   if (rope) {
-    const float2* rp = p.rope + (size_t)(f0 >> 1) * p.rope_ld + s;
-    const float2 c0 = rp[0], c1 = rp[p.rope_ld];
+    const float4 r = p.rope[(size_t)(f0 >> 2) * p.rope_ld + s];  // f0 % 4 == 0
+    const float2 c0 = make_float2(r.x, r.y), c1 = make_float2(r.z, r.w);
     o.x = v.x * c0.x + v.y * c0.y;
     o.y = v.y * c0.x - v.x * c0.y;
     o.z = v.z * c1.x + v.w * c1.y;

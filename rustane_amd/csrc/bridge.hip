@@ -117,7 +117,7 @@ struct hb_model {
   f16* embed = nullptr;  // [vocab, dim]
   float* gamma_f = nullptr;
   bool embed_uploaded = false;
-  float2* rope = nullptr;
+  float4* rope = nullptr;  // RoPE table, [hd/4][rope_len] (ensure_rope)
   int rope_len = 0;
   float* staging = nullptr;
   size_t staging_floats = 0;
@@ -293,23 +293,27 @@ int validate_config(const hb_model_config& c) {
 
 // RoPE table exactly as kernels/sdpa_fwd.rs:18-33 computes it:
 // theta = p / base^(2i/hd) in f32; (cos, sin) per (i, p), stored pair-major
-// [hd/2][len] so that consecutive positions of one pair are adjacent (the
-// prefill GEMM epilogue reads one pair for 32 consecutive tokens at a time).
+// [hd/4][len] of float4 (cos, sin of pair 2q, cos, sin of pair 2q + 1): one
+// 16-byte load gives a lane the rotation of its 4 consecutive features, and
+// consecutive positions are adjacent (the prefill GEMM epilogue reads one
+// entry for 32 consecutive tokens at a time).
 int ensure_rope(hb_model* m, int len) {
   if (len <= m->rope_len) return HB_OK;
   const int half = m->cfg.hd / 2;
-  std::vector<float2> tab((size_t)len * half);
+  std::vector<float> tab((size_t)len * half * 2);
   for (int p = 0; p < len; ++p)
     for (int i = 0; i < half; ++i) {
       const float theta =
           (float)p / powf(m->cfg.rope_theta, 2.0f * (float)i / (float)m->cfg.hd);
-      tab[(size_t)i * len + p] = make_float2(cosf(theta), sinf(theta));
+      float* t = &tab[(((size_t)(i >> 1) * len + p) * 2 + (i & 1)) * 2];
+      t[0] = cosf(theta);
+      t[1] = sinf(theta);
     }
   HIP_TRY(hipStreamSynchronize(m->ctx->stream()));
   if (m->rope) HIP_TRY(hipFree(m->rope));
   m->rope = nullptr;
-  HIP_TRY(hipMalloc(&m->rope, tab.size() * sizeof(float2)));
-  HIP_TRY(hipMemcpy(m->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+  HIP_TRY(hipMalloc(&m->rope, tab.size() * sizeof(float)));
+  HIP_TRY(hipMemcpy(m->rope, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
   m->rope_len = len;
   m->graph_epoch++;  // captured decode graphs hold the old table address
   return HB_OK;

@@ -155,8 +155,8 @@ struct EpiLogits {
 // behind the previous ones: 7B QKV epilogue 9.5 us, 5B at 2048 tokens 39 us.
 struct EpiQKV {
   int q_dim, kv_dim, hd, S, heads, kv_heads;
-  const float2* rope;  // [hd/2][rope_ld] (cos, sin), pair-major
-  int rope_ld;         // positions per pair row
+  const float4* rope;  // [hd/4][rope_ld] (cos, sin of pair 2q, cos, sin of pair 2q+1)
+  int rope_ld;         // positions per row
   const int* d_pos;    // decode: position of the current token; prefill: NULL
   // Q: q[((b*heads + h)*q_rows + s)*hd + e]
   f16* q;
@@ -210,9 +210,9 @@ struct EpiQKV {
       pos_of<DEC>(t, b, s);
       const int fr = fb - region_start(fb);
       const int e = fr - div_hd.div(fr) * hd + (f0 - fb);
-      const float2* rp = rope + (size_t)(e >> 1) * rope_ld + s;
-      a.c0 = rp[0];
-      a.c1 = rp[rope_ld];
+      const float4 r = rope[(size_t)(e >> 2) * rope_ld + s];  // e % 4 == 0
+      a.c0 = make_float2(r.x, r.y);
+      a.c1 = make_float2(r.z, r.w);
     }
     return a;
   }

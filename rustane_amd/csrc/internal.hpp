@@ -159,7 +159,7 @@ struct AttnBwd {
   float scale;
   f16 *dqkv, *dqkvT;
   int ld, tld, q_dim, kv_dim;
-  const float2* rope;  // [hd/2][rope_ld]
+  const float4* rope;  // [hd/4][rope_ld], as EpiQKV::rope
   int rope_ld;
 };
 hipError_t attention_backward_fused(const AttnBwd& p, hipStream_t st);
