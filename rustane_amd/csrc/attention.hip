@@ -98,13 +98,31 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
   const size_t voff = ((size_t)b * p.KVH + kvh) * HD * p.vt_ld;
   const float sl2 = p.scale * HB_LOG2E;
 
-  // thread tid, load i covers 16-byte chunk x = i*256 + tid of the iteration's
-  // NKIND*PK tiles (K blocks, then V^T blocks, then their low parts)
+  // thread tid, load i covers 16-byte chunk x = i*NT + tid (NT = PW*64) of the
+  // iteration's NKIND*PK tiles (K blocks, then V^T blocks, then their low
+  // parts). NT and KT8 are powers of two, so x's tile is a constant of i, or
+  // of i and the wave when NT > KT8: written that way, the branches on the
+  // tile kind below are uniform (from tid alone the compiler made them
+  // divergent, with a wait in each).
+  constexpr int NT = PW * 64;
+  auto tile_of = [&](int i) {
+    if constexpr (NT <= KT8)
+      return (i * NT) / KT8;
+    else
+      return i * (NT / KT8) + (wave * 64) / KT8;
+  };
+  auto y_of = [&](int i) {
+    if constexpr (NT <= KT8)
+      return (i * NT) % KT8 + tid;
+    else
+      return tid % KT8;
+  };
+  static_assert(NT <= KT8 ? KT8 % NT == 0 : NT % KT8 == 0, "tiles and threads nest");
   f16x8 kvreg[NLD];
   auto gload = [&](int n) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int x = i * PW * 64 + tid, tile = x / KT8, y = x % KT8;
+      const int tile = tile_of(i), y = y_of(i);
       const int kind = tile / PK;  // 0 K, 1 V^T, 2 K low, 3 V^T low
       const int kb = min(n * PK + (tile % PK), nkb - 1);
       if ((kind & 1) == 0) {
@@ -120,7 +138,7 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
   auto lstore = [&]() {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int x = i * PW * 64 + tid, tile = x / KT8, y = x % KT8;
+      const int tile = tile_of(i), y = y_of(i);
       if (((tile / PK) & 1) == 0) {
         const int r = y / NCH, c = y % NCH;
         s_kv[tile * KT8 + r * NCH + (c ^ (swap23(r) % NCH))] = kvreg[i];
