@@ -169,17 +169,23 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
     const int kb = n * PK + kh;
     if (!active || kb > qb) continue;  // wave-uniform
 
+    // all of the block's K fragments are read before the score MFMAs, so
+    // the LDS reads overlap instead of each waiting in front of its MFMA
     f32x16 s = {};
+    f16x8 kf[KS];
+#pragma unroll
+    for (int j = 0; j < KS; ++j) kf[j] = sk[krow * NCH + ((2 * j + h2) ^ (li % NCH))];
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      const int ko = krow * NCH + ((2 * j + h2) ^ (li % NCH));
-      const f16x8 kf = sk[ko];
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[j], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[j], qf[j], s, 0, 0, 0);
       if constexpr (SPLIT) {
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[j], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(skl[ko], qf[j], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[j], ql[j], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(skl[krow * NCH + ((2 * j + h2) ^ (li % NCH))], qf[j], s, 0,
+                                                   0, 0);
       }
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, SPLIT ? 2 * KS : KS, 0);  // the K fragment reads,
+    __builtin_amdgcn_sched_group_barrier(0x008, SPLIT ? 3 * KS : KS, 0);  // then the score MFMAs
     float mloc = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] *= sl2;
@@ -205,9 +211,13 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
         for (int r = 0; r < 16; ++r) o[m][r] *= corr;
       mrun = mnew;
     }
+    // v_exp_f32 itself: the arguments are <= 8, and a result below 2^-126
+    // (where exp2f would return a denormal) is 0 once rounded to fp16 and
+    // vanishes in lrun, which is >= 1 -- the same output bits, without
+    // exp2f's denormal range scaling (5 more instructions per probability)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float e = exp2f(s[r] - mrun);
+      const float e = __builtin_amdgcn_exp2f(s[r] - mrun);
       s[r] = e;
       lrun += e;  // this lane's keys; the lane pair is summed after the loop
     }
