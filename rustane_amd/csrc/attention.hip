@@ -186,9 +186,10 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
     }
     __builtin_amdgcn_sched_group_barrier(0x100, SPLIT ? 2 * KS : KS, 0);  // the K fragment reads,
     __builtin_amdgcn_sched_group_barrier(0x008, SPLIT ? 3 * KS : KS, 0);  // then the score MFMAs
+    // Scores stay unscaled here: the block maximum is scaled once (rounding
+    // is monotonic, so that is the maximum of the scaled scores) and the
+    // scale enters each exponent through one fma.
     float mloc = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] *= sl2;
     if (kb == qb) {  // diagonal block: keys after the query are masked
 #pragma unroll
       for (int r = 0; r < 16; ++r)
@@ -196,7 +197,10 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    {  // the lane pair (l, l ^ 32): swapping the wave's halves in registers
+      const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+      mloc = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1])) * sl2;
+    }
     // The reference max mrun is only raised when a score exceeds it by more
     // than 2^8 (log2 units): probabilities stay <= 256 (exact in fp16 to the
     // same relative precision) and the final 1/l cancels the common scale,
@@ -217,7 +221,7 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
     // exp2f's denormal range scaling (5 more instructions per probability)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float e = __builtin_amdgcn_exp2f(s[r] - mrun);
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], sl2, -mrun));
       s[r] = e;
       lrun += e;  // this lane's keys; the lane pair is summed after the loop
     }
