@@ -445,16 +445,14 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(AttnDecode p) {
       float d = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) d += qf[e] * kval(i, e);
-#pragma unroll
-      for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+      d = group_sum<LPK>(d);
       sc[i] = (kbase + i * STRIPE < cend) ? d * sl2 : -INFINITY;
     }
     // wave-wide max over this block's keys (lanes of a group hold equal scores)
     float mb = sc[0];
 #pragma unroll
     for (int i = 1; i < NIT; ++i) mb = fmaxf(mb, sc[i]);
-#pragma unroll
-    for (int o = LPK; o < 64; o <<= 1) mb = fmaxf(mb, __shfl_xor(mb, o, 64));
+    mb = fold_groups<LPK>(mb, [](float a, float c) { return fmaxf(a, c); });
     const float mn = fmaxf(m, mb);
     if (mn != -INFINITY) {
       if (m != mn) {  // rescale what earlier blocks left (nothing on the first)
@@ -469,7 +467,11 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(AttnDecode p) {
         if constexpr (SPLIT) load_v(i0);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-          const float pk = exp2f(sc[i0 + i] - m);
+          // v_exp_f32 itself: pk <= 1, and a pk below 2^-126 (where exp2f
+          // would return a denormal) vanishes once the lanes' sums meet the
+          // maximum key's (pk = 1), so exp2f's denormal scaling changes no
+          // result
+          const float pk = __builtin_amdgcn_exp2f(sc[i0 + i] - m);
           l += pk;
 #pragma unroll
           for (int e = 0; e < 8; ++e)
@@ -478,11 +480,11 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(AttnDecode p) {
       }
     }
   }
+  {
+    const auto add = [](float a, float c) { return a + c; };
+    l = fold_groups<LPK>(l, add);
 #pragma unroll
-  for (int o = LPK; o < 64; o <<= 1) {
-    l += __shfl_xor(l, o, 64);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+    for (int e = 0; e < 8; ++e) acc[e] = fold_groups<LPK>(acc[e], add);
   }
   if (lane == 0) {
     s_m[wave] = m;

@@ -68,6 +68,48 @@ HB_DEV float wave_max(float v) {
   return v;
 }
 
+// Cross-lane steps in registers, without an LDS permute and its wait.
+// dpp_f: a DPP lane permutation within each 16-lane row. group_sum<N>: the
+// sum over each aligned group of N = 8 or 16 lanes, equal in every lane of
+// the group (lane ^ 1, lane ^ 2, then the mirror image in the 8 and the 16,
+// which meet the other quad / half once each quad / half is uniform).
+// xor16_op / xor32_op: op(v[l], v[l ^ 16]) (or ^ 32) in every lane.
+// v_permlane{16,32}_swap exchanges 16- or 32-lane halves of the wave between
+// two registers; swapping two copies of v leaves one half of each pair
+// broadcast in each register, and op commutes, so lane and partner agree.
+template <int CTRL>
+HB_DEV float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int N>
+HB_DEV float group_sum(float v) {
+  static_assert(N == 8 || N == 16, "groups of 8 or 16 lanes");
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  if constexpr (N == 16) v += dpp_f<0x140>(v);  // row_mirror
+  return v;
+}
+template <class Op>
+HB_DEV float xor16_op(float v, Op op) {
+  const auto h = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(h[0]), __uint_as_float(h[1]));
+}
+template <class Op>
+HB_DEV float xor32_op(float v, Op op) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(h[0]), __uint_as_float(h[1]));
+}
+// op over the lanes l, l ^ G, l ^ 2G, ... (G = 8 or 16): combines the
+// groups of G lanes position by position, in every lane.
+template <int G, class Op>
+HB_DEV float fold_groups(float v, Op op) {
+  static_assert(G == 8 || G == 16, "groups of 8 or 16 lanes");
+  if constexpr (G == 8) v = op(v, dpp_f<0x128>(v));  // row_ror:8, lane ^ 8 within the row
+  v = xor16_op(v, op);
+  return xor32_op(v, op);
+}
+
 // Block-wide reduction through LDS; `red` holds one float per wave.
 template <int NWAVES>
 HB_DEV float block_sum(float v, float* red) {
