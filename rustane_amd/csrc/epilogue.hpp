@@ -311,6 +311,48 @@ struct EpiQKVAt : EpiQKV {
   EpiQKVAt() = default;
   __host__ explicit EpiQKVAt(const EpiQKV& e) : EpiQKV(e) {}
   HB_DEV Aux load(int t, int f0, int fb) const { return load_at<DECODE>(t, f0, fb); }
+  // Prefill tiles stage the RoPE rows of their TT tokens into LDS (the
+  // GEMM's EpiStage): table entry q of token t0 + j goes to lo[q * TT + j]
+  // for q < hd/8 and to hi[(q - hd/8) * TT + j] above. Thread tid keeps
+  // token j = tid % TT (one position) and copies rows q = tid / TT,
+  // + NT/TT, ... in batches of 8 loads; tiles of V features only need none.
+  static constexpr bool kStage = !DECODE;
+  template <int TT, int NT>
+  HB_DEV void stage(float4* lo, float4* hi, int t0, int f_base, int tid) const {
+    static_assert(NT % TT == 0, "whole tokens per thread pass");
+    if (f_base >= q_dim + kv_dim) return;  // uniform over the workgroup
+    constexpr int QS = NT / TT;  // rows per pass
+    const int j = tid % TT, nq = hd >> 2, half = hd >> 3;
+    int b, s;
+    pos_of<false>(t0 + j, b, s);  // a token past T still maps into [0, S)
+    const float4* src = rope + s;
+    for (int q0 = tid / TT; q0 < nq; q0 += 8 * QS) {
+      float4 r0, r1, r2, r3, r4, r5, r6, r7;
+      auto ld = [&](int k, float4& r) {
+        if (q0 + k * QS < nq) r = src[(size_t)(q0 + k * QS) * rope_ld];
+      };
+      auto st = [&](int k, const float4& r) {
+        const int q = q0 + k * QS;
+        if (q < nq) (q < half ? lo + q * TT : hi + (q - half) * TT)[j] = r;
+      };
+      ld(0, r0), ld(1, r1), ld(2, r2), ld(3, r3), ld(4, r4), ld(5, r5), ld(6, r6), ld(7, r7);
+      st(0, r0), st(1, r1), st(2, r2), st(3, r3), st(4, r4), st(5, r5), st(6, r6), st(7, r7);
+    }
+  }
+  // load_at from the staged rows, token t0 + j
+  HB_DEV Aux load_staged(const float4* lo, const float4* hi, int j, int tt, int f0, int fb) const {
+    Aux a{};
+    if (fb < q_dim + kv_dim) {
+      const int fr = fb - region_start(fb);
+      const int e = fr - div_hd.div(fr) * hd + (f0 - fb), q = e >> 2, half = hd >> 3;
+      // the 8 rows of one accumulator row's quads start at a multiple of 8:
+      // the half is wave-uniform
+      const float4 r = (q < half ? lo + q * tt : hi + (q - half) * tt)[j];
+      a.c0 = make_float2(r.x, r.y);
+      a.c1 = make_float2(r.z, r.w);
+    }
+    return a;
+  }
   HB_DEV void operator()(int t, int f0, f32x4 v4, const Aux& a, int fb) const {
     store_at<DECODE, MODE>(t, f0, v4, a, fb);
   }

@@ -48,6 +48,16 @@ struct EpiAux<E, std::void_t<typename E::Aux>> {
   }
 };
 
+// Epilogues with kStage copy a table the epilogue reads into the operand
+// LDS once the main loop is done -- `stage<TT, NT>(lo, hi, t_base, f_base,
+// tid)` by all threads, then `load_staged(lo, hi, t - t_base, TT, f0, fb)` in
+// place of load() -- so that the epilogue's operand reads wait on LDS
+// instead of behind its own global stores (one counter covers both).
+template <class E, class = void>
+struct EpiStage : std::false_type {};
+template <class E>
+struct EpiStage<E, std::void_t<decltype(E::kStage)>> : std::bool_constant<E::kStage> {};
+
 // Epilogues with kSumSq return the sum of squares of the four values they
 // stored; the kernel adds them up per workgroup and writes the total to
 // epi.sq_out[tile] (one slot per output tile, fixed order for the reader).
@@ -242,6 +252,14 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   using AuxT = typename AX::type;
   constexpr bool HOIST =
       !std::is_empty_v<AuxT> && FM * TM * 4 * sizeof(AuxT) <= 96 * 4 && FT * TT >= 192 * 128;
+  // a staged table of up to 32 float4 per token (hd <= 128) fits in the
+  // operand LDS, its first half in sW (16*FT float4) and its second in sX
+  // (16*TT), when TT <= FT; staged on the 256-feature tiles, whose long
+  // epilogues gain (7B QKV at 4096 tokens 424 -> 392 us, 5B at 2048 tokens
+  // 105 -> 100 us), not on 128x128 (600M QKV 25.6 -> 26.6 us)
+  constexpr bool STAGE = EpiStage<Epi>::value && !HOIST && TT <= FT && FT == 256;
+  float4* const stab_lo = reinterpret_cast<float4*>(&sW[0][0]);
+  float4* const stab_hi = reinterpret_cast<float4*>(&sX[0][0]);
   AuxT aux[HOIST ? FM : 2][TM * 4];
   auto tok = [&](int j) { return t_base + wt * WTT + j * 32 + (lane & 31); };
   auto fblk = [&](int i) { return f_base + wf * WFT + i * 32; };  // wave-uniform
@@ -251,7 +269,12 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
     static_for<0, TM * 4>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       const int t = tok(q / 4), f = feat(i, q % 4);
-      if (t < T && f < N) aux[HOIST ? i : (i & 1)][q] = AX::load(epi, t, f, fblk(i));
+      if constexpr (STAGE) {
+        if (t < T && f < N)
+          aux[HOIST ? i : (i & 1)][q] = epi.load_staged(stab_lo, stab_hi, t - t_base, TT, f, fblk(i));
+      } else {
+        if (t < T && f < N) aux[HOIST ? i : (i & 1)][q] = AX::load(epi, t, f, fblk(i));
+      }
     });
   };
   if constexpr (HOIST) static_for<0, FM>([&](auto ic) { load_row(ic); });
@@ -267,6 +290,10 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
     iter(R1{}, kt + 1);
   }
   if (kt < nk) iter(R0{}, kt);
+  if constexpr (STAGE) {  // the main loop ended on a barrier: the operand LDS is free
+    epi.template stage<TT, NT>(stab_lo, stab_hi, t_base, f_base, tid);
+    __syncthreads();
+  }
 
   // Epilogue over the FM x TM x 4 accumulator quads as straight-line code: a
   // loop would be left rolled once the epilogue body is large (EpiQKV on
