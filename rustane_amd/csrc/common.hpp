@@ -145,10 +145,10 @@ HB_DEV int xcd_remap(int wg, int n) {
   return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
 }
 
-// silu(x) = x * sigmoid(x), the sigmoid through v_rcp_f32 (1 ulp) instead
-// of the ~10-instruction IEEE division: the gate it feeds is rounded to
-// fp16 (11 bits) right after.
-HB_DEV float silu_f(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+// silu(x) = x * sigmoid(x). The sigmoid keeps the IEEE division: through
+// v_rcp_f32 (1 ulp) it made the 7B B=8 FFN-up GEMM 1% faster but moved the
+// pooled top-1 agreement with the oracle from 99.62% to 99.57%.
+HB_DEV float silu_f(float x) { return x * (1.0f / (1.0f + __expf(-x))); }
 
 // Two-term fp16 form of fp32 values, for the operands that must carry more
 // than fp16's 11 significant bits into an MFMA: x ~ hi + lo with hi = fp16(x)
