@@ -188,6 +188,44 @@ def test_layer_ops_match_oracle(tiny):
     np.testing.assert_allclose(dnext.cpu().numpy(), x2d + oc.alpha() * ffn, atol=1e-4)
 
 
+def test_sdpa_op_on_staged_rope_tiles_spanning_sequences(gpu):
+    """sdpaFwd for 3 sequences of 700 tokens on a 2048d / 16x128 model: the
+    QKV GEMM then runs 256x256 tiles (216 of them, the launcher's choice for
+    N = 6144, T = 2100), which copy their RoPE table slice into LDS per tile
+    and read it from there. 700 is not a multiple of 256, so tiles hold the
+    end of one sequence and the start of the next: each staged token must
+    get its own position. Every sequence is checked against the oracle run
+    alone."""
+    import torch
+    cfg = tiny_config(dim=2048, hidden=256, heads=16, hd=128, nlayers=1, seq=700, vocab=256)
+    k = CompiledKernels.compile(cfg)
+    k.ctx.set_stream(gpu.stream())
+    w = ModelWeights.synthetic(cfg, seed=77, std=0.02)
+    k.ensure_weights(w)
+    oc = oracle_cfg(cfg)
+    lw = oracle_weights(w).layers[0]
+    B, S = 3, cfg.seq
+    xn = f16_round(np.random.default_rng(11).standard_normal((B * S, cfg.dim)) * 0.5)
+    dxn = to_dev(xn, torch.float16)
+    dattn = torch.empty((B * S, cfg.q_dim), dtype=torch.float16, device="cuda")
+    tap = torch.empty((B * S, cfg.q_dim + 2 * cfg.kv_dim), device="cuda")
+    hb.call("hb_op_sdpa_fwd", k.model.handle, 0, dxn.data_ptr(), B, S, dattn.data_ptr(), tap.data_ptr())
+    torch.cuda.synchronize()
+    t, attn = tap.cpu().numpy(), dattn.float().cpu().numpy()
+    q, kv = cfg.q_dim, cfg.kv_dim
+    for b in range(B):
+        rows = slice(b * S, (b + 1) * S)
+        s = O.sdpa_fwd(oc, xn[rows].T, f16_round(lw.wq), f16_round(lw.wk), f16_round(lw.wv), S)
+        print(f"sequence {b}: max|dq| {np.abs(t[rows, :q] - s['q_rope'].T).max():.2e} "
+              f"max|dattn| {np.abs(attn[rows] - s['attn'].T).max():.2e}", flush=True)
+        np.testing.assert_allclose(t[rows, :q], s["q_rope"].T, atol=2e-3)
+        np.testing.assert_allclose(t[rows, q:q + kv], s["k_rope"].T, atol=2e-3)
+        np.testing.assert_allclose(t[rows, q + kv:], s["v"].T, atol=2e-3)
+        np.testing.assert_allclose(attn[rows], s["attn"].T, atol=3e-3)
+    k.model.close()
+    k.ctx.close()
+
+
 def test_logits_ce_op_matches_oracle(tiny):
     import torch
     cfg, k, w = tiny
