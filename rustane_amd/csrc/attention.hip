@@ -199,10 +199,8 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
-    {  // the lane pair (l, l ^ 32): swapping the wave's halves in registers
-      const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
-      mloc = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
-    }
+    // the lane pair (l, l ^ 32), in registers (common.hpp)
+    mloc = xor32_op(mloc, [](float x, float y) { return fmaxf(x, y); });
     // The reference max mrun is only raised when a score exceeds it by more
     // than 2^8 (log2 units): probabilities stay <= 256 (exact in fp16 to the
     // same relative precision) and the final 1/l cancels the common scale,
@@ -219,8 +217,9 @@ __global__ __launch_bounds__(PQ * PK * 64, (SPLIT || PK == 1) ? 1 : 2) void attn
     }
     // v_exp_f32 itself: the arguments are <= 8, and a result below 2^-126
     // (where exp2f would return a denormal) is 0 once rounded to fp16 and
-    // vanishes in lrun, which is >= 1 -- the same output bits, without
-    // exp2f's denormal range scaling (5 more instructions per probability)
+    // vanishes in the query's sum l (>= 1: the lane pair holds the key of
+    // the maximum) -- the same output bits, without exp2f's denormal range
+    // scaling (5 more instructions per probability)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float e = __builtin_amdgcn_exp2f(s[r] - mrun);

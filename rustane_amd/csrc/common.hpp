@@ -56,7 +56,9 @@ HB_DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Wave-wide reductions (64 lanes). __shfl_xor lowers to DPP / ds_swizzle.
+// Wave-wide reductions (64 lanes). __shfl_xor lowers to an LDS permute
+// (ds_bpermute) and its wait; the register forms below avoid that in inner
+// loops.
 HB_DEV float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
