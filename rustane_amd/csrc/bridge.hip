@@ -2060,7 +2060,7 @@ static int forward_enqueue(hb_model* m, const uint32_t* d_tokens, const uint32_t
   HB_MARK(tm, ST_LOGITS);
   if (d_targets) {
     float* loss = d_loss ? d_loss : w.loss;
-    HIP_TRY(cross_entropy(logits, d_targets, (int)T, c.vocab, loss, nullptr, m->ctx->d_err, st));
+    HIP_TRY(cross_entropy(logits, d_targets, (int)T, c.vocab, loss, m->ctx->d_err, st));
     if (d_mean) HIP_TRY(mean_reduce(loss, (int)T, d_mean, st));
     HB_MARK(tm, ST_CE);
   }
@@ -2308,7 +2308,7 @@ extern "C" int hb_op_logits_ce(hb_model* m, const void* xf, const uint32_t* targ
   hipStream_t st = m->ctx->stream();
   HIP_TRY(gemm_logits(m->embed, (const f16*)xf, c.vocab, T, c.dim, EpiLogits{logits, c.vocab, c.softcap}, st));
   if (targets && losses)
-    HIP_TRY(cross_entropy(logits, targets, T, c.vocab, losses, nullptr, m->ctx->d_err, st));
+    HIP_TRY(cross_entropy(logits, targets, T, c.vocab, losses, m->ctx->d_err, st));
   return HB_OK;
 }
 
@@ -2879,7 +2879,7 @@ int train_forward(hb_model* m, int B, int S) {
   }
   HIP_TRY(rmsnorm(ts->xL, c.dim, m->gamma_f, T, c.dim, c.norm_eps, ts->xf, nullptr, st));
   HIP_TRY(gemm_logits(m->embed, ts->xf, c.vocab, T, c.dim, EpiLogits{ts->logits, c.vocab, ts->softcap}, st));
-  HIP_TRY(cross_entropy(ts->logits, ts->tgt, T, c.vocab, ts->loss, nullptr, m->ctx->d_err, st));
+  HIP_TRY(cross_entropy(ts->logits, ts->tgt, T, c.vocab, ts->loss, m->ctx->d_err, st));
   HIP_TRY(mean_reduce(ts->loss, T, ts->mean, st));
   return HB_OK;
 }

@@ -122,26 +122,17 @@ hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, i
   return hipGetLastError();
 }
 
-// ---- cross-entropy + argmax (cpu/cross_entropy.rs:13-38, 58-96) ------------------
-// One workgroup per row, one pass over the logits: each thread keeps a running
-// (max, sum of exp(x - max)) pair and the first index of its maximum; pairs are
-// merged across the block. loss = ln(sum) - (x[y] - max).
+// ---- cross-entropy (cpu/cross_entropy.rs:13-38, 58-96) ---------------------------
+// One workgroup per row, one pass over the logits. Each thread takes its
+// elements (4 consecutive per 1024) in batches of 8 float4 whose loads are
+// issued together, raises its running maximum m once per batch (rescaling its
+// sum of exp(x - m) then) and adds the batch's terms. The (m, sum) pairs are
+// merged across the wave (LDS permutes) and across the 4 waves in LDS;
+// loss = ln(sum) - (x[y] - max). The earlier form, one dependent load and
+// branchy update per float4, took 29 us for 512 rows of 32000.
 struct SoftState {
-  float m, s, best;
-  int idx;
+  float m, s;
 };
-HB_DEV void soft_push(SoftState& st, float x, int i) {
-  if (x > st.m) {
-    st.s = st.s * exp2f((st.m - x) * HB_LOG2E) + 1.0f;
-    st.m = x;
-  } else {
-    st.s += exp2f((x - st.m) * HB_LOG2E);
-  }
-  if (x > st.best || (x == st.best && i < st.idx)) {
-    st.best = x;
-    st.idx = i;
-  }
-}
 HB_DEV void soft_merge(SoftState& a, const SoftState& b) {
   const float m = fmaxf(a.m, b.m);
   float s = 0.f;
@@ -149,41 +140,51 @@ HB_DEV void soft_merge(SoftState& a, const SoftState& b) {
   if (b.m != -INFINITY) s += b.s * exp2f((b.m - m) * HB_LOG2E);
   a.m = m;
   a.s = s;
-  if (b.best > a.best || (b.best == a.best && b.idx < a.idx)) {
-    a.best = b.best;
-    a.idx = b.idx;
-  }
 }
 
 __global__ __launch_bounds__(256) void cross_entropy_kernel(const float* __restrict__ logits,
                                                             const uint32_t* __restrict__ targets,
                                                             int vocab, float* __restrict__ loss,
-                                                            uint32_t* __restrict__ argmax,
                                                             int* err) {
-  __shared__ SoftState red[256];
-  const int t = blockIdx.x;
+  constexpr int NB = 8;  // float4 per thread and batch
+  __shared__ SoftState red[4];
+  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float* row = logits + (size_t)t * vocab;
-  SoftState st{-INFINITY, 0.f, -INFINITY, 0x7fffffff};
-  for (int c = threadIdx.x * 4; c < vocab; c += 1024) {
-    const f32x4 v = *(const f32x4*)(row + c);
-    soft_push(st, v.x, c);
-    soft_push(st, v.y, c + 1);
-    soft_push(st, v.z, c + 2);
-    soft_push(st, v.w, c + 3);
-  }
-  red[threadIdx.x] = st;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) {
-      SoftState a = red[threadIdx.x];
-      soft_merge(a, red[threadIdx.x + o]);
-      red[threadIdx.x] = a;
+  SoftState st{-INFINITY, 0.f};
+  for (int c0 = threadIdx.x * 4; c0 < vocab; c0 += NB * 1024) {
+    f32x4 v[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int c = c0 + i * 1024;
+      v[i] = c < vocab ? *(const f32x4*)(row + c) : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     }
-    __syncthreads();
+    float bm = -INFINITY;  // c0 < vocab: v[0] holds real logits
+#pragma unroll
+    for (int i = 0; i < NB; ++i) bm = fmaxf(bm, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    if (bm > st.m) {
+      st.s *= exp2f((st.m - bm) * HB_LOG2E);  // 0 while st.m is -inf
+      st.m = bm;
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      acc += (exp2f((v[i].x - st.m) * HB_LOG2E) + exp2f((v[i].y - st.m) * HB_LOG2E)) +
+             (exp2f((v[i].z - st.m) * HB_LOG2E) + exp2f((v[i].w - st.m) * HB_LOG2E));
+    st.s += acc;
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    SoftState b;
+    b.m = __shfl_xor(st.m, o, 64);
+    b.s = __shfl_xor(st.s, o, 64);
+    soft_merge(st, b);
+  }
+  if (lane == 0) red[wave] = st;
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const SoftState r = red[0];
-    if (argmax) argmax[t] = (uint32_t)r.idx;
+    SoftState r = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) soft_merge(r, red[w]);
     if (loss && targets) {
       const uint32_t y = targets[t];
       if (y < (uint32_t)vocab) {
@@ -197,10 +198,10 @@ __global__ __launch_bounds__(256) void cross_entropy_kernel(const float* __restr
 }
 
 hipError_t cross_entropy(const float* logits, const uint32_t* targets, int T, int vocab,
-                         float* loss, uint32_t* argmax, int* err, hipStream_t st) {
+                         float* loss, int* err, hipStream_t st) {
   if (T <= 0) return hipSuccess;
   hipLaunchKernelGGL(cross_entropy_kernel, dim3(T), dim3(256), 0, st, logits, targets, vocab, loss,
-                     argmax, err);
+                     err);
   return hipGetLastError();
 }
 

@@ -208,9 +208,9 @@ hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int voca
 // EpiSwiGLU::frag) instead of rows.
 hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, int dim, float eps,
                    f16* out, float* rms_inv, hipStream_t st, bool split = false, bool frag = false);
-// Per-row cross-entropy (targets nullable) and argmax (nullable).
+// Per-row cross-entropy against targets (ids >= vocab: NaN loss, error bit 2).
 hipError_t cross_entropy(const float* logits, const uint32_t* targets, int T, int vocab,
-                         float* loss, uint32_t* argmax, int* err, hipStream_t st);
+                         float* loss, int* err, hipStream_t st);
 hipError_t mean_reduce(const float* v, int n, float* out, hipStream_t st);
 hipError_t set_int(int* d, int value, hipStream_t st);
 

@@ -246,6 +246,40 @@ def test_logits_ce_op_matches_oracle(tiny):
     np.testing.assert_allclose(dloss.cpu().numpy(), losses, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("vocab", [8192, 32000])
+def test_cross_entropy_wide_vocab_matches_oracle(gpu, vocab):
+    """Cross-entropy at the workloads' vocabulary sizes: each thread walks its
+    row in batches of 8 float4 (32000 = 31.25 x 1024: the last batch is
+    partial) and raises its running maximum between batches. Rows range from
+    all-zero logits (loss = ln(vocab)) to logits of std ~30 (a few terms carry
+    the sum); losses against the oracle's on the device's own logits."""
+    import torch
+    cfg = tiny_config(dim=64, hidden=64, heads=1, nlayers=1, vocab=vocab)
+    k = CompiledKernels.compile(cfg)
+    k.ctx.set_stream(gpu.stream())
+    w = ModelWeights.synthetic(cfg, seed=11, std=0.02)
+    k.ensure_weights(w)
+    T = 48
+    rng = np.random.default_rng(9)
+    scale = np.array([0.0] * 4 + [1.0] * 12 + [30.0] * 16 + [200.0] * 16, F32)[:, None]
+    xf = f16_round(rng.standard_normal((T, cfg.dim)) * scale)
+    tgt = rng.integers(0, vocab, T).astype(np.uint32)
+    tgt[-1] = vocab - 1
+    dl = torch.empty((T, vocab), device="cuda")
+    dloss = torch.empty(T, device="cuda")
+    dxf, dtgt = to_dev(xf, torch.float16), to_dev(tgt)
+    hb.call("hb_op_logits_ce", k.model.handle, dxf.data_ptr(), dtgt.data_ptr(), T, dl.data_ptr(),
+            dloss.data_ptr())
+    torch.cuda.synchronize()
+    got = dloss.cpu().numpy()
+    _, ref = O.cross_entropy_batch(dl.cpu().numpy(), tgt, vocab)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(got[:4], np.log(vocab), rtol=1e-6)
+    assert np.isfinite(got).all()
+    k.model.close()
+    k.ctx.close()
+
+
 @pytest.mark.parametrize("T", [128, 200])
 def test_residual_gemm_split_k_matches_float64(gpu, T):
     """Wo of a 2048-wide model at <= 256 tokens has few output tiles and a long
