@@ -356,6 +356,57 @@ struct EpiQKVAt : EpiQKV {
   HB_DEV void operator()(int t, int f0, f32x4 v4, const Aux& a, int fb) const {
     store_at<DECODE, MODE>(t, f0, v4, a, fb);
   }
+  // Prefill PLAIN through the GEMM's EpiRows: (b, s) once per token, the
+  // row pointer of (Q/K/V region, head, b, s) once per 32-feature block and
+  // token, then per quad only the feature offset -- the same stores as
+  // store_at (QKV GEMM at 512 tokens: the per-quad division and 64-bit
+  // address arithmetic were ~4 us of its ~61 us).
+  static constexpr bool kRows = !DECODE && MODE == PLAIN;
+  struct Tok {
+    int b, s;
+  };
+  struct Row {
+    f16* p;   // row (b, s) of head h in the block's region (Q, K or V), at feature 0
+    f16* pt;  // column s of head h in V^T (V region)
+    int e0;   // feature of fb within its head
+  };
+  HB_DEV Tok tok(int t) const {
+    Tok r;
+    pos_of<false>(t, r.b, r.s);
+    return r;
+  }
+  HB_DEV Row row(const Tok& tk, int fb) const {
+    const int r0 = region_start(fb), fr = fb - r0, h = div_hd.div(fr);
+    Row r{nullptr, nullptr, fr - h * hd};
+    if (r0 == 0) {
+      r.p = q + ((size_t)tk.b * heads + h) * q_rows * hd + (size_t)tk.s * hd;
+    } else if (r0 == q_dim) {
+      r.p = k + tk.b * k_bstride + h * k_hstride + (size_t)tk.s * hd;
+    } else {
+      if (v) r.p = v + tk.b * v_bstride + h * v_hstride + (size_t)tk.s * hd;
+      if (vt) r.pt = vt + ((size_t)tk.b * kv_heads + h) * hd * vt_ld + tk.s;
+    }
+    return r;
+  }
+  HB_DEV void store_row(const Row& r, int f0, f32x4 v4, const Aux& a, int fb) const {
+    const int r0 = region_start(fb), e = r.e0 + (f0 - fb);
+    f32x4 o = v4;
+    if (r0 < q_dim + kv_dim) {  // as store_at
+      o.x = v4.x * a.c0.x - v4.y * a.c0.y;
+      o.y = v4.y * a.c0.x + v4.x * a.c0.y;
+      o.z = v4.z * a.c1.x - v4.w * a.c1.y;
+      o.w = v4.w * a.c1.x + v4.z * a.c1.y;
+    }
+    const f16x4 oh = f16x4_hi(o);
+    if (r0 < q_dim + kv_dim || v) *(f16x4*)(r.p + e) = oh;
+    if (r0 == q_dim + kv_dim && vt) {
+      f16* p = r.pt + (size_t)e * vt_ld;
+      p[0] = oh.x;
+      p[vt_ld] = oh.y;
+      p[2 * vt_ld] = oh.z;
+      p[3 * vt_ld] = oh.w;
+    }
+  }
   HB_DEV Aux load(int t, int f0) const { return load(t, f0, f0 & ~31); }
   HB_DEV void operator()(int t, int f0, f32x4 v4) const { (*this)(t, f0, v4, load(t, f0), f0 & ~31); }
 };

@@ -58,6 +58,19 @@ struct EpiStage : std::false_type {};
 template <class E>
 struct EpiStage<E, std::void_t<decltype(E::kStage)>> : std::bool_constant<E::kStage> {};
 
+// Epilogues with `Tok tok(t)`, `row(tok, fb)` and `store_row(row, f0, v, aux,
+// fb)` can split their output addressing: tok() once per token of a lane, row()
+// once per (32-feature block, token), store_row() per quad.
+// Selected by `kRows`.
+template <class E, class = void>
+struct EpiRows : std::false_type {
+  struct Tok {};
+};
+template <class E>
+struct EpiRows<E, std::enable_if_t<E::kRows>> : std::true_type {
+  using Tok = typename E::Tok;
+};
+
 // Epilogues with kSumSq return the sum of squares of the four values they
 // stored; the kernel adds them up per workgroup and writes the total to
 // epi.sq_out[tile] (one slot per output tile, fixed order for the reader).
@@ -304,26 +317,52 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   // cannot be moved above stores that might alias them, so a load-store-load
   // chain per quad would expose the load latency once per quad.
   if constexpr (!HOIST) load_row(std::integral_constant<int, 0>{});
+  // EpiRows: the token part of the output addresses once per token, the
+  // (feature block, token) part once per 4 quads, both outside the quads'
+  // bounds tests (they read no memory)
+  constexpr bool ROWS = EpiRows<Epi>::value;
+  static_assert(!ROWS || !EpiSumSq<Epi>::value, "row-addressed epilogues return nothing");
+  typename EpiRows<Epi>::Tok tkj[ROWS ? TM : 1];
+  if constexpr (ROWS) static_for<0, TM>([&](auto jc) { tkj[decltype(jc)::value] = epi.tok(tok(decltype(jc)::value)); });
   float lane_sq = 0.f;
   static_for<0, FM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     if constexpr (!HOIST && i + 1 < FM) load_row(std::integral_constant<int, i + 1>{});
-    static_for<0, TM * 4>([&](auto qc) {
-      constexpr int q = decltype(qc)::value;
-      constexpr int j = q / 4, g = q % 4;
-      const int t = tok(j), f = feat(i, g);
-      if (t < T && f < N) {
-        f32x4 v;
-        v.x = acc[i][j][4 * g + 0];
-        v.y = acc[i][j][4 * g + 1];
-        v.z = acc[i][j][4 * g + 2];
-        v.w = acc[i][j][4 * g + 3];
-        if constexpr (EpiSumSq<Epi>::value)
-          lane_sq += AX::apply(epi, t, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
-        else
-          AX::apply(epi, t, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
-      }
-    });
+    if constexpr (ROWS) {
+      static_for<0, TM>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const auto rc = epi.row(tkj[j], fblk(i));
+        static_for<0, 4>([&](auto gc) {
+          constexpr int g = decltype(gc)::value, q = 4 * j + g;
+          const int t = tok(j), f = feat(i, g);
+          if (t < T && f < N) {
+            f32x4 v;
+            v.x = acc[i][j][4 * g + 0];
+            v.y = acc[i][j][4 * g + 1];
+            v.z = acc[i][j][4 * g + 2];
+            v.w = acc[i][j][4 * g + 3];
+            epi.store_row(rc, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
+          }
+        });
+      });
+    } else {
+      static_for<0, TM * 4>([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        constexpr int j = q / 4, g = q % 4;
+        const int t = tok(j), f = feat(i, g);
+        if (t < T && f < N) {
+          f32x4 v;
+          v.x = acc[i][j][4 * g + 0];
+          v.y = acc[i][j][4 * g + 1];
+          v.z = acc[i][j][4 * g + 2];
+          v.w = acc[i][j][4 * g + 3];
+          if constexpr (EpiSumSq<Epi>::value)
+            lane_sq += AX::apply(epi, t, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
+          else
+            AX::apply(epi, t, f, v, aux[HOIST ? i : (i & 1)][q], fblk(i));
+        }
+      });
+    }
   });
   if constexpr (EpiSumSq<Epi>::value) {
     // The main loop ended on a barrier after its last LDS reads, so the

@@ -226,6 +226,35 @@ def test_sdpa_op_on_staged_rope_tiles_spanning_sequences(gpu):
     k.ctx.close()
 
 
+@pytest.mark.parametrize("B,S", [(3, 700), (1, 512), (2, 100)])
+def test_sdpa_plain_stores_equal_tapped(gpu, B, S):
+    """The QKV GEMM's plain epilogue (no tap: Q, K and V^T addressed per
+    token and per 32-feature block) and its tapped one (the fp32 tap too,
+    addressed per quad) must write the same fp16 Q, K and V^T: the attention
+    output is compared bit for bit, on several tile shapes (256x256 staged
+    tiles at 3 x 700 tokens, smaller ones below)."""
+    import torch
+    cfg = tiny_config(dim=2048, hidden=256, heads=16, hd=128, nlayers=1, seq=S, vocab=256)
+    k = CompiledKernels.compile(cfg)
+    k.ctx.set_stream(gpu.stream())
+    w = ModelWeights.synthetic(cfg, seed=78, std=0.02)
+    k.ensure_weights(w)
+    xn = f16_round(np.random.default_rng(12).standard_normal((B * S, cfg.dim)) * 0.5)
+    dxn = to_dev(xn, torch.float16)
+    plain = torch.empty((B * S, cfg.q_dim), dtype=torch.float16, device="cuda")
+    tapped = torch.empty_like(plain)
+    tap = torch.empty((B * S, cfg.q_dim + 2 * cfg.kv_dim), device="cuda")
+    print(f"sdpa plain vs tapped: B={B} S={S}", flush=True)
+    hb.call("hb_op_sdpa_fwd", k.model.handle, 0, dxn.data_ptr(), B, S, plain.data_ptr(), None)
+    hb.call("hb_op_sdpa_fwd", k.model.handle, 0, dxn.data_ptr(), B, S, tapped.data_ptr(), tap.data_ptr())
+    torch.cuda.synchronize()
+    a, b = plain.cpu().numpy(), tapped.cpu().numpy()
+    assert np.isfinite(a.astype(F32)).all()
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), np.abs(a.astype(F32) - b.astype(F32)).max()
+    k.model.close()
+    k.ctx.close()
+
+
 def test_logits_ce_op_matches_oracle(tiny):
     import torch
     cfg, k, w = tiny
