@@ -157,11 +157,11 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, -1, 0x00020000);
   const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, -1, 0x00020000);
   constexpr int kSC1 = 16;  // cache policy: sc1
-  int woff[WL], xoff[XL];
+  uint32_t wvo[WL], xvo[XL];  // byte offsets of this thread's 16-byte chunks at column 0
 #pragma unroll
-  for (int i = 0; i < WL; ++i) woff[i] = min(f_base + r0 + RSTEP * i, N - 1) * kw;
+  for (int i = 0; i < WL; ++i) wvo[i] = (uint32_t)(c0 * 8 + min(f_base + r0 + RSTEP * i, N - 1) * kw) * 2u;
 #pragma unroll
-  for (int i = 0; i < XL; ++i) xoff[i] = min(t_base + r0 + RSTEP * i, T - 1) * K;
+  for (int i = 0; i < XL; ++i) xvo[i] = (uint32_t)(c0 * 8 + min(t_base + r0 + RSTEP * i, T - 1) * K) * 2u;
 
   using R0 = std::integral_constant<int, 0>;
   using R1 = std::integral_constant<int, 1>;
@@ -169,14 +169,15 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   auto gload = [&](auto rs, int k0) {
     constexpr int R = decltype(rs)::value;
     const int kw0 = k0 < kw ? k0 : k0 - kw;  // wave-uniform
+    // per-lane row offsets in voffset, the slice's column in soffset
 #pragma unroll
     for (int i = 0; i < WL; ++i)
       wreg[R][i] = __builtin_bit_cast(
-          f16x8, __builtin_amdgcn_raw_buffer_load_b128(wrs, (uint32_t)(c0 * 8 + woff[i] + kw0) * 2u, 0, kSC1));
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[i], kw0 * 2, kSC1));
 #pragma unroll
     for (int i = 0; i < XL; ++i)
       xreg[R][i] = __builtin_bit_cast(
-          f16x8, __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)(c0 * 8 + xoff[i] + k0) * 2u, 0, kSC1));
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo[i], k0 * 2, kSC1));
   };
   auto sstore = [&](auto rs) {
     constexpr int R = decltype(rs)::value;
