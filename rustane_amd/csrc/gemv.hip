@@ -185,8 +185,8 @@ HB_DEV void stage_attn(const AttnIn& ai, int B, int K, f16* s_x) {
 }
 
 // Greedy-decode argmax partials of the logits epilogue: the first index of
-// the maximum of each sequence's 16 logits of this row block, with the
-// cross-entropy kernel's rules (NaN never wins, ties go to the lower index).
+// the maximum of each sequence's 16 logits of this row block (NaN never
+// wins, ties go to the lower index).
 HB_DEV void argmax_partial(const EpiLogits& e, f32x4 v, int f0, int col, int B, int rb, int nrb) {
   const f32x4 y = e.capped(v);
   float best = -INFINITY;
