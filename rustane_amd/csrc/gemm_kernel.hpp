@@ -324,7 +324,12 @@ __global__ __launch_bounds__(WF* WT * 64, 1) void gemm_nt_kernel(const f16* __re
   constexpr bool ROWS = EpiRows<Epi>::value;
   static_assert(!ROWS || !EpiSumSq<Epi>::value, "row-addressed epilogues return nothing");
   typename EpiRows<Epi>::Tok tkj[ROWS ? TM : 1];
-  if constexpr (ROWS) static_for<0, TM>([&](auto jc) { tkj[decltype(jc)::value] = epi.tok(tok(decltype(jc)::value)); });
+  if constexpr (ROWS) {
+    static_for<0, TM>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      tkj[j] = epi.tok(tok(j));
+    });
+  }
   float lane_sq = 0.f;
   static_for<0, FM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
