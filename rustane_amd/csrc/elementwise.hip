@@ -43,7 +43,10 @@ hipError_t embedding(const f16* E, const uint32_t* tok, int T, int dim, int voca
 // issued before any use and the row stays in registers for the second pass.
 // NPT = 0: any dim (multiple of 4), strided loop. Both add each thread's
 // squares in the same order, so the result does not depend on the variant.
-template <int NPT>
+// NPT > 0: dim = NPT * 1024 held in registers; RAG: dim <= NPT * 1024 (dim % 4
+// == 0), the chunks past dim skipped (they add 0 to the sum of squares, which
+// leaves it unchanged, so the result equals the two-pass NPT = 0 form's).
+template <int NPT, bool RAG = false>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, long row_stride,
                                                       const float* __restrict__ gamma, int dim,
                                                       float eps, f16* __restrict__ out,
@@ -55,11 +58,12 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const size_t lo = split ? (size_t)dim : 0;  // split rows: [hi | lo]
   float ss = 0.f;
   if constexpr (NPT > 0) {
+    auto in = [&](int i) { return !RAG || (int)threadIdx.x * 4 + i * 1024 < dim; };
     f32x4 v[NPT], g[NPT];
 #pragma unroll
-    for (int i = 0; i < NPT; ++i) v[i] = *(const f32x4*)(xr + threadIdx.x * 4 + i * 1024);
+    for (int i = 0; i < NPT; ++i) v[i] = in(i) ? *(const f32x4*)(xr + threadIdx.x * 4 + i * 1024) : f32x4{};
 #pragma unroll
-    for (int i = 0; i < NPT; ++i) g[i] = *(const f32x4*)(gamma + threadIdx.x * 4 + i * 1024);
+    for (int i = 0; i < NPT; ++i) g[i] = in(i) ? *(const f32x4*)(gamma + threadIdx.x * 4 + i * 1024) : f32x4{};
 #pragma unroll
     for (int i = 0; i < NPT; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
     ss = block_sum<4>(ss, red);
@@ -67,6 +71,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     if (rms_inv && threadIdx.x == 0) rms_inv[t] = r;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
+      if (!in(i)) continue;
       f32x4 o;
       o.x = v[i].x * r * g[i].x;
       o.y = v[i].y * r * g[i].y;
@@ -107,13 +112,18 @@ hipError_t rmsnorm(const float* x, long row_stride, const float* gamma, int T, i
   if (T <= 0) return hipSuccess;
   if (frag && (split || T > 16 || dim % 32)) return hipErrorInvalidValue;
   const int sp = frag ? 2 : split ? 1 : 0;
-  switch (dim % 1024 == 0 ? dim / 1024 : 0) {
-#define HB_NORM(n)                                                                              \
-  case n:                                                                                       \
-    hipLaunchKernelGGL(rmsnorm_kernel<n>, dim3(T), dim3(256), 0, st, x, row_stride, gamma, dim, \
-                       eps, out, rms_inv, sp);                                                  \
+  // 1..8: whole multiples of 1024; 9..16: ragged, ceil(dim / 1024) = 1..8
+  const int np = dim % 1024 == 0 ? dim / 1024 : dim % 4 == 0 && dim < 8192 ? 8 + dim / 1024 + 1 : 0;
+  switch (np) {
+#define HB_NORM(n, c, rag)                                                                      \
+  case c:                                                                                       \
+    hipLaunchKernelGGL((rmsnorm_kernel<n, rag>), dim3(T), dim3(256), 0, st, x, row_stride, gamma, \
+                       dim, eps, out, rms_inv, sp);                                             \
     break;
-    HB_NORM(1) HB_NORM(2) HB_NORM(3) HB_NORM(4) HB_NORM(5) HB_NORM(6) HB_NORM(7) HB_NORM(8)
+    HB_NORM(1, 1, false) HB_NORM(2, 2, false) HB_NORM(3, 3, false) HB_NORM(4, 4, false)
+    HB_NORM(5, 5, false) HB_NORM(6, 6, false) HB_NORM(7, 7, false) HB_NORM(8, 8, false)
+    HB_NORM(1, 9, true) HB_NORM(2, 10, true) HB_NORM(3, 11, true) HB_NORM(4, 12, true)
+    HB_NORM(5, 13, true) HB_NORM(6, 14, true) HB_NORM(7, 15, true) HB_NORM(8, 16, true)
 #undef HB_NORM
     default:
       hipLaunchKernelGGL(rmsnorm_kernel<0>, dim3(T), dim3(256), 0, st, x, row_stride, gamma, dim,

@@ -9,7 +9,7 @@ namespace hb {
 // splits in order, applies the residual epilogue (out = res + alpha * v), and
 // normalises the row into xn. The element-to-thread mapping and the block sum
 // are those of rmsnorm_kernel, so xn is bit-identical to reduce + rmsnorm.
-template <int NPT>  // as rmsnorm_kernel: N = NPT * 1024 held in registers, or 0 = any N
+template <int NPT, bool RAG = false>  // as rmsnorm_kernel: N = NPT * 1024 (RAG: N <= NPT * 1024) in registers, or 0 = any N
 __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __restrict__ P, int S,
                                                                  int N, size_t stride,
                                                                  EpiResidual e, NormOut no) {
@@ -21,11 +21,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
   const size_t lo = no.split ? (size_t)N : 0;  // split xn rows: [hi | lo]
   float ss = 0.f;
   if constexpr (NPT > 0) {
+    auto in = [&](int i) { return !RAG || (int)threadIdx.x * 4 + i * 1024 < N; };
     f32x4 y[NPT], g[NPT];
     {
       f32x4 part[NPT][MAXS], r[NPT];
 #pragma unroll
       for (int i = 0; i < NPT; ++i) {
+        if (!in(i)) continue;
         const size_t c = row + threadIdx.x * 4 + i * 1024;
 #pragma unroll
         for (int s = 0; s < MAXS; ++s)
@@ -33,9 +35,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
         r[i] = *(const f32x4*)(e.res + c);
       }
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) g[i] = *(const f32x4*)(no.gamma + threadIdx.x * 4 + i * 1024);
+      for (int i = 0; i < NPT; ++i) g[i] = in(i) ? *(const f32x4*)(no.gamma + threadIdx.x * 4 + i * 1024) : f32x4{};
 #pragma unroll
       for (int i = 0; i < NPT; ++i) {
+        if (!in(i)) {  // past N: adds 0 to the sum of squares
+          y[i] = f32x4{};
+          continue;
+        }
         f32x4 v = part[i][0];
 #pragma unroll
         for (int s = 1; s < MAXS; ++s)
@@ -52,6 +58,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm_kernel(const float* __
     const float rinv = 1.0f / sqrtf(ss * (1.0f / (float)N) + no.eps);
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
+      if (!in(i)) continue;
       f32x4 o;
       o.x = y[i].x * rinv * g[i].x;
       o.y = y[i].y * rinv * g[i].y;
@@ -143,13 +150,17 @@ hipError_t gemm_residual_norm(const f16* W, const f16* X, int N, int T, int K, c
              : launch_tile<128, 128, 2, 2>(W, X, N, T, K, EpiSplit{scr->p, N, stride}, st, S, {}, kw);
     if (err != hipSuccess) return err;
     if (mid && (err2 = hipEventRecord(mid, st)) != hipSuccess) return err2;
-    switch (N % 1024 == 0 ? N / 1024 : 0) {
-#define HB_RN(n)                                                                                \
-  case n:                                                                                       \
-    hipLaunchKernelGGL(splitk_reduce_norm_kernel<n>, dim3(T), dim3(256), 0, st, scr->p, S, N,   \
-                       stride, e, no);                                                          \
+    // 1..8: whole multiples of 1024; 9..16: ragged, ceil(N / 1024) = 1..8
+    switch (N % 1024 == 0 ? N / 1024 : N % 4 == 0 && N < 8192 ? 8 + N / 1024 + 1 : 0) {
+#define HB_RN(n, c, rag)                                                                        \
+  case c:                                                                                       \
+    hipLaunchKernelGGL((splitk_reduce_norm_kernel<n, rag>), dim3(T), dim3(256), 0, st, scr->p, S, \
+                       N, stride, e, no);                                                       \
     break;
-      HB_RN(1) HB_RN(2) HB_RN(3) HB_RN(4) HB_RN(5) HB_RN(6) HB_RN(7) HB_RN(8)
+      HB_RN(1, 1, false) HB_RN(2, 2, false) HB_RN(3, 3, false) HB_RN(4, 4, false)
+      HB_RN(5, 5, false) HB_RN(6, 6, false) HB_RN(7, 7, false) HB_RN(8, 8, false)
+      HB_RN(1, 9, true) HB_RN(2, 10, true) HB_RN(3, 11, true) HB_RN(4, 12, true)
+      HB_RN(5, 13, true) HB_RN(6, 14, true) HB_RN(7, 15, true) HB_RN(8, 16, true)
 #undef HB_RN
       default:
         hipLaunchKernelGGL(splitk_reduce_norm_kernel<0>, dim3(T), dim3(256), 0, st, scr->p, S, N,

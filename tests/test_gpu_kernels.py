@@ -67,9 +67,13 @@ def test_gemm_nt_mfma_layout_one_hot(gpu):
     np.testing.assert_array_equal(dc.cpu().numpy(), expect)
 
 
-def test_rmsnorm_op_matches_oracle(gpu):
+@pytest.mark.parametrize("dim", [512, 1536, 2560, 4096, 4100, 9000])
+def test_rmsnorm_op_matches_oracle(gpu, dim):
+    """Rows held in registers (dim a multiple of 1024, or up to 8 chunks of
+    1024 with the last one partial: the 600M and 5B widths) and the two-pass
+    form for wider rows."""
     import torch
-    T, dim = 37, 512
+    T = 37
     rng = np.random.default_rng(1)
     x = (rng.standard_normal((T, dim)) * 3).astype(F32)
     g = (1 + 0.1 * rng.standard_normal(dim)).astype(F32)
@@ -80,7 +84,13 @@ def test_rmsnorm_op_matches_oracle(gpu):
             out.data_ptr(), rinv.data_ptr())
     torch.cuda.synchronize()
     ref, ref_r = O.rmsnorm_channel_first(x.T.reshape(-1), g, dim, T)
-    np.testing.assert_allclose(rinv.cpu().numpy(), ref_r, rtol=2e-6)
+    got_r = rinv.cpu().numpy()
+    # the kernel's fp32 sum of squares (per-thread chunks, then a block tree)
+    # stays within 2e-6 of float64; the oracle's sequential fp32 sum drifts
+    # with the row length (about 2e-6 of rms_inv at 9000)
+    r64 = 1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1) + 1e-5)
+    np.testing.assert_allclose(got_r, r64, rtol=2e-6)
+    np.testing.assert_allclose(got_r, ref_r, rtol=2e-6 if dim <= 4100 else 1e-5)
     np.testing.assert_allclose(out.float().cpu().numpy(), ref.reshape(dim, T).T, rtol=1e-3, atol=1e-3)
 
 
