@@ -319,6 +319,39 @@ def test_cross_entropy_wide_vocab_matches_oracle(gpu, vocab):
     k.ctx.close()
 
 
+def test_cross_entropy_out_of_range_target_is_nan_and_reported(gpu):
+    """A target id >= vocab reaching the device: its row's loss is NaN, the
+    other rows are unchanged, and the next synchronisation reports the target
+    (error word bit 2) and clears it."""
+    import torch
+    cfg = tiny_config(dim=64, hidden=64, heads=1, nlayers=1, vocab=320)
+    k = CompiledKernels.compile(cfg)
+    k.ctx.set_stream(gpu.stream())
+    k.ensure_weights(ModelWeights.synthetic(cfg, seed=5, std=0.02))
+    T = 6
+    rng = np.random.default_rng(4)
+    xf = f16_round(rng.standard_normal((T, cfg.dim)))
+    tgt = rng.integers(0, cfg.vocab, T).astype(np.uint32)
+    tgt[2] = cfg.vocab
+    tgt[4] = 0xFFFFFFFF
+    dl = torch.empty((T, cfg.vocab), device="cuda")
+    dloss = torch.empty(T, device="cuda")
+    dxf, dtgt = to_dev(xf, torch.float16), to_dev(tgt)
+    hb.call("hb_op_logits_ce", k.model.handle, dxf.data_ptr(), dtgt.data_ptr(), T, dl.data_ptr(),
+            dloss.data_ptr())
+    with pytest.raises(hb.HipBridgeError) as e:
+        k.ctx.synchronize()
+    assert e.value.code == hb.HB_E_INVALID and "target" in str(e.value)
+    k.ctx.synchronize()  # the error word was cleared
+    got = dloss.cpu().numpy()
+    assert np.isnan(got[[2, 4]]).all()
+    ok = [0, 1, 3, 5]
+    _, ref = O.cross_entropy_batch(dl.cpu().numpy()[ok], tgt[ok], cfg.vocab)
+    np.testing.assert_allclose(got[ok], ref, rtol=1e-5, atol=1e-5)
+    k.model.close()
+    k.ctx.close()
+
+
 @pytest.mark.parametrize("T", [128, 200])
 def test_residual_gemm_split_k_matches_float64(gpu, T):
     """Wo of a 2048-wide model at <= 256 tokens has few output tiles and a long
